@@ -1,0 +1,271 @@
+"""MLA decode / prefill benchmark on one MI355X.
+
+Headline workload (one "step"): one decode token through a 61-layer MLA-only
+stack (input RMSNorm -> MLA -> residual per layer, distinct seeded block-FP8
+weights per layer, ~11.4 GB) at batch 8, context 32768 (position 32767, bf16
+latent + rope cache of 32768 rows per sequence and layer), replayed as one
+HIP graph.  value = microseconds per layer.
+
+Also reported in the same line: decode at batch 1 / context 4096 over the same
+61-layer weights, and one-layer prefill of 4096 tokens (TFLOP/s), plus the
+roofline of the dominant decode kernel (attention over the latent cache, timed
+with HIP events on its launch stream) and the CPU oracle on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "deepseek-on-one-gpu_amd")]
+
+import torch  # noqa: E402
+
+from amla import ops, synth  # noqa: E402
+from amla._lib import MlaArgs, check, lib  # noqa: E402
+from amla.config import DeepSeekConfig  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+CFG = DeepSeekConfig()
+WEIGHT_BYTES = sum(n * k for n, k in synth.projection_shapes(CFG).values())              # 187,105,280
+SCALE_BYTES = sum(4 * -(-n // 128) * -(-k // 128) for n, k in synth.projection_shapes(CFG).values())
+GAMMA_BYTES = 2 * (CFG.q_lora_rank + CFG.kv_lora_rank)
+ROW_BYTES = 2 * (CFG.kv_lora_rank + CFG.qk_rope_head_dim)                                 # 1152
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def decode_layer_bytes(B, T):
+    """Algorithmic HBM bytes of one decode layer: weights + scales + gammas +
+    every cached row + the new row + hidden in/out (bf16)."""
+    return WEIGHT_BYTES + SCALE_BYTES + GAMMA_BYTES + B * T * ROW_BYTES + B * ROW_BYTES + B * CFG.hidden_size * 4
+
+
+def decode_layer_flops(B, T):
+    proj = 2 * sum(n * k for name, (n, k) in synth.projection_shapes(CFG).items() if name != "kv_b_proj")
+    absorb = 2 * 2 * 128 * 128 * 512
+    return B * (proj + absorb) + B * T * 2 * 128 * (576 + 512)
+
+
+def prefill_flops(S):
+    lin = 2 * S * WEIGHT_BYTES
+    attn = 2 * 128 * (S * (S + 1) // 2) * (192 + 128)
+    return lin + attn
+
+
+# ------------------------------------------------------------------ data
+
+def make_stack(layers, B, T, dev, tag="bench"):
+    log(f"[bench] generating {layers} layers of block-FP8 weights on {dev}")
+    stack = []
+    for L in range(layers):
+        lay = synth.make_layer(CFG, tag, L, device=dev)
+        stack.append(lay)
+    return stack
+
+
+def make_caches(layers, B, T, dev, tag="bench"):
+    caches = []
+    for L in range(layers):
+        ckv = synth.randn((B, T, CFG.kv_lora_rank), synth.seed_of(tag, L, "ckv", B, T), 1.0, dev).to(torch.bfloat16)
+        kpe = synth.randn((B, T, CFG.qk_rope_head_dim), synth.seed_of(tag, L, "kpe", B, T), 1.0, dev).to(torch.bfloat16)
+        caches.append((ckv, kpe))
+    return caches
+
+
+def run_stack(stack, caches, hidden, pos, rope, ctx):
+    h = hidden
+    for lay, cache in zip(stack, caches):
+        h = ops.mla_layer(h, lay.input_layernorm, lay.attn_weights, cache, pos, rope, CFG, max_context=ctx)
+    return h
+
+
+def time_graph(fn, steps, warmup):
+    fn()                      # eager: sizes the workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps, out
+
+
+def decode_stage_times(stack, caches, hidden, pos, rope, ctx, reps=2):
+    """Per-stage mean ms of amla_mla_decode over every layer (eager, events on the launch stream)."""
+    dev = hidden.device
+    st = torch.cuda.current_stream(dev)
+    nev = 8
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(nev)] for _ in range(len(stack) * reps)]
+    out = torch.empty_like(hidden)
+    k = 0
+    for _ in range(reps):
+        for lay, cache in zip(stack, caches):
+            a, _p = ops._fill_args(hidden, lay.attn_weights, cache, pos, rope, CFG, out=out,
+                                   input_gamma=lay.input_layernorm, residual=hidden, max_context=ctx)
+            ws = ops.workspace(dev, lib().amla_mla_decode_workspace_bytes(a))
+            a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+            arr = (ctypes.c_void_p * nev)(*[e.cuda_event for e in evs[k]])
+            check(lib().amla_mla_decode_profiled(a, st.cuda_stream, arr), "mla_decode_profiled")
+            k += 1
+    torch.cuda.synchronize()
+    names = ["qkva", "q_norm", "q_b_rope", "absorb", "attention", "combine_uv", "o_proj"]
+    tot = {n: 0.0 for n in names}
+    for ev in evs:
+        for i, n in enumerate(names):
+            tot[n] += ev[i].elapsed_time(ev[i + 1])
+    return {n: v / len(evs) for n, v in tot.items()}
+
+
+# ------------------------------------------------------------------ CPU baseline
+
+def cpu_baseline(T, B):
+    """The oracle (torch-CPU restatement of the reference) on the host cores:
+    one layer x one sequence at the full context, scaled x B sequences."""
+    from oracle import ref_ops as R
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    lay = synth.make_layer(CFG, "cpu")
+    ckv, kpe = synth.make_kv_cache(CFG, 1, T, T - 1, "cpu")
+    h = synth.make_hidden(CFG, 1, 1, "cpu")
+    tab = R.precompute_rope_freqs(CFG, T)
+    t0 = time.perf_counter()
+    R.mla_attention(h, lay.attn_weights, (ckv, kpe), T - 1, tab, CFG)
+    dt = time.perf_counter() - t0
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(dt * B * 1e6, 1), "unit": "us/layer", "cores": cores, "kind": "port",
+            "sample": f"oracle mla_attention, 1 layer x 1 sequence at context {T} measured ({dt:.2f} s), "
+                      f"x{B} sequences (extrapolated); host {cpu_model}"}
+
+
+# ------------------------------------------------------------------ main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=61)
+    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--context", type=int, default=32768)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU sharding is a design "
+                                   "note only (--gpus must be 1)"}))
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    B, T, NL = args.batch, args.context, args.layers
+
+    stack = make_stack(NL, B, T, dev)
+    caches = make_caches(NL, B, T, dev)
+    rope = ops.precompute_rope_freqs(CFG, T, dev)
+    pos = torch.full((B,), T - 1, dtype=torch.int32, device=dev)
+    hidden = synth.randn((B, 1, CFG.hidden_size), synth.seed_of("bench", "hidden"), 1.0, dev).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    log("[bench] decode stack ready; capturing graph")
+    ms, _ = time_graph(lambda: run_stack(stack, caches, hidden, pos, rope, T), args.steps, args.warmup)
+    us_layer = ms * 1000 / NL
+    bytes_layer = decode_layer_bytes(B, T)
+    gbs = bytes_layer / (us_layer * 1e-6) / 1e9
+    log(f"[bench] decode B={B} T={T}: {us_layer:.1f} us/layer, {gbs:.0f} GB/s")
+
+    stages = decode_stage_times(stack, caches, hidden, pos, rope, T)
+    attn_bytes = B * T * ROW_BYTES
+    attn_ms = stages["attention"]
+    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+    log(f"[bench] stage ms: {json.dumps({k: round(v, 4) for k, v in stages.items()})}")
+    del caches
+    torch.cuda.empty_cache()
+
+    extras = {}
+    if not args.no_extras:
+        # decode B=1, ctx 4096 over the same 61 layers (MALL-proof: 11.4 GB of weights per step)
+        c4 = make_caches(NL, 1, 4096, dev, tag="bench4k")
+        rope4 = ops.precompute_rope_freqs(CFG, 4096, dev)
+        pos4 = torch.full((1,), 4095, dtype=torch.int32, device=dev)
+        h4 = hidden[:1].contiguous()
+        ms4, _ = time_graph(lambda: run_stack(stack, c4, h4, pos4, rope4, 4096), args.steps, args.warmup)
+        us4 = ms4 * 1000 / NL
+        extras["decode_ctx4096_b1_us_per_layer"] = round(us4, 2)
+        extras["decode_ctx4096_b1_hbm_gbs"] = round(decode_layer_bytes(1, 4096) / (us4 * 1e-6) / 1e9, 1)
+        del c4
+        # prefill 4096 tokens, one layer (rotating over 4 layers' weights)
+        S = 4096
+        hp = synth.randn((1, S, CFG.hidden_size), synth.seed_of("bench", "prefill"), 1.0, dev).to(torch.bfloat16)
+        cp = (torch.zeros(1, S, 512, dtype=torch.bfloat16, device=dev), torch.zeros(1, S, 64, dtype=torch.bfloat16, device=dev))
+        ropep = ops.precompute_rope_freqs(CFG, S, dev)
+        for i in range(2):
+            ops.mla_attention(hp, stack[i].attn_weights, cp, 0, ropep, CFG)
+        torch.cuda.synchronize()
+        reps = 8
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(reps):
+            ops.mla_attention(hp, stack[i % 4].attn_weights, cp, 0, ropep, CFG)
+        e.record()
+        torch.cuda.synchronize()
+        pms = s.elapsed_time(e) / reps
+        extras["prefill_4096_ms"] = round(pms, 3)
+        extras["prefill_4096_tflops"] = round(prefill_flops(S) / (pms * 1e-3) / 1e12, 1)
+        extras["prefill_frac_bf16_peak"] = round(extras["prefill_4096_tflops"] / BF16_PEAK_TFLOPS, 4)
+        log(f"[bench] extras: {extras}")
+
+    result = {
+        "metric": "MLA decode µs/layer + HBM GB/s at ctx 4k/32k; prefill TFLOP/s (4k tokens)",
+        "value": round(us_layer, 2),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights quantised to e4m3fn 128x128 blocks; N(0,1) bf16 cache and hidden)",
+        "config": {"workload": f"decode, {NL}-layer MLA-only stack (input RMSNorm + MLA + residual), batch {B}, "
+                               f"context {T} (position {T - 1}), one HIP graph per step",
+                   "batch": B, "context": T, "layers": NL},
+        "hbm_gbs": round(gbs, 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "decode_stage_ms": {k: round(v, 4) for k, v in stages.items()},
+        "roofline": {"kernel": "attn_kernel (latent-cache attention, split over context)", "bound": "hbm",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": attn_bytes, "avg_ms": round(attn_ms, 4)},
+        **extras,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (oracle) ...")
+        result["cpu_baseline"] = cpu_baseline(T, B)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

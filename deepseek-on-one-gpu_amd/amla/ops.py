@@ -1,0 +1,311 @@
+"""MLA-path operators with the reference's signatures, on gfx950 HIP kernels.
+
+Drop-in for the MLA half of inference/ops.py: ``rms_norm`` (:10-12),
+``fp8_linear`` (:15-44), ``yarn_get_mscale`` (:47-50), ``precompute_rope_freqs``
+(:53-83), ``apply_rope`` (:86-97) and ``mla_attention`` (:100-183), plus the
+attention half of ``transformer_layer`` (inference/forward.py:92-94) as
+``mla_layer``.  Same argument names, tensor layouts and dtypes; tensors must be
+on a ROCm device.  Every compute call goes to libamla.so; there is no CPU or
+PyTorch fallback (a missing library raises).
+
+Superset over the reference: ``position`` of ``mla_attention`` may also be a
+list of per-sequence start positions or an int32 device tensor of them (the
+reference's scalar position cannot express a ragged batch).
+"""
+from __future__ import annotations
+
+import math
+from typing import Sequence
+
+import torch
+
+from . import _lib
+from ._lib import MlaArgs, check, lib
+
+BF16 = torch.bfloat16
+FP8 = torch.float8_e4m3fn
+
+
+def _stream_ptr(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need_cuda(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        raise ValueError(f"{name} must be a tensor on a ROCm device")
+
+
+def _need(t: torch.Tensor, name: str, dtype, dev=None) -> None:
+    _need_cuda(t, name)
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+    if dev is not None and t.device != dev:
+        raise ValueError(f"{name} is on {t.device}, expected {dev}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+# ------------------------------------------------------------------ workspace
+
+_workspaces: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device zero-initialised scratch, grown on demand.
+
+    Kernels that use split-K counters leave them at zero, so the buffer is
+    reusable across calls on one stream.  Size it (one eager call) before a
+    HIP graph capture so that no allocation happens while capturing.
+    """
+    key = (device.type, device.index)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = buf
+    return buf
+
+
+# ------------------------------------------------------------------ elementwise / linear
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """inference/ops.py:10-12: y = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * weight)."""
+    _need_cuda(x, "x")
+    if x.dtype != BF16 or weight.dtype != BF16:
+        raise TypeError("rms_norm: x and weight must be bfloat16")
+    dim = x.shape[-1]
+    if weight.shape != (dim,):
+        raise ValueError(f"rms_norm: weight shape {tuple(weight.shape)} != ({dim},)")
+    xc = x.contiguous()
+    w = weight.contiguous()
+    y = torch.empty_like(xc)
+    rows = xc.numel() // dim if dim else 0
+    check(lib().amla_rms_norm(xc.data_ptr(), rows, dim, dim, w.data_ptr(), float(eps), y.data_ptr(), dim,
+                              _stream_ptr(xc)), "rms_norm")
+    return y
+
+
+def fp8_block_dequant(weight: torch.Tensor, scale_inv: torch.Tensor) -> torch.Tensor:
+    """inference/ops.py:30-43: fp32 f32(weight) * scale_inv[i//128, j//128], bit-exact."""
+    _need(weight, "weight", FP8)
+    _need(scale_inv, "scale_inv", torch.float32, weight.device)
+    n, k = weight.shape
+    if scale_inv.shape != (math.ceil(n / 128), math.ceil(k / 128)):
+        raise ValueError(f"scale_inv shape {tuple(scale_inv.shape)} does not match weight {n}x{k}")
+    out = torch.empty(n, k, dtype=torch.float32, device=weight.device)
+    check(lib().amla_fp8_block_dequant(weight.data_ptr(), scale_inv.data_ptr(), n, k, out.data_ptr(),
+                                       _stream_ptr(weight)), "fp8_block_dequant")
+    return out
+
+
+def fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Tensor,
+               out_dtype: torch.dtype = BF16) -> torch.Tensor:
+    """inference/ops.py:15-44: bf16( x @ dequant(weight, scale_inv).T ), fp32 accumulation."""
+    _need_cuda(x, "x")
+    if x.dtype != BF16:
+        raise TypeError(f"fp8_linear: x must be bfloat16 (got {x.dtype})")
+    if out_dtype != BF16:
+        raise TypeError("fp8_linear: only out_dtype=torch.bfloat16 is implemented")
+    _need(weight, "weight", FP8, x.device)
+    _need(scale_inv, "scale_inv", torch.float32, x.device)
+    n, k = weight.shape
+    if x.shape[-1] != k:
+        raise ValueError(f"fp8_linear: x has {x.shape[-1]} features, weight expects {k}")
+    if scale_inv.shape != (math.ceil(n / 128), math.ceil(k / 128)):
+        raise ValueError(f"scale_inv shape {tuple(scale_inv.shape)} does not match weight {n}x{k}")
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    y = torch.empty(m, n, dtype=BF16, device=x.device)
+    if m:
+        need = lib().amla_fp8_linear_workspace_bytes(m, n, k)
+        ws = workspace(x.device, need) if need else None
+        check(lib().amla_fp8_linear(x2.data_ptr(), m, k, x2.stride(0), weight.data_ptr(), scale_inv.data_ptr(),
+                                    n, y.data_ptr(), n, ws.data_ptr() if ws is not None else None,
+                                    ws.numel() if ws is not None else 0, _stream_ptr(x)), "fp8_linear")
+    return y.view(*x.shape[:-1], n)
+
+
+# ------------------------------------------------------------------ RoPE
+
+def yarn_get_mscale(scale: float = 1.0, mscale: float = 1.0) -> float:
+    """inference/ops.py:47-50 (host scalar)."""
+    if scale <= 1.0:
+        return 1.0
+    return 0.1 * mscale * math.log(scale) + 1.0
+
+
+def precompute_rope_freqs(config, seq_len: int, device) -> torch.Tensor:
+    """inference/ops.py:53-83: YaRN-blended frequencies, complex64 (seq_len, rope/2).
+
+    One-time table set-up (the engine builds it once, inference/engine.py:63):
+    computed with fp32 torch ops in the same order as the reference, so the
+    table is bit-identical, then moved to ``device``.
+    """
+    dim = config.qk_rope_head_dim
+    base = config.rope_theta
+    inv = 1.0 / (base ** (torch.arange(0, dim, 2, dtype=torch.float32) / dim))
+
+    def edge(beta):
+        return dim * math.log(config.original_max_position_embeddings / (beta * 2 * math.pi)) / (2 * math.log(base))
+
+    low = max(math.floor(edge(config.rope_scaling_beta_fast)), 0)
+    high = min(math.ceil(edge(config.rope_scaling_beta_slow)), dim // 2 - 1)
+    ramp = torch.ones(dim // 2, dtype=torch.float32)
+    if high > low:
+        ramp = ((torch.arange(dim // 2, dtype=torch.float32) - low) / (high - low)).clamp(0.0, 1.0)
+    inv = inv * (1.0 - ramp) + (inv / config.rope_scaling_factor) * ramp
+    ang = torch.outer(torch.arange(seq_len, dtype=torch.float32), inv)
+    return torch.polar(torch.ones_like(ang), ang).to(device)
+
+
+def apply_rope(x: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
+    """inference/ops.py:86-97: x (B, H, S, rope) bf16, freqs (S, rope/2) complex64."""
+    _need_cuda(x, "x")
+    if x.dtype != BF16:
+        raise TypeError("apply_rope: x must be bfloat16")
+    if freqs.dtype != torch.complex64 or freqs.device != x.device:
+        raise TypeError("apply_rope: freqs must be complex64 on the same device")
+    S, dim = x.shape[-2], x.shape[-1]
+    if freqs.shape != (S, dim // 2):
+        raise ValueError(f"apply_rope: freqs shape {tuple(freqs.shape)} != ({S}, {dim // 2})")
+    xc = x.contiguous()
+    f = torch.view_as_real(freqs.contiguous())
+    y = torch.empty_like(xc)
+    groups = xc.numel() // (S * dim) if S * dim else 0
+    check(lib().amla_apply_rope(xc.data_ptr(), groups, S, dim, f.data_ptr(), y.data_ptr(), _stream_ptr(xc)),
+          "apply_rope")
+    return y
+
+
+# ------------------------------------------------------------------ MLA
+
+def softmax_scale(config) -> float:
+    """mscale / sqrt(qk_head_dim), mscale applied once (inference/ops.py:166-167)."""
+    return yarn_get_mscale(config.rope_scaling_factor, config.rope_scaling_mscale_all_dim) / math.sqrt(
+        config.qk_head_dim)
+
+
+def _positions(position, B: int, S: int, device, max_context):
+    """(int32 device tensor (B,), max position+S) from an int, a sequence or a tensor."""
+    if isinstance(position, torch.Tensor):
+        if position.dtype != torch.int32 or position.device != device or position.shape != (B,):
+            raise ValueError("position tensor must be int32 (B,) on the hidden states' device")
+        return position, max_context
+    if isinstance(position, int):
+        if position < 0:
+            raise ValueError("position must be >= 0")
+        return torch.full((B,), position, dtype=torch.int32, device=device), position + S
+    pos = [int(p) for p in position]
+    if len(pos) != B or min(pos) < 0:
+        raise ValueError("one non-negative position per sequence is required")
+    return torch.tensor(pos, dtype=torch.int32, device=device), max(pos) + S
+
+
+def _fill_args(hidden, attn_weights, kv_cache, position, rope_freqs, config, *, out, input_gamma=None,
+               residual=None, max_context=None):
+    _need(hidden, "hidden", BF16)
+    dev = hidden.device
+    if hidden.dim() != 3:
+        raise ValueError("hidden must be (B, S, hidden_size)")
+    B, S, D = hidden.shape
+    if D != config.hidden_size:
+        raise ValueError(f"hidden size {D} != config.hidden_size {config.hidden_size}")
+    ckv, kpe = kv_cache
+    _need(ckv, "compressed_kv_cache", BF16, dev)
+    _need(kpe, "k_pe_cache", BF16, dev)
+    if ckv.dim() != 3 or kpe.dim() != 3 or ckv.shape[:2] != kpe.shape[:2]:
+        raise ValueError("kv caches must be (B_alloc, max_seq, kv_lora) and (B_alloc, max_seq, rope)")
+    if ckv.shape[0] < B or ckv.shape[2] != config.kv_lora_rank or kpe.shape[2] != config.qk_rope_head_dim:
+        raise ValueError(f"kv cache shapes {tuple(ckv.shape)} / {tuple(kpe.shape)} do not fit batch {B}")
+    max_seq = ckv.shape[1]
+    if rope_freqs.dtype != torch.complex64 or rope_freqs.device != dev or not rope_freqs.is_contiguous():
+        raise TypeError("rope_freqs must be a contiguous complex64 tensor on the same device")
+    if rope_freqs.shape[1] != config.qk_rope_head_dim // 2:
+        raise ValueError("rope_freqs must have qk_rope_head_dim/2 columns")
+    pos_t, mc = _positions(position, B, S, dev, max_context)
+    if mc is None:
+        mc = min(max_seq, rope_freqs.shape[0])
+    if mc > max_seq:
+        raise ValueError(f"position + seq_len = {mc} exceeds the cache length {max_seq}")
+    if mc > rope_freqs.shape[0]:
+        raise ValueError(f"position + seq_len = {mc} exceeds the rope table length {rope_freqs.shape[0]}")
+    a = MlaArgs()
+    a.batch, a.seq_len, a.hidden = B, S, D
+    a.heads, a.q_lora, a.kv_lora = config.num_attention_heads, config.q_lora_rank, config.kv_lora_rank
+    a.qk_nope, a.qk_rope, a.v_dim = config.qk_nope_head_dim, config.qk_rope_head_dim, config.v_head_dim
+    a.max_seq, a.rope_rows, a.max_context = max_seq, rope_freqs.shape[0], mc
+    a.eps = float(config.rms_norm_eps)
+    a.softmax_scale = float(softmax_scale(config))
+    a.positions = pos_t.data_ptr()
+    a.hidden_states, a.out = hidden.data_ptr(), out.data_ptr()
+    a.input_gamma = input_gamma.data_ptr() if input_gamma is not None else None
+    a.residual = residual.data_ptr() if residual is not None else None
+    H = config.num_attention_heads
+    shapes = {
+        "q_a_proj": (config.q_lora_rank, D),
+        "q_b_proj": (H * config.qk_head_dim, config.q_lora_rank),
+        "kv_a_proj_with_mqa": (config.kv_lora_rank + config.qk_rope_head_dim, D),
+        "kv_b_proj": (H * (config.qk_nope_head_dim + config.v_head_dim), config.kv_lora_rank),
+        "o_proj": (D, H * config.v_head_dim),
+    }
+    fields = {"q_a_proj": ("w_q_a", "s_q_a"), "q_b_proj": ("w_q_b", "s_q_b"),
+              "kv_a_proj_with_mqa": ("w_kv_a", "s_kv_a"), "kv_b_proj": ("w_kv_b", "s_kv_b"),
+              "o_proj": ("w_o", "s_o")}
+    for name, (wf, sf) in fields.items():
+        w, s = attn_weights[name]
+        _need(w, f"{name}.weight", FP8, dev)
+        _need(s, f"{name}.weight_scale_inv", torch.float32, dev)
+        n, k = shapes[name]
+        if tuple(w.shape) != (n, k) or tuple(s.shape) != (math.ceil(n / 128), math.ceil(k / 128)):
+            raise ValueError(f"{name}: weight {tuple(w.shape)} / scale {tuple(s.shape)} do not match ({n}, {k})")
+        setattr(a, wf, w.data_ptr())
+        setattr(a, sf, s.data_ptr())
+    gq, gkv = attn_weights["q_a_layernorm"], attn_weights["kv_a_layernorm"]
+    _need(gq, "q_a_layernorm", BF16, dev)
+    _need(gkv, "kv_a_layernorm", BF16, dev)
+    a.gamma_q, a.gamma_kv = gq.data_ptr(), gkv.data_ptr()
+    a.ckv_cache, a.kpe_cache = ckv.data_ptr(), kpe.data_ptr()
+    a.rope_table = rope_freqs.data_ptr()
+    return a, pos_t
+
+
+def _run_mla(a: MlaArgs, device, stream: int, keep) -> None:
+    L = lib()
+    decode = a.seq_len == 1
+    need = (L.amla_mla_decode_workspace_bytes if decode else L.amla_mla_prefill_workspace_bytes)(a)
+    ws = workspace(device, need)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    rc = (L.amla_mla_decode if decode else L.amla_mla_prefill)(a, stream)
+    check(rc, "mla_decode" if decode else "mla_prefill")
+    del keep
+
+
+def mla_attention(hidden: torch.Tensor, attn_weights: dict, kv_cache: tuple, position, rope_freqs: torch.Tensor,
+                  config, *, max_context: int | None = None) -> torch.Tensor:
+    """inference/ops.py:100-183 on gfx950.
+
+    S == 1 runs the absorbed decode; S > 1 the kv_b decompression + causal
+    flash prefill.  Writes the raw new rows into ``kv_cache`` at
+    [position, position+S) like the reference.  ``max_context`` (largest
+    position+S) is only needed when ``position`` is a device tensor.
+    """
+    out = torch.empty_like(hidden)
+    a, pos_t = _fill_args(hidden, attn_weights, kv_cache, position, rope_freqs, config, out=out,
+                          max_context=max_context)
+    _run_mla(a, hidden.device, _stream_ptr(hidden), pos_t)
+    return out
+
+
+def mla_layer(hidden: torch.Tensor, input_layernorm: torch.Tensor, attn_weights: dict, kv_cache: tuple,
+              position, rope_freqs: torch.Tensor, config, *, max_context: int | None = None) -> torch.Tensor:
+    """Attention half of transformer_layer (inference/forward.py:92-94), fused:
+    ``hidden + mla_attention(rms_norm(hidden, input_layernorm), ...)`` with the
+    norm in the first projection's input and the bf16 residual add in o_proj's
+    epilogue."""
+    _need(input_layernorm, "input_layernorm", BF16, hidden.device)
+    out = torch.empty_like(hidden)
+    a, pos_t = _fill_args(hidden, attn_weights, kv_cache, position, rope_freqs, config, out=out,
+                          input_gamma=input_layernorm, residual=hidden, max_context=max_context)
+    _run_mla(a, hidden.device, _stream_ptr(hidden), pos_t)
+    return out

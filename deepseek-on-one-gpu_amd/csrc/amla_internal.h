@@ -1,0 +1,72 @@
+// Host-side plumbing shared by the translation units of libamla.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "amla.h"
+
+namespace amla {
+
+// Records a message for amla_last_error() and returns `code`.
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int check_launch(const char *what);
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ---------------------------------------------------------------- skinny fp8 GEMM
+
+enum GemvMode : int {
+  GEMV_PLAIN = 0,  // y[m, n] = bf16(acc)
+  GEMV_RESID = 1,  // y[m, n] = bf16(res[m, n] + bf16(acc))
+  GEMV_QKVA = 2,   // rows < n_split -> y; the rest -> latent / rope-key cache rows
+  GEMV_QROPE = 3,  // y = bf16(acc); rows with (n % head_dim) >= nope rotated by RoPE at pos(m)
+};
+
+struct GemvParams {
+  const uint16_t *x;  // (M, K) bf16, row stride ldx
+  int M, ldx;
+  const uint8_t *w0;  // rows [0, n_split) (all rows unless QKVA)
+  const float *s0;
+  const uint8_t *w1;  // rows [n_split, N) for QKVA
+  const float *s1;
+  int N, K, n_split;
+  uint16_t *y;
+  int ldy;
+  const uint16_t *res;  // RESID
+  int ldr;
+  uint16_t *ckv, *kpe;  // QKVA destinations
+  int64_t ckv_bstride, kpe_bstride;
+  int kv_lora, rope;
+  const int32_t *pos;   // per-m positions (QKVA, QROPE); m indexes (b * S + s)
+  int seq_len;          // S: position of row m is pos[m / S] + m % S
+  const float *rope_table;
+  int head_dim, nope;   // QROPE
+  float *ws;            // split-K partials (KS * 16*ceil(M/16) * N floats)
+  unsigned *counters;   // one zeroed counter per row group (reset to 0 by the kernel)
+};
+
+struct GemvPlan {
+  int rt, ks, kb_per_split, groups;
+  size_t partial_bytes;  // 0 when K is not split
+  size_t counter_count;  // counters the launch uses (0 when K is not split)
+};
+
+// Bytes of a standalone workspace: [counters | partials].
+size_t gemv_ws_bytes(const GemvPlan &pl);
+
+GemvPlan plan_gemv(int M, int N, int K);
+// Launches the skinny GEMM for M <= 64 (N % 16 == 0, K % 128 == 0, 16-byte aligned rows).
+int launch_gemv(const GemvParams &p, int mode, const GemvPlan &plan, hipStream_t stream);
+
+// Large-M fp8 GEMM with the same modes (M > 64).
+size_t gemm_ws_bytes(int M, int N, int K);
+int launch_gemm(const GemvParams &p, int mode, hipStream_t stream);
+
+int launch_rms_norm(const uint16_t *x, int64_t rows, int64_t dim, int64_t ldx, const uint16_t *gamma,
+                    float eps, uint16_t *y, int64_t ldy, hipStream_t stream);
+
+}  // namespace amla

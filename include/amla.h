@@ -1,0 +1,146 @@
+/* amla: MI355X (gfx950) absorbed-MLA + block-FP8 linear kernels, C ABI.
+ *
+ * Plain pointers and sizes only.  Every pointer argument is a device pointer
+ * unless noted; bf16 tensors are passed as raw 16-bit storage, fp8 weights as
+ * raw OCP e4m3fn bytes (torch.float8_e4m3fn), scales as fp32.  All calls are
+ * asynchronous on `stream` (a hipStream_t; NULL = the default stream), never
+ * synchronise the host and never allocate: outputs and workspaces belong to the
+ * caller.  Return value: 0 on success, < 0 for a bad argument (nothing is
+ * launched), > 0 a hipError_t from a launch.  amla_last_error() gives the
+ * message of the last failing call on the calling thread.
+ *
+ * The reference (sushruta/deepseek-on-one-gpu) has no FFI: its path is the set
+ * of Python functions in inference/ops.py.  Each entry point below names the
+ * function it replaces.
+ */
+#ifndef AMLA_H_
+#define AMLA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AMLA_OK 0
+#define AMLA_EINVAL (-1)
+#define AMLA_EWORKSPACE (-2)
+#define AMLA_EUNSUPPORTED (-3)
+
+/* Version of this ABI (major * 100 + minor). */
+int amla_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *amla_last_error(void);
+
+/* Replaces the dequantisation half of fp8_linear, inference/ops.py:30-43:
+ *   out[i*k + j] = f32(weight[i*k + j]) * scale_inv[(i/128) * ceil(k/128) + j/128]
+ * Bit-exact fp32 (exact e4m3 convert, one RNE multiply).
+ * weight (n, k) e4m3fn row-major; scale_inv (ceil(n/128), ceil(k/128)) fp32;
+ * out (n, k) fp32. */
+int amla_fp8_block_dequant(const void *weight, const float *scale_inv, int64_t n, int64_t k,
+                           float *out, void *stream);
+
+/* Replaces fp8_linear(x, weight, scale_inv, out_dtype=bf16), inference/ops.py:15-44:
+ *   y[i, j] = bf16( sum_k x[i, k] * f32(weight[j, k]) * scale_inv[j/128, k/128] )
+ * fp32 accumulation; x (m, k) bf16 with row stride ldx; y (m, n) bf16 with row
+ * stride ldy.  Split-K partials use `workspace` (size from
+ * amla_fp8_linear_workspace_bytes; it must hold zeros on the first call and is
+ * left zeroed for the next). */
+int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void *weight,
+                    const float *scale_inv, int64_t n, void *y, int64_t ldy, void *workspace,
+                    size_t workspace_bytes, void *stream);
+size_t amla_fp8_linear_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
+/* Replaces rms_norm(x, weight, eps), inference/ops.py:10-12:
+ *   r = rsqrt(mean(f32(x)^2) + eps);  y = bf16( bf16(f32(x) * r) * gamma )
+ * x (rows, dim) bf16, row stride ldx; gamma (dim) bf16; y (rows, dim), ldy. */
+int amla_rms_norm(const void *x, int64_t rows, int64_t dim, int64_t ldx, const void *gamma,
+                  float eps, void *y, int64_t ldy, void *stream);
+
+/* Replaces apply_rope(x, freqs), inference/ops.py:86-97, for x laid out as
+ * (groups, s, dim) bf16 (dim even, pairs (2i, 2i+1) interleaved) and freqs as
+ * (s, dim/2) complex64 viewed as fp32 (cos, sin) pairs:
+ *   (y0, y1) = bf16( x0*cos - x1*sin, x0*sin + x1*cos )  in fp32. */
+int amla_apply_rope(const void *x, int64_t groups, int64_t s, int64_t dim, const float *freqs,
+                    void *y, void *stream);
+
+/* Arguments of one MLA call (decode or prefill) for DeepSeek-R1 dimensions.
+ * Mirrors the arguments of mla_attention(hidden, attn_weights, kv_cache,
+ * position, rope_freqs, config), inference/ops.py:100-107, unpacked:
+ * attn_weights keys (inference/weight_store.py:208-226) become w_* / s_* / gamma_*,
+ * kv_cache the two cache pointers, rope_freqs the fp32 (cos, sin) table. */
+typedef struct amla_mla_args {
+  /* dimensions (config fields, inference/config.py:8-20) */
+  int32_t batch;        /* B */
+  int32_t seq_len;      /* S new tokens per sequence (1 = decode) */
+  int32_t hidden;       /* 7168 */
+  int32_t heads;        /* 128 */
+  int32_t q_lora;       /* 1536 */
+  int32_t kv_lora;      /* 512 */
+  int32_t qk_nope;      /* 128 */
+  int32_t qk_rope;      /* 64 */
+  int32_t v_dim;        /* 128 */
+  int32_t max_seq;      /* cache rows per sequence */
+  int32_t rope_rows;    /* rows of the rope table */
+  int32_t max_context;  /* upper bound of position+S over the batch (scheduling) */
+  float eps;            /* rms_norm_eps */
+  float softmax_scale;  /* yarn_get_mscale(factor, mscale_all_dim) / sqrt(qk_head_dim) */
+  /* first new position of each sequence: positions[b] (device int32, length
+   * batch); the reference's scalar `position` is the case of all-equal entries */
+  const int32_t *positions;
+  /* activations */
+  const void *hidden_states;  /* (B, S, hidden) bf16, already input-normed unless input_gamma */
+  void *out;                  /* (B, S, hidden) bf16 */
+  /* optional transformer_layer attention half (inference/forward.py:92-94):
+   * if input_gamma != NULL, hidden_states is normed with it first; if
+   * residual != NULL, out = residual + attention (bf16 add). */
+  const void *input_gamma;
+  const void *residual;
+  /* block-FP8 projections (weight e4m3fn row-major, scale_inv fp32) */
+  const void *w_q_a;  const float *s_q_a;   /* (q_lora, hidden) */
+  const void *w_q_b;  const float *s_q_b;   /* (heads*(nope+rope), q_lora) */
+  const void *w_kv_a; const float *s_kv_a;  /* (kv_lora+rope, hidden) */
+  const void *w_kv_b; const float *s_kv_b;  /* (heads*(nope+v), kv_lora) */
+  const void *w_o;    const float *s_o;     /* (hidden, heads*v) */
+  const void *gamma_q;   /* q_a_layernorm (q_lora) bf16 */
+  const void *gamma_kv;  /* kv_a_layernorm (kv_lora) bf16 */
+  /* latent cache (B_alloc, max_seq, kv_lora) and rope-key cache
+   * (B_alloc, max_seq, qk_rope), bf16, raw (pre-norm, pre-RoPE) rows;
+   * rows [positions[b], positions[b]+S) of sequence b are written. */
+  void *ckv_cache;
+  void *kpe_cache;
+  const float *rope_table;  /* (rope_rows, qk_rope/2, 2) fp32 cos/sin */
+  void *workspace;
+  size_t workspace_bytes;
+} amla_mla_args;
+
+/* Replaces mla_attention(...) for S == 1, inference/ops.py:100-183, computed in
+ * absorbed form (q_nope.W_UK into latent space, scores on the raw latent +
+ * rope cache, online softmax split over context, latent.W_UV back to heads). */
+int amla_mla_decode(const amla_mla_args *args, void *stream);
+
+/* Measurement hook with no counterpart in the reference: amla_mla_decode that
+ * also records events[i] (hipEvent_t) on `stream` before each of its 7 stages
+ * (q_a|kv_a projection, q_a norm, q_b projection + RoPE, W_UK absorption,
+ * attention, split merge + W_UV, o_proj) and events[7] after the last, so a
+ * benchmark can time each kernel on the stream it runs on. */
+int amla_mla_decode_profiled(const amla_mla_args *args, void *stream, void *const *events);
+
+/* Replaces mla_attention(...) for S >= 1 with a causal mask over the new rows
+ * (inference/ops.py:100-183 incl. :172-177): kv_b decompression of the cached
+ * rows and flash attention with bf16 MFMA. */
+int amla_mla_prefill(const amla_mla_args *args, void *stream);
+
+/* Workspace bytes amla_mla_decode / amla_mla_prefill need for these args
+ * (pointer fields are ignored).  The workspace must be zero-filled before its
+ * first use; calls leave it zeroed where a later call relies on that. */
+size_t amla_mla_decode_workspace_bytes(const amla_mla_args *args);
+size_t amla_mla_prefill_workspace_bytes(const amla_mla_args *args);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AMLA_H_ */

@@ -1,0 +1,96 @@
+"""The C ABI (include/amla.h) without a GPU: exports, struct layout, host-side argument checks."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from amla import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "amla.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(amla_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    L = _lib.lib()
+    names = _declared()
+    assert len(names) >= 11
+    for n in names:
+        assert hasattr(L, n), n
+    assert {s[0] for s in _lib.SIGNATURES} == set(names)
+    assert L.amla_abi_version() == 100
+
+
+def test_args_struct_layout_matches_c(tmp_path):
+    fields = [f for f, _ in _lib.MlaArgs._fields_]
+    src = tmp_path / "layout.c"
+    body = "\n".join(f'  printf("{f} %zu\\n", offsetof(amla_mla_args, {f}));' for f in fields)
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "amla.h"\nint main(void){\n'
+                   f'  printf("sizeof %zu\\n", sizeof(amla_mla_args));\n{body}\n  return 0;\n}}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    out = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines())
+    assert int(out["sizeof"]) == ctypes.sizeof(_lib.MlaArgs)
+    for f in fields:
+        assert int(out[f]) == getattr(_lib.MlaArgs, f).offset, f
+
+
+def test_null_and_bad_arguments_fail_before_launch():
+    L = _lib.lib()
+    assert L.amla_fp8_linear(None, 1, 128, 128, None, None, 16, None, 16, None, 0, None) == -1
+    assert b"null" in L.amla_last_error()
+    assert L.amla_fp8_block_dequant(None, None, 4, 4, None, None) == -1
+    assert L.amla_rms_norm(None, 1, 8, 8, None, 1e-6, None, 8, None) == -1
+    assert L.amla_apply_rope(None, 1, 1, 64, None, None, None) == -1
+    assert L.amla_mla_decode(None, None) == -1
+    assert L.amla_mla_prefill(None, None) == -1
+    a = _lib.MlaArgs()
+    a.batch, a.seq_len, a.hidden, a.heads, a.q_lora = 1, 1, 7168, 64, 1536
+    a.kv_lora, a.qk_nope, a.qk_rope, a.v_dim, a.max_seq, a.rope_rows = 512, 128, 64, 128, 16, 16
+    assert L.amla_mla_decode(ctypes.byref(a), None) == -3      # unsupported head count
+    assert b"heads=128" in L.amla_last_error()
+    a.heads = 128
+    assert L.amla_mla_decode(ctypes.byref(a), None) == -1      # null pointers
+    # a fake non-null workspace that is too small: rejected on the host
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.cast(buf, ctypes.c_void_p).value
+    for f in ("positions", "hidden_states", "out", "w_q_a", "s_q_a", "w_q_b", "s_q_b", "w_kv_a", "s_kv_a",
+              "w_kv_b", "s_kv_b", "w_o", "s_o", "gamma_q", "gamma_kv", "ckv_cache", "kpe_cache", "rope_table",
+              "workspace"):
+        setattr(a, f, p + 16 - p % 16 if p % 16 else p)
+    a.workspace_bytes = 16
+    assert L.amla_mla_decode(ctypes.byref(a), None) == -2
+    assert b"workspace" in L.amla_last_error()
+    a.seq_len = 2
+    assert L.amla_mla_decode(ctypes.byref(a), None) == -1      # decode needs S == 1
+    # fp8_linear shape constraints
+    assert L.amla_fp8_linear(p, 1, 100, 100, p, p, 16, p, 16, None, 0, None) == -3
+    assert L.amla_fp8_linear(p, 1, 128, 64, p, p, 16, p, 16, None, 0, None) == -1
+
+
+def test_workspace_queries():
+    L = _lib.lib()
+    assert L.amla_fp8_linear_workspace_bytes(1, 7168, 16384) > 0      # split-K
+    assert L.amla_fp8_linear_workspace_bytes(1, 24576, 1536) == 0     # no split
+    a = _lib.MlaArgs()
+    a.batch, a.seq_len, a.hidden, a.heads, a.q_lora = 8, 1, 7168, 128, 1536
+    a.kv_lora, a.qk_nope, a.qk_rope, a.v_dim = 512, 128, 64, 128
+    a.max_seq = a.rope_rows = a.max_context = 32768
+    n = L.amla_mla_decode_workspace_bytes(ctypes.byref(a))
+    assert 32 * 8 * 128 * 512 * 4 <= n < 200 << 20
+
+
+def test_python_api_rejects_cpu_tensors():
+    from amla import ops
+    x = torch.zeros(2, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        ops.rms_norm(x, torch.ones(128, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        ops.fp8_linear(x, torch.zeros(16, 128).to(torch.float8_e4m3fn), torch.ones(1, 1))

@@ -1,0 +1,194 @@
+"""GPU parity of the MLA decode / prefill / layer entry points against the oracle.
+
+Full DeepSeek-R1 MLA dimensions; the oracle (oracle/ref_ops.py, torch on the
+CPU with the reference's rounding points) runs on identical seeded inputs.
+"""
+import functools
+
+import pytest
+import torch
+
+from oracle import ref_ops as R
+from amla import ops, synth
+from amla.config import DeepSeekConfig
+from _tol import assert_parity, assert_bf16_ulps
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+R1 = DeepSeekConfig()
+
+
+@functools.lru_cache(maxsize=2)
+def _layer(tag):
+    return synth.make_layer(R1, tag)
+
+
+@functools.lru_cache(maxsize=1)
+def _rope(n):
+    return R.precompute_rope_freqs(R1, n)
+
+
+def _to_dev(aw):
+    return {k: (tuple(t.to(DEV) for t in v) if isinstance(v, tuple) else v.to(DEV)) for k, v in aw.items()}
+
+
+def _run_case(tag, B, S, positions, max_seq, filled=None, layer_mode=False, max_context=None):
+    """Runs oracle and GPU on the same inputs; returns (gpu_out, ref_out, gpu_cache, ref_cache)."""
+    print(f"[case] {tag} B={B} S={S} positions={positions} max_seq={max_seq} layer={layer_mode}", flush=True)
+    lay = _layer("mla/" + tag.split(":")[0])
+    hidden = synth.make_hidden(R1, B, S, tag)
+    if filled is None:
+        filled = list(positions) if not isinstance(positions, int) else [positions] * B
+    ckv, kpe = synth.make_kv_cache(R1, B, max_seq, filled, tag)
+    tab = _rope(max_seq)
+    ref_ckv, ref_kpe = ckv.clone(), kpe.clone()
+    if isinstance(positions, int):
+        if layer_mode:
+            want = R.transformer_layer_attention(hidden, lay.input_layernorm, lay.attn_weights, (ref_ckv, ref_kpe),
+                                                 positions, tab, R1)
+        else:
+            want = R.mla_attention(hidden, lay.attn_weights, (ref_ckv, ref_kpe), positions, tab, R1)
+    else:
+        assert not layer_mode
+        want = R.mla_attention_per_sequence(hidden, lay.attn_weights, (ref_ckv, ref_kpe), positions, tab, R1)
+    aw = _to_dev(lay.attn_weights)
+    g_ckv, g_kpe = ckv.to(DEV), kpe.to(DEV)
+    if layer_mode:
+        got = ops.mla_layer(hidden.to(DEV), lay.input_layernorm.to(DEV), aw, (g_ckv, g_kpe), positions,
+                            tab.to(DEV), R1, max_context=max_context)
+    else:
+        got = ops.mla_attention(hidden.to(DEV), aw, (g_ckv, g_kpe), positions, tab.to(DEV), R1,
+                                max_context=max_context)
+    torch.cuda.synchronize()
+    return got.cpu(), want, (g_ckv.cpu(), g_kpe.cpu()), (ref_ckv, ref_kpe)
+
+
+def _check_cache(gc, rc, rows):
+    for b, (lo, hi) in enumerate(rows):
+        assert_bf16_ulps(gc[0][b, lo:hi], rc[0][b, lo:hi], 2, "ckv rows")
+        assert_bf16_ulps(gc[1][b, lo:hi], rc[1][b, lo:hi], 2, "kpe rows")
+    # nothing else was touched
+    mask = torch.ones(gc[0].shape[:2], dtype=torch.bool)
+    for b, (lo, hi) in enumerate(rows):
+        mask[b, lo:hi] = False
+    assert torch.equal(gc[0][mask], rc[0][mask]) and torch.equal(gc[1][mask], rc[1][mask])
+
+
+def test_decode_t257(golden):
+    got, want, gc, rc = _run_case("decode257", 1, 1, 256, 264)
+    assert_parity(got, want, "decode B=1 T=257")
+    _check_cache(gc, rc, [(256, 257)])
+    # the reference's own output for these inputs (tests/golden/make_golden.py)
+    tens, man = golden
+    e = man["r1_decode_t257"]
+    lay = synth.make_layer(R1, e["tag"])
+    if synth.sha256_of(lay.attn_weights["o_proj"][0]) == e["sha256"]["o_proj"]:
+        hidden = synth.make_hidden(R1, 1, 1, e["tag"])
+        ckv, kpe = synth.make_kv_cache(R1, 1, e["max_seq"], e["filled"], e["tag"])
+        tab = R.precompute_rope_freqs(R1, e["max_seq"]).to(DEV)
+        out = ops.mla_attention(hidden.to(DEV), _to_dev(lay.attn_weights), (ckv.to(DEV), kpe.to(DEV)), 256, tab, R1)
+        assert_parity(out.cpu(), tens["r1_decode_t257.out"].view(torch.bfloat16), "decode vs reference golden")
+
+
+def test_decode_t4096():
+    got, want, gc, rc = _run_case("decode4096", 1, 1, 4095, 4096)
+    assert_parity(got, want, "decode B=1 T=4096")
+    _check_cache(gc, rc, [(4095, 4096)])
+
+
+def test_decode_batch8_shared_position():
+    got, want, gc, rc = _run_case("decodeb8", 8, 1, 1023, 1030)
+    assert_parity(got, want, "decode B=8 T=1024")
+    _check_cache(gc, rc, [(1023, 1024)] * 8)
+
+
+def test_decode_ragged_positions():
+    pos = [100, 777, 1500, 31, 0]
+    got, want, gc, rc = _run_case("ragged", 5, 1, pos, 1600)
+    assert_parity(got, want, "ragged decode")
+    _check_cache(gc, rc, [(p, p + 1) for p in pos])
+
+
+def test_decode_split_count_does_not_matter():
+    a, want, _, _ = _run_case("splits", 2, 1, 3000, 8192, max_context=3001)
+    b, _, _, _ = _run_case("splits", 2, 1, 3000, 8192, max_context=8192)
+    assert_parity(a, want, "splits tight")
+    assert_parity(b, want, "splits loose")
+    assert_parity(a, b, "split plan independence")
+
+
+def test_decode_single_position_ignores_query():
+    # T = 1: softmax == 1, the output cannot depend on the query path
+    lay = _layer("mla/t1")
+    hidden = synth.make_hidden(R1, 1, 1, "t1").to(DEV)
+    tab = _rope(8).to(DEV)
+    outs = []
+    for mul in (1.0, 3.0):
+        aw = _to_dev(lay.attn_weights)
+        w, s = aw["q_b_proj"]
+        aw["q_b_proj"] = (w, s * mul)
+        ckv = torch.zeros(1, 8, 512, dtype=torch.bfloat16, device=DEV)
+        kpe = torch.zeros(1, 8, 64, dtype=torch.bfloat16, device=DEV)
+        outs.append(ops.mla_attention(hidden, aw, (ckv, kpe), 0, tab, R1).cpu())
+    assert_parity(outs[0], outs[1], "T=1 independent of q")
+
+
+@pytest.mark.parametrize("S", [8, 64, 300])
+def test_prefill_from_empty(S):
+    got, want, gc, rc = _run_case(f"prefill{S}", 1, S, 0, S + 8)
+    assert_parity(got, want, f"prefill S={S}")
+    _check_cache(gc, rc, [(0, S)])
+
+
+def test_prefill_1024():
+    got, want, gc, rc = _run_case("prefill1024", 1, 1024, 0, 1024)
+    assert_parity(got, want, "prefill S=1024")
+    _check_cache(gc, rc, [(0, 1024)])
+
+
+def test_prefill_chunk_after_cache():
+    got, want, gc, rc = _run_case("chunk", 2, 32, 100, 200)
+    assert_parity(got, want, "chunked prefill B=2 S=32 at 100")
+    _check_cache(gc, rc, [(100, 132)] * 2)
+
+
+def test_layer_mode_decode_and_prefill():
+    got, want, _, _ = _run_case("layerdec", 2, 1, 700, 704, layer_mode=True)
+    assert_parity(got, want, "layer decode")
+    got, want, _, _ = _run_case("layerpre", 1, 96, 0, 96, layer_mode=True)
+    assert_parity(got, want, "layer prefill")
+
+
+def test_prefill_row_equals_decode():
+    """Prefill of S tokens, row S-1 == prefill of S-1 tokens followed by a decode step."""
+    lay = _layer("mla/consistency")
+    aw = _to_dev(lay.attn_weights)
+    S = 40
+    hidden = synth.make_hidden(R1, 1, S, "consistency").to(DEV)
+    tab = _rope(64).to(DEV)
+    c1 = (torch.zeros(1, 64, 512, dtype=torch.bfloat16, device=DEV), torch.zeros(1, 64, 64, dtype=torch.bfloat16, device=DEV))
+    full = ops.mla_attention(hidden, aw, c1, 0, tab, R1)
+    c2 = (torch.zeros_like(c1[0]), torch.zeros_like(c1[1]))
+    ops.mla_attention(hidden[:, :S - 1].contiguous(), aw, c2, 0, tab, R1)
+    last = ops.mla_attention(hidden[:, S - 1:].contiguous(), aw, c2, S - 1, tab, R1)
+    assert_parity(last.cpu(), full[:, S - 1:].cpu(), "decode step vs prefill row")
+    assert_bf16_ulps(c2[0].cpu(), c1[0].cpu(), 2, "cache rows")
+
+
+def test_bad_arguments_raise_before_launch():
+    lay = _layer("mla/t1")
+    aw = _to_dev(lay.attn_weights)
+    tab = _rope(8).to(DEV)
+    hidden = torch.zeros(1, 1, 7168, dtype=torch.bfloat16, device=DEV)
+    ckv = torch.zeros(1, 8, 512, dtype=torch.bfloat16, device=DEV)
+    kpe = torch.zeros(1, 8, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        ops.mla_attention(hidden, aw, (ckv, kpe), 8, tab, R1)            # beyond the cache
+    with pytest.raises(TypeError):
+        ops.mla_attention(hidden.float(), aw, (ckv, kpe), 0, tab, R1)    # dtype
+    with pytest.raises(ValueError):
+        ops.mla_attention(hidden, aw, (ckv[:, :, :256].contiguous(), kpe), 0, tab, R1)   # cache width
+    bad = dict(aw)
+    bad["o_proj"] = (aw["o_proj"][0][:, :8192].contiguous(), aw["o_proj"][1])
+    with pytest.raises(ValueError):
+        ops.mla_attention(hidden, bad, (ckv, kpe), 0, tab, R1)
