@@ -55,7 +55,19 @@ struct GemvPlan {
   size_t counter_count;  // counters the launch uses (0 when K is not split)
 };
 
-// Bytes of a standalone workspace: [counters | partials].
+// Every workspace handed to an entry point starts with the same counter
+// region: COUNTER_SLOTS slots of COUNTERS_PER_SLOT split-K tile counters.  The
+// kernels leave counters at zero, and no entry point puts anything else there,
+// so one zero-filled workspace can be shared by all entry points.
+constexpr int COUNTER_SLOTS = 8;
+constexpr int COUNTERS_PER_SLOT = 4096;
+constexpr size_t COUNTER_BYTES = (size_t)COUNTER_SLOTS * COUNTERS_PER_SLOT * sizeof(unsigned);
+
+inline unsigned *counter_slot(void *ws, int slot) {
+  return reinterpret_cast<unsigned *>(ws) + (size_t)slot * COUNTERS_PER_SLOT;
+}
+
+// Bytes of a standalone fp8_linear workspace: [counter region | partials].
 size_t gemv_ws_bytes(const GemvPlan &pl);
 
 GemvPlan plan_gemv(int M, int N, int K);

@@ -274,9 +274,7 @@ GemvPlan plan_gemv(int M, int N, int K) {
   return pl;
 }
 
-size_t gemv_ws_bytes(const GemvPlan &pl) {
-  return pl.ks > 1 ? align_up(pl.counter_count * sizeof(unsigned), 256) + pl.partial_bytes : 0;
-}
+size_t gemv_ws_bytes(const GemvPlan &pl) { return pl.ks > 1 ? COUNTER_BYTES + pl.partial_bytes : 0; }
 
 template <int RT, int MT>
 static void launch_rt_mt(const GemvParams &p, int mode, const GemvPlan &pl, hipStream_t st) {
@@ -303,6 +301,8 @@ int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t 
     return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM needs N %% 16 == 0 and K %% 128 == 0 (N=%d K=%d)", p0.N, p0.K);
   if (pl.ks > 1 && (!p0.ws || !p0.counters))
     return fail(AMLA_EWORKSPACE, "split-K GEMM needs partial and counter workspace");
+  if (pl.counter_count > (size_t)COUNTERS_PER_SLOT)
+    return fail(AMLA_EUNSUPPORTED, "split-K GEMM: %zu tile counters exceed a slot", pl.counter_count);
   if (pl.rt == 1) launch_rt<1>(p0, mode, pl, st);
   else launch_rt<2>(p0, mode, pl, st);
   return check_launch("fp8 skinny GEMM");
@@ -427,9 +427,10 @@ int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void
   if (m > 64) return launch_gemm(p, GEMV_PLAIN, st);
   const GemvPlan pl = plan_gemv((int)m, (int)n, (int)k);
   if (pl.ks > 1) {
-    p.counters = reinterpret_cast<unsigned *>(workspace);
-    p.ws = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) +
-                                     align_up(pl.counter_count * sizeof(unsigned), 256));
+    if (pl.counter_count > (size_t)COUNTERS_PER_SLOT)
+      return fail(AMLA_EUNSUPPORTED, "fp8_linear: %zu split-K tiles exceed a counter slot", pl.counter_count);
+    p.counters = counter_slot(workspace, 0);
+    p.ws = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) + COUNTER_BYTES);
   }
   return launch_gemv(p, GEMV_PLAIN, pl, st);
 }

@@ -442,7 +442,7 @@ static DecodeLayout decode_layout(const amla_mla_args &a) {
   L.splits = (ntiles + L.tiles_per_split - 1) / L.tiles_per_split;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes, 256); return o; };
-  L.counters = take(3 * 4096 * sizeof(unsigned));
+  L.counters = take(COUNTER_BYTES);
   L.partials = take(std::max({L.pa.partial_bytes, L.pb.partial_bytes, L.po.partial_bytes, (size_t)256}));
   L.xn = take((size_t)B * a.hidden * 2);
   L.qa = take((size_t)B * a.q_lora * 2);
@@ -494,7 +494,6 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   if (a->workspace_bytes < L.total)
     return fail(AMLA_EWORKSPACE, "mla_decode: workspace %zu bytes < %zu needed", a->workspace_bytes, L.total);
   char *ws = reinterpret_cast<char *>(a->workspace);
-  unsigned *cnt = reinterpret_cast<unsigned *>(ws + L.counters);
   float *partials = reinterpret_cast<float *>(ws + L.partials);
   const int B = a->batch;
   const int HD = a->qk_nope + a->qk_rope;
@@ -524,7 +523,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pa.kpe = reinterpret_cast<uint16_t *>(a->kpe_cache);
   pa.ckv_bstride = (int64_t)a->max_seq * LORA; pa.kpe_bstride = (int64_t)a->max_seq * ROPE;
   pa.kv_lora = LORA; pa.rope = ROPE; pa.pos = a->positions; pa.seq_len = 1;
-  pa.ws = partials; pa.counters = cnt;
+  pa.ws = partials; pa.counters = counter_slot(ws, 1);
   if ((rc = launch_gemv(pa, GEMV_QKVA, L.pa, st))) return rc;
 
   // 2. q_a_layernorm (inference/ops.py:130)
@@ -542,7 +541,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pb.y = q; pb.ldy = pb.N;
   pb.pos = a->positions; pb.seq_len = 1; pb.rope = ROPE; pb.rope_table = a->rope_table;
   pb.head_dim = HD; pb.nope = a->qk_nope;
-  pb.ws = partials; pb.counters = cnt + 4096;
+  pb.ws = partials; pb.counters = counter_slot(ws, 2);
   if ((rc = launch_gemv(pb, GEMV_QROPE, L.pb, st))) return rc;
 
   // 4. absorb W_UK into the query
@@ -585,7 +584,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   po.y = reinterpret_cast<uint16_t *>(a->out); po.ldy = a->hidden;
   po.res = reinterpret_cast<const uint16_t *>(a->residual); po.ldr = a->hidden;
   po.seq_len = 1;
-  po.ws = partials; po.counters = cnt + 2 * 4096;
+  po.ws = partials; po.counters = counter_slot(ws, 3);
   rc = launch_gemv(po, a->residual ? GEMV_RESID : GEMV_PLAIN, L.po, st);
   mark(ev, NSTAGE, st);
   return rc;

@@ -413,7 +413,7 @@ static PrefillLayout prefill_layout(const amla_mla_args &a) {
   upd((int)M, a.hidden, a.heads * a.v_dim);
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes, 256); return o; };
-  L.counters = take(4 * 4096 * sizeof(unsigned));
+  L.counters = take(COUNTER_BYTES);
   L.partials = take(part);
   L.xn = take(M * a.hidden * 2);
   L.qa = take(M * a.q_lora * 2);
@@ -464,7 +464,6 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   if (a->workspace_bytes < L.total)
     return fail(AMLA_EWORKSPACE, "mla_prefill: workspace %zu bytes < %zu needed", a->workspace_bytes, L.total);
   char *ws = reinterpret_cast<char *>(a->workspace);
-  unsigned *cnt = reinterpret_cast<unsigned *>(ws + L.counters);
   float *partials = reinterpret_cast<float *>(ws + L.partials);
   const int B = a->batch, S = a->seq_len, M = B * S;
   const int HD = a->qk_nope + a->qk_rope;
@@ -496,7 +495,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   pa.kpe = reinterpret_cast<uint16_t *>(a->kpe_cache);
   pa.ckv_bstride = (int64_t)a->max_seq * a->kv_lora; pa.kpe_bstride = (int64_t)a->max_seq * a->qk_rope;
   pa.kv_lora = a->kv_lora; pa.rope = a->qk_rope; pa.pos = a->positions; pa.seq_len = S;
-  if ((rc = run_linear(pa, GEMV_QKVA, cnt, partials, st))) return rc;
+  if ((rc = run_linear(pa, GEMV_QKVA, counter_slot(ws, 4), partials, st))) return rc;
 
   if ((rc = launch_rms_norm(qa, M, a->q_lora, a->q_lora, reinterpret_cast<const uint16_t *>(a->gamma_q), a->eps,
                             qan, a->q_lora, st)))
@@ -509,7 +508,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   pb.y = q; pb.ldy = pb.N;
   pb.pos = a->positions; pb.seq_len = S; pb.rope = a->qk_rope; pb.rope_table = a->rope_table;
   pb.head_dim = HD; pb.nope = a->qk_nope;
-  if ((rc = run_linear(pb, GEMV_QROPE, cnt + 4096, partials, st))) return rc;
+  if ((rc = run_linear(pb, GEMV_QROPE, counter_slot(ws, 5), partials, st))) return rc;
 
   const int T = L.Tmax;
   FlashParams fp = {};
@@ -529,7 +528,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
     pk.w0 = reinterpret_cast<const uint8_t *>(a->w_kv_b); pk.s0 = a->s_kv_b;
     pk.N = a->heads * (a->qk_nope + a->v_dim); pk.K = a->kv_lora; pk.n_split = pk.N;
     pk.y = kvb; pk.ldy = pk.N; pk.seq_len = 1;
-    if ((rc = run_linear(pk, GEMV_PLAIN, cnt + 2 * 4096, partials, st))) return rc;
+    if ((rc = run_linear(pk, GEMV_PLAIN, counter_slot(ws, 6), partials, st))) return rc;
     fp.b = b;
     flash_kernel<<<dim3(P_H, (S + P_QB - 1) / P_QB), 256, 0, st>>>(fp);
     if ((rc = check_launch("flash attention"))) return rc;
@@ -541,7 +540,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   po.N = a->hidden; po.K = a->heads * a->v_dim; po.n_split = po.N;
   po.y = reinterpret_cast<uint16_t *>(a->out); po.ldy = a->hidden;
   po.res = reinterpret_cast<const uint16_t *>(a->residual); po.ldr = a->hidden; po.seq_len = 1;
-  return run_linear(po, a->residual ? GEMV_RESID : GEMV_PLAIN, cnt + 3 * 4096, partials, st);
+  return run_linear(po, a->residual ? GEMV_RESID : GEMV_PLAIN, counter_slot(ws, 7), partials, st);
 }
 
 }  // namespace amla

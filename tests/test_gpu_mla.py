@@ -175,6 +175,21 @@ def test_prefill_row_equals_decode():
     assert_bf16_ulps(c2[0].cpu(), c1[0].cpu(), 2, "cache rows")
 
 
+def test_entry_points_share_one_workspace():
+    """Decode, standalone split-K fp8_linear and prefill interleaved on one
+    workspace: each leaves the shared split-K counters at zero for the next."""
+    a, want_a, _, _ = _run_case("share", 4, 1, 2047, 2050)
+    w, s = _layer("mla/share").attn_weights["o_proj"]
+    x = synth.randn((3, w.shape[1]), 77).to(torch.bfloat16)
+    y = ops.fp8_linear(x.to(DEV), w.to(DEV), s.to(DEV)).cpu()
+    b, want_b, _, _ = _run_case("share:pre", 1, 8, 0, 16)
+    c, want_c, _, _ = _run_case("share", 4, 1, 2047, 2050)
+    assert_parity(a, want_a, "decode before")
+    assert_parity(y, R.fp8_linear(x, w, s), "split-K linear between")
+    assert_parity(b, want_b, "prefill after decode")
+    assert_parity(c, want_c, "decode after prefill")
+
+
 def test_bad_arguments_raise_before_launch():
     lay = _layer("mla/t1")
     aw = _to_dev(lay.attn_weights)
