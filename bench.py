@@ -113,6 +113,10 @@ def decode_stage_times(stack, caches, hidden, pos, rope, ctx, reps=2):
     st = torch.cuda.current_stream(dev)
     nev = 8
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(nev)] for _ in range(len(stack) * reps)]
+    for row in evs:          # torch creates the hipEvent on first record
+        for e in row:
+            e.record(st)
+    torch.cuda.synchronize()
     out = torch.empty_like(hidden)
     k = 0
     for _ in range(reps):

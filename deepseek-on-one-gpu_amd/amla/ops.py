@@ -51,16 +51,15 @@ _workspaces: dict = {}
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device zero-initialised scratch, grown on demand.
+    """Per-device scratch for the MLA entry points, grown on demand.
 
-    Kernels that use split-K counters leave them at zero, so the buffer is
-    reusable across calls on one stream.  Size it (one eager call) before a
-    HIP graph capture so that no allocation happens while capturing.
+    Size it (one eager call) before a HIP graph capture so that no allocation
+    happens while capturing.
     """
     key = (device.type, device.index)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf
 

@@ -45,30 +45,13 @@ struct GemvParams {
   int seq_len;          // S: position of row m is pos[m / S] + m % S
   const float *rope_table;
   int head_dim, nope;   // QROPE
-  float *ws;            // split-K partials (KS * 16*ceil(M/16) * N floats)
-  unsigned *counters;   // one zeroed counter per row group (reset to 0 by the kernel)
 };
 
 struct GemvPlan {
-  int rt, ks, kb_per_split, groups;
-  size_t partial_bytes;  // 0 when K is not split
-  size_t counter_count;  // counters the launch uses (0 when K is not split)
+  int rt;      // 16-row tiles per workgroup
+  int nw;      // waves per workgroup (split of K inside the workgroup)
+  int groups;  // workgroups
 };
-
-// Every workspace handed to an entry point starts with the same counter
-// region: COUNTER_SLOTS slots of COUNTERS_PER_SLOT split-K tile counters.  The
-// kernels leave counters at zero, and no entry point puts anything else there,
-// so one zero-filled workspace can be shared by all entry points.
-constexpr int COUNTER_SLOTS = 8;
-constexpr int COUNTERS_PER_SLOT = 4096;
-constexpr size_t COUNTER_BYTES = (size_t)COUNTER_SLOTS * COUNTERS_PER_SLOT * sizeof(unsigned);
-
-inline unsigned *counter_slot(void *ws, int slot) {
-  return reinterpret_cast<unsigned *>(ws) + (size_t)slot * COUNTERS_PER_SLOT;
-}
-
-// Bytes of a standalone fp8_linear workspace: [counter region | partials].
-size_t gemv_ws_bytes(const GemvPlan &pl);
 
 GemvPlan plan_gemv(int M, int N, int K);
 // Launches the skinny GEMM for M <= 64 (N % 16 == 0, K % 128 == 0, 16-byte aligned rows).

@@ -12,10 +12,11 @@
 // v_mfma_f32_16x16x32_bf16 against x^T (batch rows as the MFMA N dimension).
 // The block's partial product is scaled by its fp32 scale_inv (wave-uniform:
 // a 16-row tile never straddles a 128-row scale block) and added to an fp32
-// accumulator, so the weight is never materialised.  The four waves of a
-// workgroup split the K blocks and reduce through LDS; when K is long the grid
-// also splits K and the last workgroup of a tile (atomic counter) sums the
-// fp32 partials in a fixed order, so results are deterministic.
+// accumulator, so the weight is never materialised.  The 4-16 waves of a
+// workgroup split the K blocks and reduce through LDS in a fixed order, so
+// results are deterministic and no workgroup waits on another (a split of K
+// across workgroups would need device-scope release fences, which write back
+// the per-XCD L2s and cost more than they save).
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -135,14 +136,15 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
 
 // ---------------------------------------------------------------- skinny GEMM
 
-template <int RT, int MT, int MODE>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int kb_per_split) {
+// Workgroup = NW waves over one group of RT 16-row tiles; wave w takes the
+// K blocks kb = w, w + NW, ...; partials reduce through LDS in wave order, so
+// results are deterministic and no workgroup depends on another.
+template <int RT, int MT, int NW, int MODE>
+__global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvParams p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int tile0 = blockIdx.x * RT;
   const int KB = p.K >> 7;
-  const int kb0 = blockIdx.y * kb_per_split;
-  const int kb1 = min(kb0 + kb_per_split, KB);
 
   const uint8_t *wrow[RT];
   const float *srow[RT];
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int kb_per_spli
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int kb = kb0 + wave; kb < kb1; kb += 4) {
+  for (int kb = wave; kb < KB; kb += NW) {
     u32x4 a0[RT], a1[RT];
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
@@ -210,81 +212,54 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int kb_per_spli
     }
   }
 
-  __shared__ f32x4 red[4][RT * MT][64];
+  __shared__ f32x4 red[NW][RT * MT][64];
 #pragma unroll
   for (int r = 0; r < RT; ++r)
 #pragma unroll
     for (int t = 0; t < MT; ++t) red[wave][r * MT + t][lane] = acc[r][t];
   __syncthreads();
-
-  const bool split = gridDim.y > 1;
-  for (int idx = threadIdx.x; idx < RT * MT * 64; idx += 256) {
+  for (int idx = threadIdx.x; idx < RT * MT * 64; idx += NW * 64) {
     const int rt = idx >> 6, ln = idx & 63;
     const int r = rt / MT, t = rt % MT;
     const int m = t * 16 + (ln & 15);
     const int n = (tile0 + r) * 16 + 4 * (ln >> 4);
     if (m >= p.M || n >= p.N) continue;
-    f32x4 v = red[0][rt][ln] + red[1][rt][ln] + red[2][rt][ln] + red[3][rt][ln];
-    if (!split)
-      store4<MODE>(p, m, n, v);
-    else
-      *reinterpret_cast<f32x4 *>(p.ws + ((size_t)blockIdx.y * p.M + m) * p.N + n) = v;
-  }
-  if (!split) return;
-
-  // Split-K: the last workgroup of this row group sums the partials in order.
-  __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(&p.counters[blockIdx.x], 1u);
-    s_last = (prev == gridDim.y - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  for (int idx = threadIdx.x; idx < RT * MT * 64; idx += 256) {
-    const int rt = idx >> 6, ln = idx & 63;
-    const int r = rt / MT, t = rt % MT;
-    const int m = t * 16 + (ln & 15);
-    const int n = (tile0 + r) * 16 + 4 * (ln >> 4);
-    if (m >= p.M || n >= p.N) continue;
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    for (int ks = 0; ks < (int)gridDim.y; ++ks)
-      v += __builtin_nontemporal_load(
-          reinterpret_cast<const f32x4 *>(p.ws + ((size_t)ks * p.M + m) * p.N + n));
+    f32x4 v = red[0][rt][ln];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += red[w][rt][ln];
     store4<MODE>(p, m, n, v);
   }
-  if (threadIdx.x == 0) p.counters[blockIdx.x] = 0u;
 }
 
 GemvPlan plan_gemv(int M, int N, int K) {
   GemvPlan pl;
   const int tiles = (N + 15) / 16;
   const int KB = K / 128;
-  pl.rt = (M <= 4) ? 1 : 2;
-  pl.groups = (tiles + pl.rt - 1) / pl.rt;
-  pl.ks = 1;
-  while ((int64_t)pl.groups * pl.ks < 1024 && KB / (pl.ks * 2) >= 8) pl.ks *= 2;
-  pl.kb_per_split = (KB + pl.ks - 1) / pl.ks;
-  pl.ks = (KB + pl.kb_per_split - 1) / pl.kb_per_split;
   const int MT = (M + 15) / 16;
-  pl.partial_bytes = pl.ks > 1 ? align_up((size_t)pl.ks * MT * 16 * N * sizeof(float), 256) : 0;
-  pl.counter_count = pl.ks > 1 ? (size_t)pl.groups : 0;
+  pl.nw = KB >= 48 ? 16 : (KB >= 24 ? 8 : 4);
+  // two row tiles per wave halve the x traffic once there are enough rows
+  pl.rt = (M > 4 && tiles >= 2 * 256) ? 2 : 1;
+  while (pl.nw * pl.rt * (MT > 2 ? 4 : MT) > 64) pl.nw /= 2;
+  pl.groups = (tiles + pl.rt - 1) / pl.rt;
   return pl;
 }
 
-size_t gemv_ws_bytes(const GemvPlan &pl) { return pl.ks > 1 ? COUNTER_BYTES + pl.partial_bytes : 0; }
+template <int RT, int MT, int NW>
+static void launch_cfg(const GemvParams &p, int mode, const GemvPlan &pl, hipStream_t st) {
+  dim3 grid(pl.groups);
+  switch (mode) {
+    case GEMV_PLAIN: gemv_kernel<RT, MT, NW, GEMV_PLAIN><<<grid, NW * 64, 0, st>>>(p); break;
+    case GEMV_RESID: gemv_kernel<RT, MT, NW, GEMV_RESID><<<grid, NW * 64, 0, st>>>(p); break;
+    case GEMV_QKVA: gemv_kernel<RT, MT, NW, GEMV_QKVA><<<grid, NW * 64, 0, st>>>(p); break;
+    default: gemv_kernel<RT, MT, NW, GEMV_QROPE><<<grid, NW * 64, 0, st>>>(p); break;
+  }
+}
 
 template <int RT, int MT>
 static void launch_rt_mt(const GemvParams &p, int mode, const GemvPlan &pl, hipStream_t st) {
-  dim3 grid(pl.groups, pl.ks);
-  switch (mode) {
-    case GEMV_PLAIN: gemv_kernel<RT, MT, GEMV_PLAIN><<<grid, 256, 0, st>>>(p, pl.kb_per_split); break;
-    case GEMV_RESID: gemv_kernel<RT, MT, GEMV_RESID><<<grid, 256, 0, st>>>(p, pl.kb_per_split); break;
-    case GEMV_QKVA: gemv_kernel<RT, MT, GEMV_QKVA><<<grid, 256, 0, st>>>(p, pl.kb_per_split); break;
-    default: gemv_kernel<RT, MT, GEMV_QROPE><<<grid, 256, 0, st>>>(p, pl.kb_per_split); break;
-  }
+  if (pl.nw == 16) launch_cfg<RT, MT, 16>(p, mode, pl, st);
+  else if (pl.nw == 8) launch_cfg<RT, MT, 8>(p, mode, pl, st);
+  else launch_cfg<RT, MT, 4>(p, mode, pl, st);
 }
 
 template <int RT>
@@ -299,10 +274,6 @@ int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t 
   if (p0.M < 1 || p0.M > 64) return fail(AMLA_EINVAL, "skinny fp8 GEMM needs 1 <= M <= 64 (got %d)", p0.M);
   if (p0.N % 16 || p0.K % 128)
     return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM needs N %% 16 == 0 and K %% 128 == 0 (N=%d K=%d)", p0.N, p0.K);
-  if (pl.ks > 1 && (!p0.ws || !p0.counters))
-    return fail(AMLA_EWORKSPACE, "split-K GEMM needs partial and counter workspace");
-  if (pl.counter_count > (size_t)COUNTERS_PER_SLOT)
-    return fail(AMLA_EUNSUPPORTED, "split-K GEMM: %zu tile counters exceed a slot", pl.counter_count);
   if (pl.rt == 1) launch_rt<1>(p0, mode, pl, st);
   else launch_rt<2>(p0, mode, pl, st);
   return check_launch("fp8 skinny GEMM");
@@ -391,9 +362,8 @@ int amla_fp8_block_dequant(const void *weight, const float *scale_inv, int64_t n
 }
 
 size_t amla_fp8_linear_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-  if (m <= 0 || n <= 0 || k <= 0) return 0;
-  if (m > 64) return gemm_ws_bytes((int)m, (int)n, (int)k);
-  return gemv_ws_bytes(plan_gemv((int)m, (int)n, (int)k));
+  (void)m; (void)n; (void)k;
+  return 0;
 }
 
 int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void *weight,
@@ -409,9 +379,6 @@ int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void
                 "fp8_linear: needs n %% 16 == 0, k %% 128 == 0, ldx %% 8 == 0, ldy %% 4 == 0 and 16-byte "
                 "aligned x/weight (n=%lld k=%lld)",
                 (long long)n, (long long)k);
-  const size_t need = amla_fp8_linear_workspace_bytes(m, n, k);
-  if (need > workspace_bytes || (need && !workspace))
-    return fail(AMLA_EWORKSPACE, "fp8_linear: workspace %zu bytes < %zu needed", workspace_bytes, need);
   GemvParams p = {};
   p.x = reinterpret_cast<const uint16_t *>(x);
   p.M = (int)m;
@@ -423,16 +390,12 @@ int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void
   p.n_split = (int)n;
   p.y = reinterpret_cast<uint16_t *>(y);
   p.ldy = (int)ldy;
+  p.seq_len = 1;
+  (void)workspace;
+  (void)workspace_bytes;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (m > 64) return launch_gemm(p, GEMV_PLAIN, st);
-  const GemvPlan pl = plan_gemv((int)m, (int)n, (int)k);
-  if (pl.ks > 1) {
-    if (pl.counter_count > (size_t)COUNTERS_PER_SLOT)
-      return fail(AMLA_EUNSUPPORTED, "fp8_linear: %zu split-K tiles exceed a counter slot", pl.counter_count);
-    p.counters = counter_slot(workspace, 0);
-    p.ws = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) + COUNTER_BYTES);
-  }
-  return launch_gemv(p, GEMV_PLAIN, pl, st);
+  return launch_gemv(p, GEMV_PLAIN, plan_gemv((int)m, (int)n, (int)k), st);
 }
 
 int amla_rms_norm(const void *x, int64_t rows, int64_t dim, int64_t ldx, const void *gamma, float eps,

@@ -36,8 +36,6 @@ constexpr int HEADS = 128;
 constexpr int NOPE = 128;
 constexpr int VD = 128;
 constexpr int TT = 32;               // cache rows per tile
-constexpr int KT_STRIDE = QKD + 8;   // bf16 elements per t-major LDS row (16 B pad)
-constexpr int CT_STRIDE = TT + 4;    // bf16 elements per latent-major LDS row (8 B pad)
 
 // ---------------------------------------------------------------- absorb
 
@@ -118,43 +116,62 @@ struct AttnParams {
   int splits, tiles_per_split;
   float scale_log2;  // softmax scale * log2(e)
   float eps;
-  float *part_o;   // (B, splits, H, 512) unnormalised sum_t p r_t c_t
-  float *part_ml;  // (B, splits, H, 2) running max (log2 units) and sum of p
+  float *part_o;   // (B, splits, H, 512) sum_t p_t r_t c_t, p relative to the split's reference max
+  float *part_ml;  // (B, splits, H, 2) reference max (log2 units) and sum of p; sum < 0 marks a
+                   // (split, head) whose scores overflowed the reference (recomputed by the combine)
 };
 
-struct TileRegs {
-  u32x4 c[4][2];  // 4 rows x 16 latent values
-  u32x4 k;        // 8 rope values of one row
-  f32x4 cs[2];    // 4 (cos, sin) pairs
-};
+// LDS: a ring of NST stages, each one tile of TT cache rows
+//   K   [TT][KROW] bf16: raw latent row (DMA) | rotated rope key (written after DMA)
+//   raw [TT][64]   bf16: raw rope keys (DMA)
+// plus one (cos, sin) table block for the tile being prepared and the rope
+// part of the 128 head queries (B operand of the rope K steps).
+constexpr int NST = 3;
+constexpr int KROW = QKD + 8;  // 1168 B rows: the 16 B pad spreads 16 rows over all LDS banks
+constexpr int K_BYTES = TT * KROW * 2;
+constexpr int RAW_BYTES = TT * ROPE * 2;
+constexpr int STAGE_BYTES = K_BYTES + RAW_BYTES;
+constexpr int TAB_OFF = NST * STAGE_BYTES;
+constexpr int TAB_BYTES = TT * ROPE * 4;
+constexpr int QPE_OFF = TAB_OFF + TAB_BYTES;
+constexpr int QPE_BYTES = HEADS * ROPE * 2;
+constexpr int ATTN_LDS_BYTES = QPE_OFF + QPE_BYTES;
+constexpr int TILE_DMA = 9;   // copies per wave per tile: 8 latent rows + 1 block of rope keys
+constexpr float REF_HEADROOM = 64.f;      // p = 2^(s - m_ref) <= 2^64: no overflow anywhere
 
-// Thread roles in the loader: rows 4*rg .. 4*rg+3, latent columns 16*cg .. +15;
-// rope key row tid/8, pairs 4*(tid%8) .. +3.
-AMLA_DEV void load_tile(const AttnParams &p, int b, int t0, int T, TileRegs &R) {
-  const int tid = threadIdx.x;
-  const int rg = tid >> 5, cg = tid & 31;
-  const uint16_t *cbase = p.ckv + (size_t)b * p.ckv_bstride;
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
+
+// Wave w copies rows 8w .. 8w+7 of the tile straight into LDS (no VGPRs):
+// every global_load_lds_dwordx4 writes 64 lanes x 16 B contiguously at its
+// LDS base.  Row indices are wave-uniform (scalar bases, one lane offset).
+// Rows past the context re-read row T-1 (in bounds; their scores are masked).
+AMLA_DEV void dma_rows(const AttnParams &p, int b, int tile, int T, uint8_t *stage, int wave, int lane) {
+  const int t0 = tile * TT + wave * 8;
+  const char *cb = reinterpret_cast<const char *>(p.ckv + (size_t)b * p.ckv_bstride);
+  int voff;
+  asm volatile("v_lshlrev_b32 %0, 4, %1" : "=v"(voff) : "v"(lane));  // lane * 16, kept out of loop-invariant hoisting
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int t = t0 + rg * 4 + r;
-    if (t < T) {
-      const uint16_t *src = cbase + (size_t)t * LORA + cg * 16;
-      R.c[r][0] = ldg16_nt(src);
-      R.c[r][1] = ldg16_nt(src + 8);
-    } else {
-      R.c[r][0] = R.c[r][1] = u32x4{0, 0, 0, 0};
-    }
+  for (int r = 0; r < 8; ++r) {
+    const int t = min(t0 + r, T - 1);
+    __builtin_amdgcn_global_load_lds(cb + (size_t)t * (LORA * 2) + voff, LDS_PTR(stage + (wave * 8 + r) * (KROW * 2)),
+                                     16, 0, 0);
   }
-  const int kt = t0 + (tid >> 3);
-  const int kq = tid & 7;
-  if (kt < T) {
-    R.k = ldg16_nt(p.kpe + (size_t)b * p.kpe_bstride + (size_t)kt * ROPE + kq * 8);
-    const f32x4 *tab = reinterpret_cast<const f32x4 *>(p.rope_table + ((size_t)kt * (ROPE / 2) + kq * 4) * 2);
-    R.cs[0] = tab[0];
-    R.cs[1] = tab[1];
-  } else {
-    R.k = u32x4{0, 0, 0, 0};
-    R.cs[0] = R.cs[1] = f32x4{1.f, 0.f, 1.f, 0.f};
+  const int last = T - 1 - t0;
+  const char *kb = reinterpret_cast<const char *>(p.kpe + (size_t)b * p.kpe_bstride) + (size_t)t0 * (ROPE * 2);
+  const int off = min(lane >> 3, last) * (ROPE * 2) + (lane & 7) * 16;
+  __builtin_amdgcn_global_load_lds(kb + off, LDS_PTR(stage + K_BYTES + wave * 1024), 16, 0, 0);
+}
+
+// (cos, sin) of the 8 rows wave w rotates: 8 x 256 B in two copies.
+AMLA_DEV void dma_table(const AttnParams &p, int tile, int T, uint8_t *smem, int wave, int lane) {
+  const int t0 = tile * TT + wave * 8;
+  const int last = T - 1 - t0;
+  const char *tb = reinterpret_cast<const char *>(p.rope_table) + (size_t)t0 * (ROPE * 4);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = j * 64 + lane;
+    const int off = min(e >> 4, last) * (ROPE * 4) + (e & 15) * 16;
+    __builtin_amdgcn_global_load_lds(tb + off, LDS_PTR(smem + TAB_OFF + wave * 2048 + j * 1024), 16, 0, 0);
   }
 }
 
@@ -163,129 +180,173 @@ AMLA_DEV uint32_t rot_pair(uint32_t x, float c, float s) {
   return pack_bf16(__fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s)), __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c)));
 }
 
-AMLA_DEV void store_tile(const AttnParams &p, const TileRegs &R, uint16_t *kt, uint16_t *ct, float *rs) {
-  const int tid = threadIdx.x;
-  const int rg = tid >> 5, cg = tid & 31;
-  // t-major copy and per-row sum of squares
-  float ss[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int t = rg * 4 + r;
-    u32x4 *dst = reinterpret_cast<u32x4 *>(kt + t * KT_STRIDE + cg * 16);
-    dst[0] = R.c[r][0];
-    dst[1] = R.c[r][1];
-    float a = 0.f;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float x0 = lo_bf(R.c[r][h][q]), x1 = hi_bf(R.c[r][h][q]);
-        a += x0 * x0 + x1 * x1;
-      }
-    ss[r] = a;
-  }
-  // reduce over the 32 column groups of the same rows (lanes 0-31 / 32-63)
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) ss[r] += __shfl_xor(ss[r], o, 64);
-  }
-  if (cg == 0) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) rs[rg * 4 + r] = rsqrtf(ss[r] * (1.f / LORA) + p.eps);
-  }
-  // latent-major (transposed) copy: column c holds rows 4rg .. 4rg+3
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t d0 = R.c[0][h][q], d1 = R.c[1][h][q], d2 = R.c[2][h][q], d3 = R.c[3][h][q];
-      const int c = cg * 16 + h * 8 + q * 2;
-      u32x2 even = {__builtin_amdgcn_perm(d1, d0, 0x05040100u), __builtin_amdgcn_perm(d3, d2, 0x05040100u)};
-      u32x2 odd = {__builtin_amdgcn_perm(d1, d0, 0x07060302u), __builtin_amdgcn_perm(d3, d2, 0x07060302u)};
-      *reinterpret_cast<u32x2 *>(ct + c * CT_STRIDE + rg * 4) = even;
-      *reinterpret_cast<u32x2 *>(ct + (c + 1) * CT_STRIDE + rg * 4) = odd;
-    }
-  // rotated rope key (fp32 rotation rounded to bf16, as inference/ops.py:97)
-  const int krow = tid >> 3, kq = tid & 7;
-  u32x4 kr;
-  kr.x = rot_pair(R.k.x, R.cs[0].x, R.cs[0].y);
-  kr.y = rot_pair(R.k.y, R.cs[0].z, R.cs[0].w);
-  kr.z = rot_pair(R.k.z, R.cs[1].x, R.cs[1].y);
-  kr.w = rot_pair(R.k.w, R.cs[1].z, R.cs[1].w);
-  *reinterpret_cast<u32x4 *>(kt + krow * KT_STRIDE + LORA + kq * 8) = kr;
+// Wave w rotates the rope keys of the rows it copied (fp32 rotation rounded to
+// bf16, as inference/ops.py:93-97) into the K rows of the stage.
+AMLA_DEV void rotate_own_rows(uint8_t *stage, const uint8_t *smem, int wave, int lane) {
+  const int row = wave * 8 + (lane >> 3), q = lane & 7;
+  const u32x4 raw = *reinterpret_cast<const u32x4 *>(stage + K_BYTES + row * (ROPE * 2) + q * 16);
+  const f32x4 c0 = *reinterpret_cast<const f32x4 *>(smem + TAB_OFF + row * (ROPE * 4) + q * 32);
+  const f32x4 c1 = *reinterpret_cast<const f32x4 *>(smem + TAB_OFF + row * (ROPE * 4) + q * 32 + 16);
+  u32x4 r;
+  r.x = rot_pair(raw.x, c0.x, c0.y);
+  r.y = rot_pair(raw.y, c0.z, c0.w);
+  r.z = rot_pair(raw.z, c1.x, c1.y);
+  r.w = rot_pair(raw.w, c1.z, c1.w);
+  *reinterpret_cast<u32x4 *>(stage + row * (KROW * 2) + (LORA + q * 8) * 2) = r;
 }
 
-// Grid (splits, B), 256 threads.  Wave w owns heads 32w .. 32w+31 for the
-// whole tile: S^T = K_tile (32 x 576) . Q^T (576 x 32 heads) with the rows of
-// the tile as the MFMA M dimension, so each lane ends with 8 scores of one
-// head; those are exactly the B operand of O^T += C^T (512 x 32) . P^T, so the
-// probabilities never leave registers.  O^T (512 x 32 heads, fp32) lives in
-// 256 accumulator registers per lane.
+template <int N>
+AMLA_DEV void wait_vmcnt() {
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
+}
+
+AMLA_DEV float dot2_bf16(uint32_t a, float acc) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 v = __builtin_bit_cast(bf16x2, a);
+  return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
+}
+
+// Grid (splits, B), 256 threads, one workgroup per CU (~145 KB of LDS).
+// Wave w owns heads 32w .. 32w+31.  Per tile of 32 cache rows:
+//   S^T (t x head) = K_tile (32 x 576) . Q^T with the tile rows as the MFMA M
+//     dimension, so each lane ends with 8 scores of one head (its column);
+//   r_t = rsqrt(mean(c_t^2) + eps) from the same A fragments (v_dot2), moved
+//     to the C layout with lane permutes and applied between the latent and the
+//     rope K steps (one accumulator set);
+//   p = 2^(s - m_ref): m_ref is the head's max over the split's first tile and
+//     stays fixed, so O^T is only ever touched by MFMA (no rescaling); a head
+//     whose later tile exceeds m_ref by REF_HEADROOM is flagged instead;
+//   O^T (512 x 32 heads, fp32) += C^T (512 x t) . P^T, C^T from a latent-major
+//     copy of the tile, P^T = the score registers (p * r_t as bf16).
+// Registers: O^T takes 256 accumulators, the latent query fragments 128; the
+// loop must not spill (a scratch reload would wait for every copy in flight),
+// which is why the copies use scalar bases and there is no rescaling path.
 __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   const int split = blockIdx.x, b = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
   const int T = p.pos[b] + 1;
   const int ntiles = (T + TT - 1) / TT;
   const int tb = split * p.tiles_per_split;
   const int te = min(tb + p.tiles_per_split, ntiles);
-
   extern __shared__ __align__(16) uint8_t smem[];
-  // [kt 0 | kt 1 | ct 0 | ct 1 | rs 0 | rs 1]
-  uint16_t *const kt_base = reinterpret_cast<uint16_t *>(smem);
-  uint16_t *const ct_base = kt_base + 2 * TT * KT_STRIDE;
-  float *const rs_base = reinterpret_cast<float *>(ct_base + 2 * LORA * CT_STRIDE);
-
   const int head0 = wave * 32;
-  // query fragments (B operand): lane holds Q[head][ks*32 + 8*lg .. +7]
-  bf16x8 qf[2][QKD / 32];
+
+  // rope half of this wave's 32 head queries -> LDS (read back by the same wave)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = j * 64 + lane, hh = e >> 3, q = e & 7;
+    *reinterpret_cast<u32x4 *>(smem + QPE_OFF + ((head0 + hh) * ROPE + q * 8) * 2) =
+        ldg16(p.qbuf + ((size_t)b * HEADS + head0 + hh) * QKD + LORA + q * 8);
+  }
+  // latent query fragments (B operand: head = column l%16, K = 8*lg .. of each 32-wide step)
+  bf16x8 qf[2][LORA / 32];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const uint16_t *qr = p.qbuf + ((size_t)b * HEADS + head0 + nt * 16 + li) * QKD + 8 * lg;
 #pragma unroll
-    for (int ks = 0; ks < QKD / 32; ++ks) qf[nt][ks] = as_bf16x8(ldg16(qr + ks * 32));
+    for (int ks = 0; ks < LORA / 32; ++ks) {
+      qf[nt][ks] = as_bf16x8(ldg16(qr + ks * 32));
+    }
   }
 
   f32x4 o[LORA / 16][2];
 #pragma unroll
   for (int mt = 0; mt < LORA / 16; ++mt) o[mt][0] = o[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  float m_ref[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  bool bad[2] = {false, false};
 
   if (tb < te) {
-    TileRegs R;
-    load_tile(p, b, tb * TT, T, R);
-    store_tile(p, R, kt_base, ct_base, rs_base);
+    dma_table(p, tb, T, smem, wave, lane);
+    dma_rows(p, b, tb, T, smem, wave, lane);
+    if (tb + 1 < te) {
+      dma_rows(p, b, tb + 1, T, smem + STAGE_BYTES, wave, lane);
+      wait_vmcnt<TILE_DMA>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    rotate_own_rows(smem, smem, wave, lane);
     __syncthreads();
+    bool have_ref = false;
     for (int tile = tb; tile < te; ++tile) {
-      const int buf = (tile - tb) & 1;
-      const bool more = tile + 1 < te;
-      const uint16_t *K = kt_base + buf * (TT * KT_STRIDE);
-      const uint16_t *C = ct_base + buf * (LORA * CT_STRIDE);
-      const float *RS = rs_base + buf * TT;
+      const int it = tile - tb;
+      uint8_t *const cur = smem + (it % NST) * STAGE_BYTES;
+      // the table block only ever holds this wave's rows: no barrier needed
+      if (tile + 1 < te) dma_table(p, tile + 1, T, smem, wave, lane);
+      if (tile + 2 < te) dma_rows(p, b, tile + 2, T, smem + ((it + 2) % NST) * STAGE_BYTES, wave, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint16_t *K = reinterpret_cast<const uint16_t *>(cur);
 
-      // ---- scores: S^T (t x head)
-      f32x4 sl[2][2], sp[2][2];
+      // ---- latent K steps: S^T and row sums of squares, one A fragment step ahead
+      f32x4 sc[2][2];
+      float ssq[2] = {0.f, 0.f};
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) sl[mt][nt] = sp[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < 2; ++nt) sc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      u32x4 acur[2], anext[2];
 #pragma unroll
-      for (int ks = 0; ks < QKD / 32; ++ks) {
+      for (int mt = 0; mt < 2; ++mt) acur[mt] = *reinterpret_cast<const u32x4 *>(K + (mt * 16 + li) * KROW + 8 * lg);
+#pragma unroll
+      for (int ks = 0; ks < LORA / 32; ++ks) {
+        if (ks + 1 < LORA / 32) {
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+            anext[mt] = *reinterpret_cast<const u32x4 *>(K + (mt * 16 + li) * KROW + (ks + 1) * 32 + 8 * lg);
+        }
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-          const bf16x8 a = as_bf16x8(
-              *reinterpret_cast<const u32x4 *>(K + (mt * 16 + li) * KT_STRIDE + ks * 32 + 8 * lg));
+          ssq[mt] = dot2_bf16(acur[mt].x, ssq[mt]);
+          ssq[mt] = dot2_bf16(acur[mt].y, ssq[mt]);
+          ssq[mt] = dot2_bf16(acur[mt].z, ssq[mt]);
+          ssq[mt] = dot2_bf16(acur[mt].w, ssq[mt]);
+          const bf16x8 a = as_bf16x8(acur[mt]);
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt) {
-            if (ks < LORA / 32) sl[mt][nt] = mfma16(a, qf[nt][ks], sl[mt][nt]);
-            else sp[mt][nt] = mfma16(a, qf[nt][ks], sp[mt][nt]);
+            sc[mt][nt] = mfma16(a, qf[nt][ks], sc[mt][nt]);
+          }
+        }
+        asm volatile("" ::: "memory");
+        acur[0] = anext[0];
+        acur[1] = anext[1];
+      }
+      // ---- r_t: full sum for row mt*16+li (4 lane groups), then to the C
+      // layout (lane (head, lg) holds rows mt*16 + 4*lg + r) and applied
+      float rc[2][4];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        float v = ssq[mt];
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        const float rrow = rsqrtf(v * (1.f / LORA) + p.eps);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rc[mt][r] = __shfl(rrow, 4 * lg + r, 64);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[mt][nt][r] *= rc[mt][r];
+      }
+      // ---- rope K steps: rotated keys (K columns 512..575) x rope queries (LDS)
+#pragma unroll
+      for (int kk = 0; kk < ROPE / 32; ++kk) {
+        bf16x8 qp[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          qp[nt] = *reinterpret_cast<const bf16x8 *>(smem + QPE_OFF + ((head0 + nt * 16 + li) * ROPE + kk * 32 + 8 * lg) * 2);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8 *>(K + (mt * 16 + li) * KROW + LORA + kk * 32 + 8 * lg);
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            sc[mt][nt] = mfma16(a, qp[nt], sc[mt][nt]);
           }
         }
       }
-      // next tile's rows are fetched while softmax and P.V run
-      if (more) load_tile(p, b, (tile + 1) * TT, T, R);
-      // ---- online softmax per head (column); lane holds t = mt*16 + 4*lg + r
+      __builtin_amdgcn_sched_barrier(0);
+
+      // ---- probabilities relative to the head's fixed reference max
       const int tbase = tile * TT;
       bf16x8 pf[2];
 #pragma unroll
@@ -297,48 +358,80 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int tl = mt * 16 + 4 * lg + r;
-            float v = p.scale_log2 * (RS[tl] * sl[mt][nt][r] + sp[mt][nt][r]);
-            v = (tbase + tl < T) ? v : -INFINITY;
+            const float v = (tbase + tl < T) ? p.scale_log2 * sc[mt][nt][r] : -INFINITY;
             sv[mt * 4 + r] = v;
             mx = fmaxf(mx, v);
           }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run[nt], mx);
-        const float alpha = (m_run[nt] == -INFINITY) ? 0.f : exp2f(m_run[nt] - m_new);
-        float lsum = 0.f;
+        if (!have_ref) m_ref[nt] = mx;
+        bad[nt] = bad[nt] || (mx > m_ref[nt] + REF_HEADROOM);
         float pv[8];
+        float lsum = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float pe = (sv[e] == -INFINITY) ? 0.f : exp2f(sv[e] - m_new);
+          const float pe = (sv[e] == -INFINITY) ? 0.f : exp2f(sv[e] - m_ref[nt]);
           lsum += pe;
-          const int tl = (e >> 2) * 16 + 4 * lg + (e & 3);
-          pv[e] = pe * RS[tl];
+          pv[e] = pe * rc[e >> 2][e & 3];
         }
-        l_run[nt] = l_run[nt] * alpha + lsum;
-        m_run[nt] = m_new;
-        if (__any(alpha != 1.f)) {
-#pragma unroll
-          for (int mt = 0; mt < LORA / 16; ++mt) o[mt][nt] *= alpha;
-        }
-        u32x4 pk = {pack_bf16(pv[0], pv[1]), pack_bf16(pv[2], pv[3]), pack_bf16(pv[4], pv[5]),
-                    pack_bf16(pv[6], pv[7])};
+        l_run[nt] += lsum;
+        const u32x4 pk = {pack_bf16(pv[0], pv[1]), pack_bf16(pv[2], pv[3]), pack_bf16(pv[4], pv[5]),
+                          pack_bf16(pv[6], pv[7])};
         pf[nt] = as_bf16x8(pk);
       }
-      // ---- O^T (latent x head) += C^T (latent x t) . P^T (t x head)
+      have_ref = true;
+      __builtin_amdgcn_sched_barrier(0);
+
+      // ---- O^T (latent x head) += C^T (latent x t) . P^T (t x head); C^T by
+      // transpose reads: within a 16-lane group, lane s addresses row
+      // t0 + s/4, columns c0 + 4(s%4) .. +3 and lane L receives
+      // C[t0 .. t0+3][c0 + L]; t0 = 4*lg and 16 + 4*lg match P^T's rows.
+      {
+        // The transpose reads are issued as inline asm: the builtin makes the
+        // compiler wait for every LDS-DMA copy in flight (vmcnt(0)) before the
+        // first read, which would drain the prefetch of the tile after next.
+        // Ordering against the DMA and rotation writes to this stage is
+        // already given by the explicit vmcnt waits and the tile barrier.
+        const int s16 = lane & 15;
+        const uint32_t a0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+            (__attribute__((address_space(3))) const uint16_t *)(K + (4 * lg + (s16 >> 2)) * KROW + 4 * (s16 & 3))));
+        u32x2 t0[2], t1[2];
+        // The reads complete asynchronously: each wait names the registers it
+        // guards as in/out operands, so no use of them is scheduled before it;
+        // outputs are early-clobber (two reads share the address register).
+#define AMLA_TR(dst0, dst1, MT)                                                                            \
+  asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"               \
+               : "=&v"(dst0), "=&v"(dst1)                                                                \
+               : "v"(a0), "i"((MT) * 32), "i"((MT) * 32 + 16 * KROW * 2))
+        AMLA_TR(t0[0], t1[0], 0);
 #pragma unroll
-      for (int mt = 0; mt < LORA / 16; ++mt) {
-        const uint16_t *cr = C + (mt * 16 + li) * CT_STRIDE + 4 * lg;
-        const u32x2 lo = *reinterpret_cast<const u32x2 *>(cr);
-        const u32x2 hi = *reinterpret_cast<const u32x2 *>(cr + 16);
-        const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
-        o[mt][0] = mfma16(a, pf[0], o[mt][0]);
-        o[mt][1] = mfma16(a, pf[1], o[mt][1]);
+        for (int mt = 0; mt < LORA / 16; ++mt) {
+          const int c = mt & 1, n = c ^ 1;
+          if (mt + 1 < LORA / 16) {
+            AMLA_TR(t0[n], t1[n], mt + 1);
+            asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
+          } else {
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
+          }
+          const bf16x8 a = as_bf16x8(u32x4{t0[c].x, t0[c].y, t1[c].x, t1[c].y});
+          o[mt][0] = mfma16(a, pf[0], o[mt][0]);
+          o[mt][1] = mfma16(a, pf[1], o[mt][1]);
+        }
+#undef AMLA_TR
       }
-      if (more)
-        store_tile(p, R, kt_base + (buf ^ 1) * (TT * KT_STRIDE), ct_base + (buf ^ 1) * (LORA * CT_STRIDE),
-                   rs_base + (buf ^ 1) * TT);
-      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+
+      // ---- next tile: own rows and table landed -> rotate their rope keys
+      if (tile + 1 < te) {
+        if (tile + 2 < te) wait_vmcnt<TILE_DMA>();
+        else wait_vmcnt<0>();
+        rotate_own_rows(smem + ((it + 1) % NST) * STAGE_BYTES, smem, wave, lane);
+      }
+      // barrier without a memory fence: a fence would also wait for the copy
+      // of the tile after next; LDS writes (rotated keys) are drained by hand
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
     }
   }
 
@@ -351,8 +444,8 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
     const int head = head0 + nt * 16 + li;
     const size_t row = ((size_t)b * p.splits + split) * HEADS + head;
     if (lg == 0) {
-      p.part_ml[row * 2] = m_run[nt];
-      p.part_ml[row * 2 + 1] = l;
+      p.part_ml[row * 2] = m_ref[nt];
+      p.part_ml[row * 2 + 1] = bad[nt] ? -1.f : l;
     }
     float *dst = p.part_o + row * LORA + 4 * lg;
 #pragma unroll
@@ -360,47 +453,118 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   }
 }
 
-constexpr size_t ATTN_LDS = (size_t)2 * TT * KT_STRIDE * 2 + (size_t)2 * LORA * CT_STRIDE * 2 + 2 * TT * 4;
+constexpr size_t ATTN_LDS = ATTN_LDS_BYTES;
 
 // ---------------------------------------------------------------- combine + W_UV
 
-// Grid (H, B): blockIdx.x = head so consecutive workgroups of one head (same
-// XCD, shared L2) reuse its W_UV rows across the batch.
-__global__ __launch_bounds__(256) void combine_uv_kernel(const float *__restrict__ part_o,
-                                                         const float *__restrict__ part_ml, int splits,
-                                                         const uint8_t *__restrict__ wkvb,
+AMLA_DEV float block_reduce(float v, float *red, bool is_max) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = is_max ? wave_max(v) : wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return is_max ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) : (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Exact online-softmax recomputation of one (split, head) in fp32, used only
+// for heads attn_kernel flagged (a score more than REF_HEADROOM above the
+// split's reference max).  Thread tid owns latent columns tid and tid+256.
+AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, int split, float *qs, float *ps, float *red,
+                              float &m_out, float &l_out, float &o0, float &o1) {
+  const int tid = threadIdx.x;
+  const int T = p.pos[b] + 1;
+  const int t0 = split * p.tiles_per_split * TT;
+  const int t1 = min(t0 + p.tiles_per_split * TT, T);
+  __syncthreads();
+  for (int c = tid; c < QKD; c += 256) qs[c] = bf2f(p.qbuf[((size_t)b * HEADS + h) * QKD + c]);
+  __syncthreads();
+  const uint16_t *cb = p.ckv + (size_t)b * p.ckv_bstride;
+  const uint16_t *kb = p.kpe + (size_t)b * p.kpe_bstride;
+  float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int c0 = t0; c0 < t1; c0 += 256) {
+    const int t = c0 + tid;
+    float sv = -INFINITY, rt = 0.f;
+    if (t < t1) {
+      const uint16_t *row = cb + (size_t)t * LORA;
+      float ss = 0.f, dl = 0.f;
+      for (int c = 0; c < LORA; ++c) {
+        const float x = bf2f(row[c]);
+        ss += x * x;
+        dl += x * qs[c];
+      }
+      float dp = 0.f;
+      for (int i = 0; i < ROPE / 2; ++i) {
+        const uint32_t kv = *reinterpret_cast<const uint32_t *>(kb + (size_t)t * ROPE + 2 * i);
+        const float cs = p.rope_table[((size_t)t * (ROPE / 2) + i) * 2];
+        const float sn = p.rope_table[((size_t)t * (ROPE / 2) + i) * 2 + 1];
+        const uint32_t rk = rot_pair(kv, cs, sn);
+        dp += lo_bf(rk) * qs[LORA + 2 * i] + hi_bf(rk) * qs[LORA + 2 * i + 1];
+      }
+      rt = rsqrtf(ss * (1.f / LORA) + p.eps);
+      sv = p.scale_log2 * (rt * dl + dp);
+    }
+    const float mc = block_reduce(sv, red, true);
+    const float Mn = fmaxf(M, mc);
+    const float f = (M == -INFINITY) ? 0.f : exp2f(M - Mn);
+    const float pe = (sv == -INFINITY) ? 0.f : exp2f(sv - Mn);
+    ps[tid] = pe * rt;
+    const float ls = block_reduce(pe, red, false);
+    L = L * f + ls;
+    a0 *= f;
+    a1 *= f;
+    M = Mn;
+    const int n = min(256, t1 - c0);
+    for (int j = 0; j < n; ++j) {
+      const float w = ps[j];
+      const uint16_t *row = cb + (size_t)(c0 + j) * LORA;
+      a0 += w * bf2f(row[tid]);
+      a1 += w * bf2f(row[tid + 256]);
+    }
+    __syncthreads();
+  }
+  m_out = M;
+  l_out = L;
+  o0 = a0;
+  o1 = a1;
+}
+
+// Grid (H, B): blockIdx.x = head, so one head's workgroups (all sequences)
+// land on the same XCD (XCD = workgroup id mod 8) and share W_UV[h] in L2.
+// Merges the splits with an online max (exact recomputation for flagged
+// ones), folds kv_a_layernorm gamma, then out[v] = W_UV[h][v] . lat.
+__global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const uint8_t *__restrict__ wkvb,
                                                          const float *__restrict__ skvb,
                                                          const uint16_t *__restrict__ gamma,
                                                          uint16_t *__restrict__ attn) {
   const int h = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  __shared__ float wsp[256];
   __shared__ float lat[LORA];
+  __shared__ float qs[QKD];
+  __shared__ float ps[256];
   __shared__ float red[4];
-  const size_t base = (size_t)b * splits * HEADS + h;  // row of split 0
-  float m = -INFINITY;
-  for (int s = tid; s < splits; s += 256) m = fmaxf(m, part_ml[(base + (size_t)s * HEADS) * 2]);
-  m = wave_max(m);
-  if (lane == 0) red[wave] = m;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  float lsum = 0.f;
-  for (int s = tid; s < splits; s += 256) {
-    const float ms = part_ml[(base + (size_t)s * HEADS) * 2];
-    const float w = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
-    wsp[s] = w;
-    lsum += w * part_ml[(base + (size_t)s * HEADS) * 2 + 1];
+  const size_t base = (size_t)b * ap.splits * HEADS + h;
+  float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int s = 0; s < ap.splits; ++s) {
+    const size_t row = base + (size_t)s * HEADS;
+    float ms = ap.part_ml[row * 2], ls = ap.part_ml[row * 2 + 1], o0, o1;
+    if (ls < 0.f) {
+      recompute_split(ap, b, h, s, qs, ps, red, ms, ls, o0, o1);
+    } else {
+      o0 = ap.part_o[row * LORA + tid];
+      o1 = ap.part_o[row * LORA + tid + 256];
+    }
+    if (ms == -INFINITY) continue;  // split past this sequence's context
+    const float Mn = fmaxf(M, ms);
+    const float fo = (M == -INFINITY) ? 0.f : exp2f(M - Mn);
+    const float fn = exp2f(ms - Mn);
+    a0 = a0 * fo + o0 * fn;
+    a1 = a1 * fo + o1 * fn;
+    L = L * fo + ls * fn;
+    M = Mn;
   }
-  lsum = wave_sum(lsum);
-  if (lane == 0) red[wave] = lsum;
-  __syncthreads();
-  const float inv_l = 1.f / (red[0] + red[1] + red[2] + red[3]);
-  for (int c = tid; c < LORA; c += 256) {
-    float a = 0.f;
-    for (int s = 0; s < splits; ++s) a += wsp[s] * part_o[(base + (size_t)s * HEADS) * LORA + c];
-    lat[c] = a * inv_l * bf2f(gamma[c]);
-  }
+  const float inv = 1.f / L;
+  lat[tid] = a0 * inv * bf2f(gamma[tid]);
+  lat[tid + 256] = a1 * inv * bf2f(gamma[tid + 256]);
   __syncthreads();
   // out[v] = sum_c W_UV[h][v][c] * scale * lat[c]; wave handles 32 rows, lane 8 columns
   float lv[8];
@@ -422,7 +586,7 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(const float *__restrict
 // ---------------------------------------------------------------- orchestration
 
 struct DecodeLayout {
-  size_t counters, partials, xn, qa, qan, q, qbuf, part_ml, part_o, attn, total;
+  size_t xn, qa, qan, q, qbuf, part_ml, part_o, attn, total;
   GemvPlan pa, pb, po;
   int splits, tiles_per_split;
 };
@@ -442,8 +606,6 @@ static DecodeLayout decode_layout(const amla_mla_args &a) {
   L.splits = (ntiles + L.tiles_per_split - 1) / L.tiles_per_split;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes, 256); return o; };
-  L.counters = take(COUNTER_BYTES);
-  L.partials = take(std::max({L.pa.partial_bytes, L.pb.partial_bytes, L.po.partial_bytes, (size_t)256}));
   L.xn = take((size_t)B * a.hidden * 2);
   L.qa = take((size_t)B * a.q_lora * 2);
   L.qan = take((size_t)B * a.q_lora * 2);
@@ -494,7 +656,6 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   if (a->workspace_bytes < L.total)
     return fail(AMLA_EWORKSPACE, "mla_decode: workspace %zu bytes < %zu needed", a->workspace_bytes, L.total);
   char *ws = reinterpret_cast<char *>(a->workspace);
-  float *partials = reinterpret_cast<float *>(ws + L.partials);
   const int B = a->batch;
   const int HD = a->qk_nope + a->qk_rope;
 
@@ -523,7 +684,6 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pa.kpe = reinterpret_cast<uint16_t *>(a->kpe_cache);
   pa.ckv_bstride = (int64_t)a->max_seq * LORA; pa.kpe_bstride = (int64_t)a->max_seq * ROPE;
   pa.kv_lora = LORA; pa.rope = ROPE; pa.pos = a->positions; pa.seq_len = 1;
-  pa.ws = partials; pa.counters = counter_slot(ws, 1);
   if ((rc = launch_gemv(pa, GEMV_QKVA, L.pa, st))) return rc;
 
   // 2. q_a_layernorm (inference/ops.py:130)
@@ -541,7 +701,6 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pb.y = q; pb.ldy = pb.N;
   pb.pos = a->positions; pb.seq_len = 1; pb.rope = ROPE; pb.rope_table = a->rope_table;
   pb.head_dim = HD; pb.nope = a->qk_nope;
-  pb.ws = partials; pb.counters = counter_slot(ws, 2);
   if ((rc = launch_gemv(pb, GEMV_QROPE, L.pb, st))) return rc;
 
   // 4. absorb W_UK into the query
@@ -570,8 +729,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   // 6. merge splits, W_UV
   mark(ev, 5, st);
   uint16_t *attn = reinterpret_cast<uint16_t *>(ws + L.attn);
-  combine_uv_kernel<<<dim3(HEADS, B), 256, 0, st>>>(ap.part_o, ap.part_ml, L.splits,
-                                                     reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b,
+  combine_uv_kernel<<<dim3(HEADS, B), 256, 0, st>>>(ap, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b,
                                                      reinterpret_cast<const uint16_t *>(a->gamma_kv), attn);
   if ((rc = check_launch("mla combine"))) return rc;
 
@@ -584,7 +742,6 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   po.y = reinterpret_cast<uint16_t *>(a->out); po.ldy = a->hidden;
   po.res = reinterpret_cast<const uint16_t *>(a->residual); po.ldr = a->hidden;
   po.seq_len = 1;
-  po.ws = partials; po.counters = counter_slot(ws, 3);
   rc = launch_gemv(po, a->residual ? GEMV_RESID : GEMV_PLAIN, L.po, st);
   mark(ev, NSTAGE, st);
   return rc;

@@ -383,18 +383,13 @@ __global__ __launch_bounds__(256, 1) void flash_kernel(FlashParams p) {
 
 // ---------------------------------------------------------------- orchestration
 
-static int run_linear(GemvParams p, int mode, unsigned *counters, float *partials, hipStream_t st) {
-  if (p.M <= 64) {
-    const GemvPlan pl = plan_gemv(p.M, p.N, p.K);
-    p.counters = counters;
-    p.ws = partials;
-    return launch_gemv(p, mode, pl, st);
-  }
+static int run_linear(const GemvParams &p, int mode, hipStream_t st) {
+  if (p.M <= 64) return launch_gemv(p, mode, plan_gemv(p.M, p.N, p.K), st);
   return launch_gemm(p, mode, st);
 }
 
 struct PrefillLayout {
-  size_t counters, partials, xn, qa, qan, q, kvn, kpe, kvb, attn, total;
+  size_t xn, qa, qan, q, kvn, kpe, kvb, attn, total;
   int Tmax;
 };
 
@@ -403,18 +398,8 @@ static PrefillLayout prefill_layout(const amla_mla_args &a) {
   const size_t M = (size_t)a.batch * a.seq_len;
   const int HD = a.qk_nope + a.qk_rope;
   L.Tmax = a.max_context > 0 ? std::min(a.max_context, a.max_seq) : a.max_seq;
-  size_t part = 256;
-  auto upd = [&](int m, int n, int k) {
-    if (m <= 64) part = std::max(part, plan_gemv(m, n, k).partial_bytes);
-  };
-  upd((int)M, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
-  upd((int)M, a.heads * HD, a.q_lora);
-  upd(L.Tmax, a.heads * (a.qk_nope + a.v_dim), a.kv_lora);
-  upd((int)M, a.hidden, a.heads * a.v_dim);
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes, 256); return o; };
-  L.counters = take(COUNTER_BYTES);
-  L.partials = take(part);
   L.xn = take(M * a.hidden * 2);
   L.qa = take(M * a.q_lora * 2);
   L.qan = take(M * a.q_lora * 2);
@@ -464,7 +449,6 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   if (a->workspace_bytes < L.total)
     return fail(AMLA_EWORKSPACE, "mla_prefill: workspace %zu bytes < %zu needed", a->workspace_bytes, L.total);
   char *ws = reinterpret_cast<char *>(a->workspace);
-  float *partials = reinterpret_cast<float *>(ws + L.partials);
   const int B = a->batch, S = a->seq_len, M = B * S;
   const int HD = a->qk_nope + a->qk_rope;
   int rc;
@@ -495,7 +479,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   pa.kpe = reinterpret_cast<uint16_t *>(a->kpe_cache);
   pa.ckv_bstride = (int64_t)a->max_seq * a->kv_lora; pa.kpe_bstride = (int64_t)a->max_seq * a->qk_rope;
   pa.kv_lora = a->kv_lora; pa.rope = a->qk_rope; pa.pos = a->positions; pa.seq_len = S;
-  if ((rc = run_linear(pa, GEMV_QKVA, counter_slot(ws, 4), partials, st))) return rc;
+  if ((rc = run_linear(pa, GEMV_QKVA, st))) return rc;
 
   if ((rc = launch_rms_norm(qa, M, a->q_lora, a->q_lora, reinterpret_cast<const uint16_t *>(a->gamma_q), a->eps,
                             qan, a->q_lora, st)))
@@ -508,7 +492,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   pb.y = q; pb.ldy = pb.N;
   pb.pos = a->positions; pb.seq_len = S; pb.rope = a->qk_rope; pb.rope_table = a->rope_table;
   pb.head_dim = HD; pb.nope = a->qk_nope;
-  if ((rc = run_linear(pb, GEMV_QROPE, counter_slot(ws, 5), partials, st))) return rc;
+  if ((rc = run_linear(pb, GEMV_QROPE, st))) return rc;
 
   const int T = L.Tmax;
   FlashParams fp = {};
@@ -528,7 +512,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
     pk.w0 = reinterpret_cast<const uint8_t *>(a->w_kv_b); pk.s0 = a->s_kv_b;
     pk.N = a->heads * (a->qk_nope + a->v_dim); pk.K = a->kv_lora; pk.n_split = pk.N;
     pk.y = kvb; pk.ldy = pk.N; pk.seq_len = 1;
-    if ((rc = run_linear(pk, GEMV_PLAIN, counter_slot(ws, 6), partials, st))) return rc;
+    if ((rc = run_linear(pk, GEMV_PLAIN, st))) return rc;
     fp.b = b;
     flash_kernel<<<dim3(P_H, (S + P_QB - 1) / P_QB), 256, 0, st>>>(fp);
     if ((rc = check_launch("flash attention"))) return rc;
@@ -540,7 +524,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   po.N = a->hidden; po.K = a->heads * a->v_dim; po.n_split = po.N;
   po.y = reinterpret_cast<uint16_t *>(a->out); po.ldy = a->hidden;
   po.res = reinterpret_cast<const uint16_t *>(a->residual); po.ldr = a->hidden; po.seq_len = 1;
-  return run_linear(po, a->residual ? GEMV_RESID : GEMV_PLAIN, counter_slot(ws, 7), partials, st);
+  return run_linear(po, a->residual ? GEMV_RESID : GEMV_PLAIN, st);
 }
 
 }  // namespace amla

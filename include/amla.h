@@ -45,9 +45,8 @@ int amla_fp8_block_dequant(const void *weight, const float *scale_inv, int64_t n
 /* Replaces fp8_linear(x, weight, scale_inv, out_dtype=bf16), inference/ops.py:15-44:
  *   y[i, j] = bf16( sum_k x[i, k] * f32(weight[j, k]) * scale_inv[j/128, k/128] )
  * fp32 accumulation; x (m, k) bf16 with row stride ldx; y (m, n) bf16 with row
- * stride ldy.  Split-K partials use `workspace` (size from
- * amla_fp8_linear_workspace_bytes; it must hold zeros on the first call and is
- * left zeroed for the next). */
+ * stride ldy.  `workspace` is reserved (amla_fp8_linear_workspace_bytes
+ * returns 0 in this version; NULL is accepted). */
 int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void *weight,
                     const float *scale_inv, int64_t n, void *y, int64_t ldy, void *workspace,
                     size_t workspace_bytes, void *stream);
@@ -134,8 +133,7 @@ int amla_mla_decode_profiled(const amla_mla_args *args, void *stream, void *cons
 int amla_mla_prefill(const amla_mla_args *args, void *stream);
 
 /* Workspace bytes amla_mla_decode / amla_mla_prefill need for these args
- * (pointer fields are ignored).  The workspace must be zero-filled before its
- * first use; calls leave it zeroed where a later call relies on that. */
+ * (pointer fields are ignored).  Scratch only: no contents carry between calls. */
 size_t amla_mla_decode_workspace_bytes(const amla_mla_args *args);
 size_t amla_mla_prefill_workspace_bytes(const amla_mla_args *args);
 

@@ -77,8 +77,8 @@ def test_null_and_bad_arguments_fail_before_launch():
 
 def test_workspace_queries():
     L = _lib.lib()
-    assert L.amla_fp8_linear_workspace_bytes(1, 7168, 16384) > 0      # split-K
-    assert L.amla_fp8_linear_workspace_bytes(1, 24576, 1536) == 0     # no split
+    assert L.amla_fp8_linear_workspace_bytes(1, 7168, 16384) == 0
+    assert L.amla_fp8_linear_workspace_bytes(4096, 24576, 1536) == 0
     a = _lib.MlaArgs()
     a.batch, a.seq_len, a.hidden, a.heads, a.q_lora = 8, 1, 7168, 128, 1536
     a.kv_lora, a.qk_nope, a.qk_rope, a.v_dim = 512, 128, 64, 128

@@ -117,6 +117,22 @@ def test_decode_split_count_does_not_matter():
     assert_parity(a, b, "split plan independence")
 
 
+def test_decode_overflow_recompute():
+    """A cached rope key 500x larger than the rest, in the second tile of its
+    split: heads whose score jumps more than 2^64 above the split's reference
+    max take the exact recomputation path of the combine kernel."""
+    tag = "overflow"
+    lay = _layer("mla/" + tag)
+    pos = 2000
+    hidden = synth.make_hidden(R1, 1, 1, tag)
+    ckv, kpe = synth.make_kv_cache(R1, 1, 2008, pos, tag)
+    kpe[0, 1510] = (kpe[0, 1510].float() * 500).to(torch.bfloat16)
+    tab = _rope(2008)
+    want = R.mla_attention(hidden, lay.attn_weights, (ckv.clone(), kpe.clone()), pos, tab, R1)
+    got = ops.mla_attention(hidden.to(DEV), _to_dev(lay.attn_weights), (ckv.to(DEV), kpe.to(DEV)), pos, tab.to(DEV), R1)
+    assert_parity(got.cpu(), want, "overflow recompute")
+
+
 def test_decode_single_position_ignores_query():
     # T = 1: softmax == 1, the output cannot depend on the query path
     lay = _layer("mla/t1")
