@@ -175,42 +175,54 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int kb = wave; kb < KB; kb += NW) {
-    u32x4 a0[RT], a1[RT];
+  // block kb + NW is loaded while block kb is computed (a wave otherwise sits
+  // out one memory latency per 2 KB of weights)
+  u32x4 a0[2][RT], a1[2][RT];
+  bf16x8 xb[2][MT][4];
+  auto load_block = [&](int kb, int buf) {
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
       if (rvalid[r]) {
-        a0[r] = ldg16_nt(wrow[r] + (size_t)kb * 128);
-        a1[r] = ldg16_nt(wrow[r] + (size_t)kb * 128 + 16);
+        a0[buf][r] = ldg16_nt(wrow[r] + (size_t)kb * 128);
+        a1[buf][r] = ldg16_nt(wrow[r] + (size_t)kb * 128 + 16);
       } else {
-        a0[r] = u32x4{0, 0, 0, 0};
-        a1[r] = u32x4{0, 0, 0, 0};
+        a0[buf][r] = u32x4{0, 0, 0, 0};
+        a1[buf][r] = u32x4{0, 0, 0, 0};
       }
     }
-    bf16x8 b[MT][4];
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        b[t][u] = mvalid[t] ? as_bf16x8(ldg16(xrow[t] + kb * 128 + u * 8))
-                            : as_bf16x8(u32x4{0, 0, 0, 0});
+        xb[buf][t][u] = mvalid[t] ? as_bf16x8(ldg16(xrow[t] + kb * 128 + u * 8)) : as_bf16x8(u32x4{0, 0, 0, 0});
+  };
+  auto compute_block = [&](int kb, int buf) {
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
       const float s = rvalid[r] ? srow[r][kb] : 0.f;
       bf16x8 w0, w1, w2, w3;
-      fp8x16_to_bf16x16(a0[r], w0, w1);
-      fp8x16_to_bf16x16(a1[r], w2, w3);
+      fp8x16_to_bf16x16(a0[buf][r], w0, w1);
+      fp8x16_to_bf16x16(a1[buf][r], w2, w3);
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
         f32x4 c = {0.f, 0.f, 0.f, 0.f};
-        c = mfma16(w0, b[t][0], c);
-        c = mfma16(w1, b[t][1], c);
-        c = mfma16(w2, b[t][2], c);
-        c = mfma16(w3, b[t][3], c);
+        c = mfma16(w0, xb[buf][t][0], c);
+        c = mfma16(w1, xb[buf][t][1], c);
+        c = mfma16(w2, xb[buf][t][2], c);
+        c = mfma16(w3, xb[buf][t][3], c);
         acc[r][t] += s * c;
       }
     }
+  };
+  if (wave < KB) load_block(wave, 0);
+  int kb = wave;
+  for (; kb + NW < KB; kb += 2 * NW) {
+    load_block(kb + NW, 1);
+    compute_block(kb, 0);
+    if (kb + 2 * NW < KB) load_block(kb + 2 * NW, 0);
+    compute_block(kb + NW, 1);
   }
+  if (kb < KB) compute_block(kb, 0);
 
   __shared__ f32x4 red[NW][RT * MT][64];
 #pragma unroll
@@ -236,11 +248,16 @@ GemvPlan plan_gemv(int M, int N, int K) {
   const int tiles = (N + 15) / 16;
   const int KB = K / 128;
   const int MT = (M + 15) / 16;
-  pl.nw = KB >= 48 ? 16 : (KB >= 24 ? 8 : 4);
   // two row tiles per wave halve the x traffic once there are enough rows
   pl.rt = (M > 4 && tiles >= 2 * 256) ? 2 : 1;
-  while (pl.nw * pl.rt * (MT > 2 ? 4 : MT) > 64) pl.nw /= 2;
   pl.groups = (tiles + pl.rt - 1) / pl.rt;
+  // waves per workgroup: enough waves in flight to cover the memory latency
+  // (~24 resident waves per CU at this kernel's register count) while every
+  // workgroup stays resident, and at least two K blocks per wave
+  int nw = 16;
+  while (nw > 4 && ((int64_t)pl.groups * nw > 256 * 24 || KB < 2 * nw)) nw /= 2;
+  while (nw > 4 && nw * pl.rt * (MT > 2 ? 4 : MT) > 64) nw /= 2;
+  pl.nw = nw;
   return pl;
 }
 

@@ -286,31 +286,35 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) sc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      u32x4 acur[2], anext[2];
+      // A fragments two K steps ahead of the MFMAs that use them (one wave per
+      // SIMD: nothing else hides the LDS latency)
+      constexpr int S_DEPTH = 3;
+      u32x4 ab[S_DEPTH][2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) acur[mt] = *reinterpret_cast<const u32x4 *>(K + (mt * 16 + li) * KROW + 8 * lg);
+      for (int d = 0; d < S_DEPTH - 1; ++d)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+          ab[d][mt] = *reinterpret_cast<const u32x4 *>(K + (mt * 16 + li) * KROW + d * 32 + 8 * lg);
 #pragma unroll
       for (int ks = 0; ks < LORA / 32; ++ks) {
-        if (ks + 1 < LORA / 32) {
+        if (ks + S_DEPTH - 1 < LORA / 32) {
 #pragma unroll
           for (int mt = 0; mt < 2; ++mt)
-            anext[mt] = *reinterpret_cast<const u32x4 *>(K + (mt * 16 + li) * KROW + (ks + 1) * 32 + 8 * lg);
+            ab[(ks + S_DEPTH - 1) % S_DEPTH][mt] =
+                *reinterpret_cast<const u32x4 *>(K + (mt * 16 + li) * KROW + (ks + S_DEPTH - 1) * 32 + 8 * lg);
         }
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-          ssq[mt] = dot2_bf16(acur[mt].x, ssq[mt]);
-          ssq[mt] = dot2_bf16(acur[mt].y, ssq[mt]);
-          ssq[mt] = dot2_bf16(acur[mt].z, ssq[mt]);
-          ssq[mt] = dot2_bf16(acur[mt].w, ssq[mt]);
-          const bf16x8 a = as_bf16x8(acur[mt]);
+          const u32x4 cur = ab[ks % S_DEPTH][mt];
+          ssq[mt] = dot2_bf16(cur.x, ssq[mt]);
+          ssq[mt] = dot2_bf16(cur.y, ssq[mt]);
+          ssq[mt] = dot2_bf16(cur.z, ssq[mt]);
+          ssq[mt] = dot2_bf16(cur.w, ssq[mt]);
+          const bf16x8 a = as_bf16x8(cur);
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            sc[mt][nt] = mfma16(a, qf[nt][ks], sc[mt][nt]);
-          }
+          for (int nt = 0; nt < 2; ++nt) sc[mt][nt] = mfma16(a, qf[nt][ks], sc[mt][nt]);
         }
         asm volatile("" ::: "memory");
-        acur[0] = anext[0];
-        acur[1] = anext[1];
       }
       // ---- r_t: full sum for row mt*16+li (4 lane groups), then to the C
       // layout (lane (head, lg) holds rows mt*16 + 4*lg + r) and applied
@@ -346,6 +350,31 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       }
       __builtin_amdgcn_sched_barrier(0);
 
+      // ---- O^T (latent x head) += C^T (latent x t) . P^T (t x head); C^T by
+      // transpose reads: within a 16-lane group, lane s addresses row
+      // t0 + s/4, columns c0 + 4(s%4) .. +3 and lane L receives
+      // C[t0 .. t0+3][c0 + L]; t0 = 4*lg and 16 + 4*lg match P^T's rows.
+      // The reads are inline asm: the builtin makes the compiler wait for every
+      // LDS-DMA copy in flight (vmcnt(0)) before the first read, which would
+      // drain the prefetch of the tile after next; ordering against the DMA
+      // and rotation writes to this stage is given by the explicit vmcnt waits
+      // and the tile barrier.  They complete asynchronously: each wait names
+      // the registers it guards as in/out operands so no use is scheduled
+      // before it; outputs are early-clobber (two reads share one address).
+      // PV_DEPTH steps are in flight; the first ones are issued before the
+      // softmax so their latency hides under it.
+      constexpr int PV_DEPTH = 4;
+      const int s16 = lane & 15;
+      const uint32_t a0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+          (__attribute__((address_space(3))) const uint16_t *)(K + (4 * lg + (s16 >> 2)) * KROW + 4 * (s16 & 3))));
+      u32x2 t0[PV_DEPTH], t1[PV_DEPTH];
+#define AMLA_TR(dst0, dst1, MT)                                                                            \
+  asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"               \
+               : "=&v"(dst0), "=&v"(dst1)                                                                \
+               : "v"(a0), "i"((MT) * 32), "i"((MT) * 32 + 16 * KROW * 2))
+#pragma unroll
+      for (int d = 0; d < PV_DEPTH; ++d) AMLA_TR(t0[d], t1[d], d);
+
       // ---- probabilities relative to the head's fixed reference max
       const int tbase = tile * TT;
       bf16x8 pf[2];
@@ -380,45 +409,22 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
         pf[nt] = as_bf16x8(pk);
       }
       have_ref = true;
-      __builtin_amdgcn_sched_barrier(0);
 
-      // ---- O^T (latent x head) += C^T (latent x t) . P^T (t x head); C^T by
-      // transpose reads: within a 16-lane group, lane s addresses row
-      // t0 + s/4, columns c0 + 4(s%4) .. +3 and lane L receives
-      // C[t0 .. t0+3][c0 + L]; t0 = 4*lg and 16 + 4*lg match P^T's rows.
-      {
-        // The transpose reads are issued as inline asm: the builtin makes the
-        // compiler wait for every LDS-DMA copy in flight (vmcnt(0)) before the
-        // first read, which would drain the prefetch of the tile after next.
-        // Ordering against the DMA and rotation writes to this stage is
-        // already given by the explicit vmcnt waits and the tile barrier.
-        const int s16 = lane & 15;
-        const uint32_t a0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-            (__attribute__((address_space(3))) const uint16_t *)(K + (4 * lg + (s16 >> 2)) * KROW + 4 * (s16 & 3))));
-        u32x2 t0[2], t1[2];
-        // The reads complete asynchronously: each wait names the registers it
-        // guards as in/out operands, so no use of them is scheduled before it;
-        // outputs are early-clobber (two reads share the address register).
-#define AMLA_TR(dst0, dst1, MT)                                                                            \
-  asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"               \
-               : "=&v"(dst0), "=&v"(dst1)                                                                \
-               : "v"(a0), "i"((MT) * 32), "i"((MT) * 32 + 16 * KROW * 2))
-        AMLA_TR(t0[0], t1[0], 0);
 #pragma unroll
-        for (int mt = 0; mt < LORA / 16; ++mt) {
-          const int c = mt & 1, n = c ^ 1;
-          if (mt + 1 < LORA / 16) {
-            AMLA_TR(t0[n], t1[n], mt + 1);
-            asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
-          } else {
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
-          }
-          const bf16x8 a = as_bf16x8(u32x4{t0[c].x, t0[c].y, t1[c].x, t1[c].y});
-          o[mt][0] = mfma16(a, pf[0], o[mt][0]);
-          o[mt][1] = mfma16(a, pf[1], o[mt][1]);
-        }
-#undef AMLA_TR
+      for (int mt = 0; mt < LORA / 16; ++mt) {
+        const int c = mt % PV_DEPTH;
+        // reads of steps mt+1 .. min(mt+DEPTH-1, last) may stay in flight
+        const int ahead = (LORA / 16 - 1 - mt) < (PV_DEPTH - 1) ? (LORA / 16 - 1 - mt) : (PV_DEPTH - 1);
+        if (ahead == 3) asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
+        else if (ahead == 2) asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
+        else if (ahead == 1) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
+        else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
+        const bf16x8 a = as_bf16x8(u32x4{t0[c].x, t0[c].y, t1[c].x, t1[c].y});
+        o[mt][0] = mfma16(a, pf[0], o[mt][0]);
+        o[mt][1] = mfma16(a, pf[1], o[mt][1]);
+        if (mt + PV_DEPTH < LORA / 16) AMLA_TR(t0[c], t1[c], mt + PV_DEPTH);
       }
+#undef AMLA_TR
       __builtin_amdgcn_sched_barrier(0);
 
       // ---- next tile: own rows and table landed -> rotate their rope keys
@@ -542,25 +548,66 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
   __shared__ float qs[QKD];
   __shared__ float ps[256];
   __shared__ float red[4];
+  __shared__ float wsp[256];
+  __shared__ int s_flag;
   const size_t base = (size_t)b * ap.splits * HEADS + h;
   float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
-  for (int s = 0; s < ap.splits; ++s) {
-    const size_t row = base + (size_t)s * HEADS;
-    float ms = ap.part_ml[row * 2], ls = ap.part_ml[row * 2 + 1], o0, o1;
-    if (ls < 0.f) {
-      recompute_split(ap, b, h, s, qs, ps, red, ms, ls, o0, o1);
-    } else {
-      o0 = ap.part_o[row * LORA + tid];
-      o1 = ap.part_o[row * LORA + tid + 256];
+  // fast path: every split carries a valid (m, l, O); max, weights, then a
+  // weighted sum with independent loads (splits <= 256)
+  float ms = -INFINITY, ls = 0.f;
+  if (tid < ap.splits) {
+    ms = ap.part_ml[(base + (size_t)tid * HEADS) * 2];
+    ls = ap.part_ml[(base + (size_t)tid * HEADS) * 2 + 1];
+  }
+  if (tid == 0) s_flag = 0;
+  __syncthreads();
+  if (ls < 0.f) s_flag = 1;
+  M = block_reduce(ms, red, true);
+  if (!s_flag) {
+    const float w = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
+    if (tid < ap.splits) wsp[tid] = w;
+    L = block_reduce(w * ls, red, false);
+    const float *po = ap.part_o + base * LORA + tid;
+    const size_t stride = (size_t)HEADS * LORA;
+    int s = 0;
+    for (; s + 8 <= ap.splits; s += 8) {
+      float v0[8], v1[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v0[j] = po[(s + j) * stride];
+        v1[j] = po[(s + j) * stride + 256];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        a0 += wsp[s + j] * v0[j];
+        a1 += wsp[s + j] * v1[j];
+      }
     }
-    if (ms == -INFINITY) continue;  // split past this sequence's context
-    const float Mn = fmaxf(M, ms);
-    const float fo = (M == -INFINITY) ? 0.f : exp2f(M - Mn);
-    const float fn = exp2f(ms - Mn);
-    a0 = a0 * fo + o0 * fn;
-    a1 = a1 * fo + o1 * fn;
-    L = L * fo + ls * fn;
-    M = Mn;
+    for (; s < ap.splits; ++s) {
+      a0 += wsp[s] * po[s * stride];
+      a1 += wsp[s] * po[s * stride + 256];
+    }
+  } else {
+    // rare path: online merge with exact recomputation of flagged splits
+    M = -INFINITY;
+    for (int s = 0; s < ap.splits; ++s) {
+      const size_t row = base + (size_t)s * HEADS;
+      float m1 = ap.part_ml[row * 2], l1 = ap.part_ml[row * 2 + 1], o0, o1;
+      if (l1 < 0.f) {
+        recompute_split(ap, b, h, s, qs, ps, red, m1, l1, o0, o1);
+      } else {
+        o0 = ap.part_o[row * LORA + tid];
+        o1 = ap.part_o[row * LORA + tid + 256];
+      }
+      if (m1 == -INFINITY) continue;  // split past this sequence's context
+      const float Mn = fmaxf(M, m1);
+      const float fo = (M == -INFINITY) ? 0.f : exp2f(M - Mn);
+      const float fn = exp2f(m1 - Mn);
+      a0 = a0 * fo + o0 * fn;
+      a1 = a1 * fo + o1 * fn;
+      L = L * fo + l1 * fn;
+      M = Mn;
+    }
   }
   const float inv = 1.f / L;
   lat[tid] = a0 * inv * bf2f(gamma[tid]);
@@ -572,8 +619,13 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
   for (int j = 0; j < 8; ++j) lv[j] = lat[lane * 8 + j];
   const float sc = skvb[(size_t)(2 * h + 1) * (LORA / 128) + (lane * 8) / 128];
   const uint8_t *wrow = wkvb + ((size_t)h * (NOPE + VD) + NOPE) * LORA + lane * 8;
-  for (int v = wave * 32; v < wave * 32 + 32; ++v) {
-    const u32x2 raw = ldg8(wrow + (size_t)v * LORA);
+  u32x2 wv[32];  // all 32 rows in flight at once
+#pragma unroll
+  for (int j = 0; j < 32; ++j) wv[j] = ldg8(wrow + (size_t)(wave * 32 + j) * LORA);
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const int v = wave * 32 + j;
+    const u32x2 raw = wv[j];
     const f32x2 w01 = fp8x2_to_f32<false>(raw.x), w23 = fp8x2_to_f32<true>(raw.x);
     const f32x2 w45 = fp8x2_to_f32<false>(raw.y), w67 = fp8x2_to_f32<true>(raw.y);
     float a = w01.x * lv[0] + w01.y * lv[1] + w23.x * lv[2] + w23.y * lv[3] + w45.x * lv[4] +
