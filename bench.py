@@ -137,6 +137,19 @@ def decode_stage_times(stack, caches, hidden, pos, rope, ctx, reps=2):
     return {n: v / len(evs) for n, v in tot.items()}
 
 
+def attn_traffic(B, T):
+    """Measured HBM bytes per attention launch (FETCH_SIZE + WRITE_SIZE, each
+    scaled by the same counters on a copy of known size), read from the
+    committed counter summary of this workload; None when there is none."""
+    import re
+    path = os.path.join(ROOT, "profiles", f"attn_kernel_b{B}_ctx{T}_traffic.md")
+    try:
+        m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", open(path).read())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 # ------------------------------------------------------------------ CPU baseline
 
 def cpu_baseline(T, B):
@@ -177,12 +190,24 @@ def main():
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (5 launches) and exit: the known-size "
+                         "kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU sharding is a design "
                                    "note only (--gpus must be 1)"}))
         sys.exit(2)
     dev = torch.device("cuda:0")
+    if args.copy_calibration_mib:
+        n = args.copy_calibration_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
+        return
     torch.manual_seed(0)
     B, T, NL = args.batch, args.context, args.layers
 
@@ -261,7 +286,7 @@ def main():
         "decode_stage_ms": {k: round(v, 4) for k, v in stages.items()},
         "roofline": {"kernel": "attn_kernel (latent-cache attention, split over context)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": attn_traffic(B, T),
                      "bytes_per_launch": attn_bytes, "avg_ms": round(attn_ms, 4)},
         **extras,
     }
