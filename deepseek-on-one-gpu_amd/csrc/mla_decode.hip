@@ -124,8 +124,8 @@ struct AttnParams {
 // LDS: a ring of NST stages, each one tile of TT cache rows
 //   K   [TT][KROW] bf16: raw latent row (DMA) | rotated rope key (written after DMA)
 //   raw [TT][64]   bf16: raw rope keys (DMA)
-// plus one (cos, sin) table block for the tile being prepared and the rope
-// part of the 128 head queries (B operand of the rope K steps).
+// plus two (cos, sin) table blocks (tiles of even / odd index), copied two
+// tiles ahead like the rows.
 constexpr int NST = 3;
 constexpr int KROW = QKD + 8;  // 1168 B rows: the 16 B pad spreads 16 rows over all LDS banks
 constexpr int K_BYTES = TT * KROW * 2;
@@ -133,10 +133,8 @@ constexpr int RAW_BYTES = TT * ROPE * 2;
 constexpr int STAGE_BYTES = K_BYTES + RAW_BYTES;
 constexpr int TAB_OFF = NST * STAGE_BYTES;
 constexpr int TAB_BYTES = TT * ROPE * 4;
-constexpr int QPE_OFF = TAB_OFF + TAB_BYTES;
-constexpr int QPE_BYTES = HEADS * ROPE * 2;
-constexpr int ATTN_LDS_BYTES = QPE_OFF + QPE_BYTES;
-constexpr int TILE_DMA = 9;   // copies per wave per tile: 8 latent rows + 1 block of rope keys
+constexpr int ATTN_LDS_BYTES = TAB_OFF + 2 * TAB_BYTES;
+constexpr int TILE_DMA = 11;  // copies per wave per tile: 8 latent rows, 1 block of rope keys, 2 table blocks
 constexpr float REF_HEADROOM = 64.f;      // p = 2^(s - m_ref) <= 2^64: no overflow anywhere
 
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
@@ -171,7 +169,8 @@ AMLA_DEV void dma_table(const AttnParams &p, int tile, int T, uint8_t *smem, int
   for (int j = 0; j < 2; ++j) {
     const int e = j * 64 + lane;
     const int off = min(e >> 4, last) * (ROPE * 4) + (e & 15) * 16;
-    __builtin_amdgcn_global_load_lds(tb + off, LDS_PTR(smem + TAB_OFF + wave * 2048 + j * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(tb + off, LDS_PTR(smem + TAB_OFF + (tile & 1) * TAB_BYTES + wave * 2048 + j * 1024),
+                                     16, 0, 0);
   }
 }
 
@@ -182,11 +181,11 @@ AMLA_DEV uint32_t rot_pair(uint32_t x, float c, float s) {
 
 // Wave w rotates the rope keys of the rows it copied (fp32 rotation rounded to
 // bf16, as inference/ops.py:93-97) into the K rows of the stage.
-AMLA_DEV void rotate_own_rows(uint8_t *stage, const uint8_t *smem, int wave, int lane) {
+AMLA_DEV void rotate_own_rows(uint8_t *stage, const uint8_t *tab, int wave, int lane) {
   const int row = wave * 8 + (lane >> 3), q = lane & 7;
   const u32x4 raw = *reinterpret_cast<const u32x4 *>(stage + K_BYTES + row * (ROPE * 2) + q * 16);
-  const f32x4 c0 = *reinterpret_cast<const f32x4 *>(smem + TAB_OFF + row * (ROPE * 4) + q * 32);
-  const f32x4 c1 = *reinterpret_cast<const f32x4 *>(smem + TAB_OFF + row * (ROPE * 4) + q * 32 + 16);
+  const f32x4 c0 = *reinterpret_cast<const f32x4 *>(tab + row * (ROPE * 4) + q * 32);
+  const f32x4 c1 = *reinterpret_cast<const f32x4 *>(tab + row * (ROPE * 4) + q * 32 + 16);
   u32x4 r;
   r.x = rot_pair(raw.x, c0.x, c0.y);
   r.y = rot_pair(raw.y, c0.z, c0.w);
@@ -198,7 +197,21 @@ AMLA_DEV void rotate_own_rows(uint8_t *stage, const uint8_t *smem, int wave, int
 template <int N>
 AMLA_DEV void wait_vmcnt() {
   if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
+}
+
+// sum / max over the four lanes l, l^16, l^32, l^48 (lane swaps, no LDS)
+AMLA_DEV float sum_lane_groups(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+AMLA_DEV float max_lane_groups(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float s = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 AMLA_DEV float dot2_bf16(uint32_t a, float acc) {
@@ -207,21 +220,31 @@ AMLA_DEV float dot2_bf16(uint32_t a, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
 }
 
-// Grid (splits, B), 256 threads, one workgroup per CU (~145 KB of LDS).
+// Grid (splits, B), 256 threads, one workgroup per CU (~138 KB of LDS).
 // Wave w owns heads 32w .. 32w+31.  Per tile of 32 cache rows:
 //   S^T (t x head) = K_tile (32 x 576) . Q^T with the tile rows as the MFMA M
 //     dimension, so each lane ends with 8 scores of one head (its column);
-//   r_t = rsqrt(mean(c_t^2) + eps) from the same A fragments (v_dot2), moved
-//     to the C layout with lane permutes and applied between the latent and the
-//     rope K steps (one accumulator set);
+//     18 K steps of 32 (16 latent, 2 rotated rope), A fragments read from LDS
+//     three steps ahead;
+//   r_t = rsqrt(mean(c_t^2) + eps) from the same A fragments (v_dot2), summed
+//     over the four lane groups with lane swaps, moved to the C layout with
+//     one round of lane permutes and applied before the rope K steps;
 //   p = 2^(s - m_ref): m_ref is the head's max over the split's first tile and
 //     stays fixed, so O^T is only ever touched by MFMA (no rescaling); a head
 //     whose later tile exceeds m_ref by REF_HEADROOM is flagged instead;
-//   O^T (512 x 32 heads, fp32) += C^T (512 x t) . P^T, C^T from a latent-major
-//     copy of the tile, P^T = the score registers (p * r_t as bf16).
-// Registers: O^T takes 256 accumulators, the latent query fragments 128; the
-// loop must not spill (a scratch reload would wait for every copy in flight),
+//   O^T (512 x 32 heads, fp32) += C^T (512 x t) . P^T, C^T by transpose reads
+//     of the same tile, P^T = the score registers (p * r_t as bf16).
+// Registers: O^T takes 256 accumulators, the query fragments 144; the loop
+// must not spill (a scratch reload would wait for every copy in flight),
 // which is why the copies use scalar bases and there is no rescaling path.
+//
+// LDS reads of the score steps and the transpose reads are inline asm with
+// explicit lgkmcnt waits: the compiler would otherwise wait for every read
+// (and, for the transpose builtin, every LDS-DMA copy) before each use.  A
+// wait names the registers it guards as in/out operands so no use is
+// scheduled before it.  Counting only this code's own reads is safe: LDS
+// operations complete in order, so any other LDS operation issued in between
+// only makes a wait stricter; nothing in the loop uses scalar memory loads.
 __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   const int split = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -234,22 +257,13 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int head0 = wave * 32;
 
-  // rope half of this wave's 32 head queries -> LDS (read back by the same wave)
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = j * 64 + lane, hh = e >> 3, q = e & 7;
-    *reinterpret_cast<u32x4 *>(smem + QPE_OFF + ((head0 + hh) * ROPE + q * 8) * 2) =
-        ldg16(p.qbuf + ((size_t)b * HEADS + head0 + hh) * QKD + LORA + q * 8);
-  }
-  // latent query fragments (B operand: head = column l%16, K = 8*lg .. of each 32-wide step)
-  bf16x8 qf[2][LORA / 32];
+  // query fragments (B operand: head = column l%16, K = 8*lg .. of each 32-wide step)
+  bf16x8 qf[2][QKD / 32];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const uint16_t *qr = p.qbuf + ((size_t)b * HEADS + head0 + nt * 16 + li) * QKD + 8 * lg;
 #pragma unroll
-    for (int ks = 0; ks < LORA / 32; ++ks) {
-      qf[nt][ks] = as_bf16x8(ldg16(qr + ks * 32));
-    }
+    for (int ks = 0; ks < QKD / 32; ++ks) qf[nt][ks] = as_bf16x8(ldg16(qr + ks * 32));
   }
 
   f32x4 o[LORA / 16][2];
@@ -262,107 +276,97 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
     dma_table(p, tb, T, smem, wave, lane);
     dma_rows(p, b, tb, T, smem, wave, lane);
     if (tb + 1 < te) {
+      dma_table(p, tb + 1, T, smem, wave, lane);
       dma_rows(p, b, tb + 1, T, smem + STAGE_BYTES, wave, lane);
       wait_vmcnt<TILE_DMA>();
     } else {
       wait_vmcnt<0>();
     }
-    rotate_own_rows(smem, smem, wave, lane);
+    rotate_own_rows(smem, smem + TAB_OFF + (tb & 1) * TAB_BYTES, wave, lane);
     __syncthreads();
     bool have_ref = false;
     for (int tile = tb; tile < te; ++tile) {
       const int it = tile - tb;
       uint8_t *const cur = smem + (it % NST) * STAGE_BYTES;
-      // the table block only ever holds this wave's rows: no barrier needed
-      if (tile + 1 < te) dma_table(p, tile + 1, T, smem, wave, lane);
-      if (tile + 2 < te) dma_rows(p, b, tile + 2, T, smem + ((it + 2) % NST) * STAGE_BYTES, wave, lane);
+      // copies of the tile after next (the table block only ever holds this
+      // wave's rows: no barrier needed for it)
+      if (tile + 2 < te) {
+        dma_table(p, tile + 2, T, smem, wave, lane);
+        dma_rows(p, b, tile + 2, T, smem + ((it + 2) % NST) * STAGE_BYTES, wave, lane);
+      }
       __builtin_amdgcn_sched_barrier(0);
       const uint16_t *K = reinterpret_cast<const uint16_t *>(cur);
 
-      // ---- latent K steps: S^T and row sums of squares, one A fragment step ahead
+      // ---- scores: 18 K steps, A fragments SD steps ahead
+      constexpr int NSTEP = QKD / 32;
+      constexpr int SD = 3;
+      const uint32_t kaddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+          (__attribute__((address_space(3))) const uint16_t *)(K + li * KROW + 8 * lg)));
+#define AMLA_RDA(dst, S, MT) \
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(kaddr), "i"(((MT) * 16 * KROW + (S) * 32) * 2))
       f32x4 sc[2][2];
       float ssq[2] = {0.f, 0.f};
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) sc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      // A fragments two K steps ahead of the MFMAs that use them (one wave per
-      // SIMD: nothing else hides the LDS latency)
-      constexpr int S_DEPTH = 3;
-      u32x4 ab[S_DEPTH][2];
+      u32x4 ab[SD][2];
 #pragma unroll
-      for (int d = 0; d < S_DEPTH - 1; ++d)
+      for (int d = 0; d < SD; ++d) {
+        AMLA_RDA(ab[d][0], d, 0);
+        AMLA_RDA(ab[d][1], d, 1);
+      }
+      float rc[2][4];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-          ab[d][mt] = *reinterpret_cast<const u32x4 *>(K + (mt * 16 + li) * KROW + d * 32 + 8 * lg);
+      for (int ks = 0; ks < NSTEP; ++ks) {
+        const int c = ks % SD;
+        const int later = (NSTEP - 1 - ks) < (SD - 1) ? (NSTEP - 1 - ks) : (SD - 1);  // steps issued after ks
+        if (later == 2) asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
+        else if (later == 1) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
+        else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
+        if (ks == LORA / 32) {
+          // r_t: full sum for row mt*16+li over the 4 lane groups, then to the
+          // C layout (lane (head, lg) holds rows mt*16 + 4*lg + r) and applied
+          // to the latent part of the scores
 #pragma unroll
-      for (int ks = 0; ks < LORA / 32; ++ks) {
-        if (ks + S_DEPTH - 1 < LORA / 32) {
+          for (int mt = 0; mt < 2; ++mt) {
+            const float rrow = rsqrtf(sum_lane_groups(ssq[mt]) * (1.f / LORA) + p.eps);
 #pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
-            ab[(ks + S_DEPTH - 1) % S_DEPTH][mt] =
-                *reinterpret_cast<const u32x4 *>(K + (mt * 16 + li) * KROW + (ks + S_DEPTH - 1) * 32 + 8 * lg);
+            for (int r = 0; r < 4; ++r) rc[mt][r] = __shfl(rrow, 4 * lg + r, 64);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) sc[mt][nt][r] *= rc[mt][r];
+          }
         }
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-          const u32x4 cur = ab[ks % S_DEPTH][mt];
-          ssq[mt] = dot2_bf16(cur.x, ssq[mt]);
-          ssq[mt] = dot2_bf16(cur.y, ssq[mt]);
-          ssq[mt] = dot2_bf16(cur.z, ssq[mt]);
-          ssq[mt] = dot2_bf16(cur.w, ssq[mt]);
-          const bf16x8 a = as_bf16x8(cur);
+          const u32x4 cur_a = ab[c][mt];
+          if (ks < LORA / 32) {
+            ssq[mt] = dot2_bf16(cur_a.x, ssq[mt]);
+            ssq[mt] = dot2_bf16(cur_a.y, ssq[mt]);
+            ssq[mt] = dot2_bf16(cur_a.z, ssq[mt]);
+            ssq[mt] = dot2_bf16(cur_a.w, ssq[mt]);
+          }
+          const bf16x8 a = as_bf16x8(cur_a);
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt) sc[mt][nt] = mfma16(a, qf[nt][ks], sc[mt][nt]);
         }
-        asm volatile("" ::: "memory");
-      }
-      // ---- r_t: full sum for row mt*16+li (4 lane groups), then to the C
-      // layout (lane (head, lg) holds rows mt*16 + 4*lg + r) and applied
-      float rc[2][4];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        float v = ssq[mt];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        const float rrow = rsqrtf(v * (1.f / LORA) + p.eps);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) rc[mt][r] = __shfl(rrow, 4 * lg + r, 64);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) sc[mt][nt][r] *= rc[mt][r];
-      }
-      // ---- rope K steps: rotated keys (K columns 512..575) x rope queries (LDS)
-#pragma unroll
-      for (int kk = 0; kk < ROPE / 32; ++kk) {
-        bf16x8 qp[2];
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          qp[nt] = *reinterpret_cast<const bf16x8 *>(smem + QPE_OFF + ((head0 + nt * 16 + li) * ROPE + kk * 32 + 8 * lg) * 2);
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8 *>(K + (mt * 16 + li) * KROW + LORA + kk * 32 + 8 * lg);
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            sc[mt][nt] = mfma16(a, qp[nt], sc[mt][nt]);
-          }
+        if (ks + SD < NSTEP) {
+          AMLA_RDA(ab[c][0], ks + SD, 0);
+          AMLA_RDA(ab[c][1], ks + SD, 1);
         }
       }
+#undef AMLA_RDA
       __builtin_amdgcn_sched_barrier(0);
 
       // ---- O^T (latent x head) += C^T (latent x t) . P^T (t x head); C^T by
       // transpose reads: within a 16-lane group, lane s addresses row
       // t0 + s/4, columns c0 + 4(s%4) .. +3 and lane L receives
       // C[t0 .. t0+3][c0 + L]; t0 = 4*lg and 16 + 4*lg match P^T's rows.
-      // The reads are inline asm: the builtin makes the compiler wait for every
-      // LDS-DMA copy in flight (vmcnt(0)) before the first read, which would
-      // drain the prefetch of the tile after next; ordering against the DMA
-      // and rotation writes to this stage is given by the explicit vmcnt waits
-      // and the tile barrier.  They complete asynchronously: each wait names
-      // the registers it guards as in/out operands so no use is scheduled
-      // before it; outputs are early-clobber (two reads share one address).
-      // PV_DEPTH steps are in flight; the first ones are issued before the
-      // softmax so their latency hides under it.
+      // Outputs are early-clobber (two reads share one address).  PV_DEPTH
+      // steps are in flight; the first ones are issued before the softmax so
+      // their latency hides under it.
       constexpr int PV_DEPTH = 4;
       const int s16 = lane & 15;
       const uint32_t a0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
@@ -391,8 +395,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
             sv[mt * 4 + r] = v;
             mx = fmaxf(mx, v);
           }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mx = max_lane_groups(mx);
         if (!have_ref) m_ref[nt] = mx;
         bad[nt] = bad[nt] || (mx > m_ref[nt] + REF_HEADROOM);
         float pv[8];
@@ -431,7 +434,8 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       if (tile + 1 < te) {
         if (tile + 2 < te) wait_vmcnt<TILE_DMA>();
         else wait_vmcnt<0>();
-        rotate_own_rows(smem + ((it + 1) % NST) * STAGE_BYTES, smem, wave, lane);
+        rotate_own_rows(smem + ((it + 1) % NST) * STAGE_BYTES, smem + TAB_OFF + ((tile + 1) & 1) * TAB_BYTES, wave,
+                        lane);
       }
       // barrier without a memory fence: a fence would also wait for the copy
       // of the tile after next; LDS writes (rotated keys) are drained by hand
