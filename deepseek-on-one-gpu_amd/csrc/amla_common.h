@@ -40,7 +40,9 @@ AMLA_DEV float lo_bf(uint32_t v) { return __uint_as_float(v << 16); }
 AMLA_DEV float hi_bf(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
 
 AMLA_DEV uint32_t pack_bf16(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));  // v_cvt_pk_bf16_f32, RNE
 }
 
 // Two e4m3fn bytes (bytes 0,1 or 2,3 of w) -> two exact f32.

@@ -122,18 +122,22 @@ struct AttnParams {
 };
 
 // LDS: a ring of NST stages, each one tile of TT cache rows
-//   K   [TT][KROW] bf16: raw latent row (DMA) | rotated rope key (written after DMA)
+//   K   [TT][KROW] bf16: raw latent row (DMA) | rotated rope key / r_t (written after DMA)
 //   raw [TT][64]   bf16: raw rope keys (DMA)
+//   rt  [TT]       fp32: r_t = rsqrt(mean(c_t^2) + eps) of each row
 // plus two (cos, sin) table blocks (tiles of even / odd index), copied two
-// tiles ahead like the rows.
+// tiles ahead like the rows, and the tile's probabilities P^T of all heads.
 constexpr int NST = 3;
 constexpr int KROW = QKD + 8;  // 1168 B rows: the 16 B pad spreads 16 rows over all LDS banks
 constexpr int K_BYTES = TT * KROW * 2;
 constexpr int RAW_BYTES = TT * ROPE * 2;
-constexpr int STAGE_BYTES = K_BYTES + RAW_BYTES;
+constexpr int RT_OFF = K_BYTES + RAW_BYTES;  // r_t of the tile's rows, fp32
+constexpr int STAGE_BYTES = RT_OFF + TT * 4;
 constexpr int TAB_OFF = NST * STAGE_BYTES;
 constexpr int TAB_BYTES = TT * ROPE * 4;
-constexpr int ATTN_LDS_BYTES = TAB_OFF + 2 * TAB_BYTES;
+constexpr int P_OFF = TAB_OFF + 2 * TAB_BYTES;
+constexpr int PROW = TT * 2 + 16;  // bf16 probabilities of one head, 80 B rows (conflict-free 16 B reads)
+constexpr int ATTN_LDS_BYTES = P_OFF + HEADS * PROW;
 constexpr int TILE_DMA = 11;  // copies per wave per tile: 8 latent rows, 1 block of rope keys, 2 table blocks
 constexpr float REF_HEADROOM = 64.f;      // p = 2^(s - m_ref) <= 2^64: no overflow anywhere
 
@@ -179,19 +183,51 @@ AMLA_DEV uint32_t rot_pair(uint32_t x, float c, float s) {
   return pack_bf16(__fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s)), __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c)));
 }
 
-// Wave w rotates the rope keys of the rows it copied (fp32 rotation rounded to
-// bf16, as inference/ops.py:93-97) into the K rows of the stage.
-AMLA_DEV void rotate_own_rows(uint8_t *stage, const uint8_t *tab, int wave, int lane) {
+
+AMLA_DEV float dot2_bf16(uint32_t a, float acc) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 v = __builtin_bit_cast(bf16x2, a);
+  return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
+}
+
+template <int CTRL>
+AMLA_DEV float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Wave w prepares the 8 rows it copied, 8 lanes per row (lane q of a row
+// reads 16 B chunks q, q+8, ..: eight lanes cover 128 contiguous bytes):
+//   r_t = rsqrt(mean(c_t^2) + eps) (rms_norm's factor, inference/ops.py:10-12)
+//     goes to the stage's rt array; the latent row stays raw;
+//   the rope key is rotated in fp32 and rounded to bf16 (inference/ops.py:93-97).
+AMLA_DEV void prepare_own_rows(uint8_t *stage, const uint8_t *tab, int wave, int lane, float eps) {
   const int row = wave * 8 + (lane >> 3), q = lane & 7;
+  uint8_t *rp = stage + row * (KROW * 2);
+  u32x4 v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const u32x4 *>(rp + (q + 8 * i) * 16);
   const u32x4 raw = *reinterpret_cast<const u32x4 *>(stage + K_BYTES + row * (ROPE * 2) + q * 16);
   const f32x4 c0 = *reinterpret_cast<const f32x4 *>(tab + row * (ROPE * 4) + q * 32);
   const f32x4 c1 = *reinterpret_cast<const f32x4 *>(tab + row * (ROPE * 4) + q * 32 + 16);
-  u32x4 r;
-  r.x = rot_pair(raw.x, c0.x, c0.y);
-  r.y = rot_pair(raw.y, c0.z, c0.w);
-  r.z = rot_pair(raw.z, c1.x, c1.y);
-  r.w = rot_pair(raw.w, c1.z, c1.w);
-  *reinterpret_cast<u32x4 *>(stage + row * (KROW * 2) + (LORA + q * 8) * 2) = r;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    ss = dot2_bf16(v[i].x, ss);
+    ss = dot2_bf16(v[i].y, ss);
+    ss = dot2_bf16(v[i].z, ss);
+    ss = dot2_bf16(v[i].w, ss);
+  }
+  // sum over the 8 lanes of the row: quad xor 1, xor 2, then the other quad
+  ss += dpp_f32<0xB1>(ss);   // quad_perm [1,0,3,2]
+  ss += dpp_f32<0x4E>(ss);   // quad_perm [2,3,0,1]
+  ss += dpp_f32<0x141>(ss);  // row_half_mirror
+  if (q == 0) *reinterpret_cast<float *>(stage + RT_OFF + row * 4) = rsqrtf(ss * (1.f / LORA) + eps);
+  u32x4 k;
+  k.x = rot_pair(raw.x, c0.x, c0.y);
+  k.y = rot_pair(raw.y, c0.z, c0.w);
+  k.z = rot_pair(raw.z, c1.x, c1.y);
+  k.w = rot_pair(raw.w, c1.z, c1.w);
+  *reinterpret_cast<u32x4 *>(rp + (LORA + q * 8) * 2) = k;
 }
 
 template <int N>
@@ -214,26 +250,22 @@ AMLA_DEV float max_lane_groups(float v) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-AMLA_DEV float dot2_bf16(uint32_t a, float acc) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  const bf16x2 v = __builtin_bit_cast(bf16x2, a);
-  return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
-}
 
-// Grid (splits, B), 256 threads, one workgroup per CU (~138 KB of LDS).
-// Wave w owns heads 32w .. 32w+31.  Per tile of 32 cache rows:
+// Grid (splits, B), 256 threads, one workgroup per CU (~148 KB of LDS).
+// Scores: wave w owns heads 32w .. 32w+31; values: wave w owns latent columns
+// 128w .. 128w+127 of every head.  Per tile of 32 cache rows:
+//   each wave computes r_t of its 8 copied rows and rotates their rope keys,
+//     one tile ahead of use;
 //   S^T (t x head) = K_tile (32 x 576) . Q^T with the tile rows as the MFMA M
 //     dimension, so each lane ends with 8 scores of one head (its column);
-//     18 K steps of 32 (16 latent, 2 rotated rope), A fragments read from LDS
-//     three steps ahead;
-//   r_t = rsqrt(mean(c_t^2) + eps) from the same A fragments (v_dot2), summed
-//     over the four lane groups with lane swaps, moved to the C layout with
-//     one round of lane permutes and applied before the rope K steps;
+//     18 K steps of 32 (16 latent, then r_t applied, 2 rotated rope), A
+//     fragments read from LDS three steps ahead;
 //   p = 2^(s - m_ref): m_ref is the head's max over the split's first tile and
 //     stays fixed, so O^T is only ever touched by MFMA (no rescaling); a head
 //     whose later tile exceeds m_ref by REF_HEADROOM is flagged instead;
-//   O^T (512 x 32 heads, fp32) += C^T (512 x t) . P^T, C^T by transpose reads
-//     of the same tile, P^T = the score registers (p * r_t as bf16).
+//   P^T (p * r_t as bf16) of the wave's heads goes to LDS; after a barrier
+//   O^T (128 latent x 128 heads, fp32) += C^T (128 x t) . P^T (t x 128), C^T
+//     by transpose reads of the wave's 128 columns of the raw tile.
 // Registers: O^T takes 256 accumulators, the query fragments 144; the loop
 // must not spill (a scratch reload would wait for every copy in flight),
 // which is why the copies use scalar bases and there is no rescaling path.
@@ -266,9 +298,11 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
     for (int ks = 0; ks < QKD / 32; ++ks) qf[nt][ks] = as_bf16x8(ldg16(qr + ks * 32));
   }
 
-  f32x4 o[LORA / 16][2];
+  f32x4 o[8][8];  // O^T: latent 128*wave + 16*mt + .., heads 16*nt + ..
 #pragma unroll
-  for (int mt = 0; mt < LORA / 16; ++mt) o[mt][0] = o[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) o[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_ref[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
   bool bad[2] = {false, false};
 
@@ -282,7 +316,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
     } else {
       wait_vmcnt<0>();
     }
-    rotate_own_rows(smem, smem + TAB_OFF + (tb & 1) * TAB_BYTES, wave, lane);
+    prepare_own_rows(smem, smem + TAB_OFF + (tb & 1) * TAB_BYTES, wave, lane, p.eps);
     __syncthreads();
     bool have_ref = false;
     for (int tile = tb; tile < te; ++tile) {
@@ -305,18 +339,20 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
 #define AMLA_RDA(dst, S, MT) \
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(kaddr), "i"(((MT) * 16 * KROW + (S) * 32) * 2))
       f32x4 sc[2][2];
-      float ssq[2] = {0.f, 0.f};
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) sc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // r_t of the lane's C-layout rows 4*lg + r (mt 0) and 16 + 4*lg + r (mt 1)
+      f32x4 rc[2];
+      rc[0] = *reinterpret_cast<const f32x4 *>(cur + RT_OFF + (4 * lg) * 4);
+      rc[1] = *reinterpret_cast<const f32x4 *>(cur + RT_OFF + (16 + 4 * lg) * 4);
       u32x4 ab[SD][2];
 #pragma unroll
       for (int d = 0; d < SD; ++d) {
         AMLA_RDA(ab[d][0], d, 0);
         AMLA_RDA(ab[d][1], d, 1);
       }
-      float rc[2][4];
 #pragma unroll
       for (int ks = 0; ks < NSTEP; ++ks) {
         const int c = ks % SD;
@@ -325,30 +361,15 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
         else if (later == 1) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
         else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
         if (ks == LORA / 32) {
-          // r_t: full sum for row mt*16+li over the 4 lane groups, then to the
-          // C layout (lane (head, lg) holds rows mt*16 + 4*lg + r) and applied
-          // to the latent part of the scores
+          // latent part complete: apply r_t before the rope K steps
 #pragma unroll
-          for (int mt = 0; mt < 2; ++mt) {
-            const float rrow = rsqrtf(sum_lane_groups(ssq[mt]) * (1.f / LORA) + p.eps);
+          for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) rc[mt][r] = __shfl(rrow, 4 * lg + r, 64);
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-              for (int r = 0; r < 4; ++r) sc[mt][nt][r] *= rc[mt][r];
-          }
+            for (int nt = 0; nt < 2; ++nt) sc[mt][nt] *= rc[mt];
         }
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-          const u32x4 cur_a = ab[c][mt];
-          if (ks < LORA / 32) {
-            ssq[mt] = dot2_bf16(cur_a.x, ssq[mt]);
-            ssq[mt] = dot2_bf16(cur_a.y, ssq[mt]);
-            ssq[mt] = dot2_bf16(cur_a.z, ssq[mt]);
-            ssq[mt] = dot2_bf16(cur_a.w, ssq[mt]);
-          }
-          const bf16x8 a = as_bf16x8(cur_a);
+          const bf16x8 a = as_bf16x8(ab[c][mt]);
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt) sc[mt][nt] = mfma16(a, qf[nt][ks], sc[mt][nt]);
         }
@@ -360,28 +381,10 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
 #undef AMLA_RDA
       __builtin_amdgcn_sched_barrier(0);
 
-      // ---- O^T (latent x head) += C^T (latent x t) . P^T (t x head); C^T by
-      // transpose reads: within a 16-lane group, lane s addresses row
-      // t0 + s/4, columns c0 + 4(s%4) .. +3 and lane L receives
-      // C[t0 .. t0+3][c0 + L]; t0 = 4*lg and 16 + 4*lg match P^T's rows.
-      // Outputs are early-clobber (two reads share one address).  PV_DEPTH
-      // steps are in flight; the first ones are issued before the softmax so
-      // their latency hides under it.
-      constexpr int PV_DEPTH = 4;
-      const int s16 = lane & 15;
-      const uint32_t a0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-          (__attribute__((address_space(3))) const uint16_t *)(K + (4 * lg + (s16 >> 2)) * KROW + 4 * (s16 & 3))));
-      u32x2 t0[PV_DEPTH], t1[PV_DEPTH];
-#define AMLA_TR(dst0, dst1, MT)                                                                            \
-  asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"               \
-               : "=&v"(dst0), "=&v"(dst1)                                                                \
-               : "v"(a0), "i"((MT) * 32), "i"((MT) * 32 + 16 * KROW * 2))
-#pragma unroll
-      for (int d = 0; d < PV_DEPTH; ++d) AMLA_TR(t0[d], t1[d], d);
-
-      // ---- probabilities relative to the head's fixed reference max
+      // ---- probabilities relative to the head's fixed reference max; r_t of
+      // the lane's rows 4*lg + r (mt 0) and 16 + 4*lg + r (mt 1)
       const int tbase = tile * TT;
-      bf16x8 pf[2];
+      u32x4 pk[2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         float sv[8];
@@ -402,30 +405,69 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
         float lsum = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float pe = (sv[e] == -INFINITY) ? 0.f : exp2f(sv[e] - m_ref[nt]);
+          const float pe = __builtin_amdgcn_exp2f(sv[e] - m_ref[nt]);  // v_exp_f32: 2^-inf = 0
           lsum += pe;
           pv[e] = pe * rc[e >> 2][e & 3];
         }
         l_run[nt] += lsum;
-        const u32x4 pk = {pack_bf16(pv[0], pv[1]), pack_bf16(pv[2], pv[3]), pack_bf16(pv[4], pv[5]),
-                          pack_bf16(pv[6], pv[7])};
-        pf[nt] = as_bf16x8(pk);
+        pk[nt] = u32x4{pack_bf16(pv[0], pv[1]), pack_bf16(pv[2], pv[3]), pack_bf16(pv[4], pv[5]),
+                       pack_bf16(pv[6], pv[7])};
       }
       have_ref = true;
 
+      // ---- P^T to LDS: row = head, bf16 slot 8*lg + j holds t = 4*lg + j
+      // (j < 4) or 16 + 4*lg + j - 4: exactly this lane's eight scores, and the
+      // k order of the transpose reads below
 #pragma unroll
-      for (int mt = 0; mt < LORA / 16; ++mt) {
+      for (int nt = 0; nt < 2; ++nt)
+        *reinterpret_cast<u32x4 *>(smem + P_OFF + (head0 + nt * 16 + li) * PROW + lg * 16) = pk[nt];
+      asm volatile("" ::: "memory");  // the P^T stores stay before the reads counted below
+
+      // ---- O^T (latent x head) += C^T (latent x t) . P^T (t x head).  C^T by
+      // transpose reads: within a 16-lane group, lane s addresses row
+      // t0 + s/4, columns c0 + 4(s%4) .. +3 and lane L receives
+      // C[t0 .. t0+3][c0 + L]; t0 = 4*lg and 16 + 4*lg match P^T's k order.
+      // Outputs are early-clobber (two reads share one address).  PV_DEPTH
+      // column blocks are in flight; the first ones are issued before the
+      // barrier that publishes P^T.
+      constexpr int PV_DEPTH = 3;
+      const int s16 = lane & 15;
+      const uint32_t a0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+          (__attribute__((address_space(3))) const uint16_t *)(K + (4 * lg + (s16 >> 2)) * KROW + wave * 128 +
+                                                                4 * (s16 & 3))));
+      u32x2 t0[PV_DEPTH], t1[PV_DEPTH];
+#define AMLA_TR(dst0, dst1, MT)                                                                            \
+  asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"               \
+               : "=&v"(dst0), "=&v"(dst1)                                                                \
+               : "v"(a0), "i"((MT) * 32), "i"((MT) * 32 + 16 * KROW * 2))
+#pragma unroll
+      for (int d = 0; d < PV_DEPTH; ++d) AMLA_TR(t0[d], t1[d], d);
+      // P^T writes done (the 2*PV_DEPTH reads after them may stay in flight)
+      asm volatile("s_waitcnt lgkmcnt(6)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      const uint32_t paddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+          (__attribute__((address_space(3))) const uint8_t *)(smem + P_OFF + li * PROW + lg * 16)));
+      u32x4 pb[8];
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt)
+        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(pb[nt]) : "v"(paddr), "i"(nt * 16 * PROW));
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(pb[0]), "+v"(pb[1]), "+v"(pb[2]), "+v"(pb[3]), "+v"(pb[4]), "+v"(pb[5]), "+v"(pb[6]),
+                     "+v"(pb[7]), "+v"(t0[0]), "+v"(t1[0])::"memory");
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
         const int c = mt % PV_DEPTH;
-        // reads of steps mt+1 .. min(mt+DEPTH-1, last) may stay in flight
-        const int ahead = (LORA / 16 - 1 - mt) < (PV_DEPTH - 1) ? (LORA / 16 - 1 - mt) : (PV_DEPTH - 1);
-        if (ahead == 3) asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
-        else if (ahead == 2) asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
-        else if (ahead == 1) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
-        else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
+        const int ahead = (7 - mt) < (PV_DEPTH - 1) ? (7 - mt) : (PV_DEPTH - 1);
+        if (mt > 0) {
+          if (ahead == 2) asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
+          else if (ahead == 1) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
+          else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
+        }
         const bf16x8 a = as_bf16x8(u32x4{t0[c].x, t0[c].y, t1[c].x, t1[c].y});
-        o[mt][0] = mfma16(a, pf[0], o[mt][0]);
-        o[mt][1] = mfma16(a, pf[1], o[mt][1]);
-        if (mt + PV_DEPTH < LORA / 16) AMLA_TR(t0[c], t1[c], mt + PV_DEPTH);
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) o[mt][nt] = mfma16(a, as_bf16x8(pb[nt]), o[mt][nt]);
+        if (mt + PV_DEPTH < 8) AMLA_TR(t0[c], t1[c], mt + PV_DEPTH);
       }
 #undef AMLA_TR
       __builtin_amdgcn_sched_barrier(0);
@@ -434,8 +476,8 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       if (tile + 1 < te) {
         if (tile + 2 < te) wait_vmcnt<TILE_DMA>();
         else wait_vmcnt<0>();
-        rotate_own_rows(smem + ((it + 1) % NST) * STAGE_BYTES, smem + TAB_OFF + ((tile + 1) & 1) * TAB_BYTES, wave,
-                        lane);
+        prepare_own_rows(smem + ((it + 1) % NST) * STAGE_BYTES, smem + TAB_OFF + ((tile + 1) & 1) * TAB_BYTES, wave,
+                         lane, p.eps);
       }
       // barrier without a memory fence: a fence would also wait for the copy
       // of the tile after next; LDS writes (rotated keys) are drained by hand
@@ -445,7 +487,8 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
     }
   }
 
-  // ---- partial results of this split
+  // ---- partial results of this split: (m, l) of the wave's heads, O of its
+  // latent columns for every head
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     float l = l_run[nt];
@@ -457,9 +500,13 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       p.part_ml[row * 2] = m_ref[nt];
       p.part_ml[row * 2 + 1] = bad[nt] ? -1.f : l;
     }
-    float *dst = p.part_o + row * LORA + 4 * lg;
+  }
 #pragma unroll
-    for (int mt = 0; mt < LORA / 16; ++mt) *reinterpret_cast<f32x4 *>(dst + mt * 16) = o[mt][nt];
+  for (int nt = 0; nt < 8; ++nt) {
+    const size_t row = ((size_t)b * p.splits + split) * HEADS + nt * 16 + li;
+    float *dst = p.part_o + row * LORA + wave * 128 + 4 * lg;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<f32x4 *>(dst + mt * 16) = o[mt][nt];
   }
 }
 
