@@ -45,16 +45,20 @@ struct GemvParams {
   int seq_len;          // S: position of row m is pos[m / S] + m % S
   const float *rope_table;
   int head_dim, nope;   // QROPE
+  float *part;          // fp32 partial sums of the K parts (GemvPlan::part_bytes), else unused
 };
 
 struct GemvPlan {
-  int rt;      // 16-row tiles per workgroup
-  int nw;      // waves per workgroup (split of K inside the workgroup)
-  int groups;  // workgroups
+  int bw;            // 128-wide K blocks per wave
+  int kparts;        // K parts (workgroups per row group); > 1 needs GemvParams::part
+  int rg;            // 16-row tiles per workgroup
+  int groups;        // workgroups
+  size_t part_bytes; // fp32 partial sums (kparts * M * N * 4) when kparts > 1
 };
 
 GemvPlan plan_gemv(int M, int N, int K);
-// Launches the skinny GEMM for M <= 64 (N % 16 == 0, K % 128 == 0, 16-byte aligned rows).
+// Launches the skinny GEMM for M <= 64 (N % 16 == 0, K % 128 == 0, 16-byte aligned rows);
+// p.part must hold plan.part_bytes when plan.kparts > 1.
 int launch_gemv(const GemvParams &p, int mode, const GemvPlan &plan, hipStream_t stream);
 
 // Large-M fp8 GEMM with the same modes (M > 64).

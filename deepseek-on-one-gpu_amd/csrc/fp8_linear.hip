@@ -136,163 +136,250 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
 
 // ---------------------------------------------------------------- skinny GEMM
 
-// Workgroup = NW waves over one group of RT 16-row tiles; wave w takes the
-// K blocks kb = w, w + NW, ...; partials reduce through LDS in wave order, so
-// results are deterministic and no workgroup depends on another.
-template <int RT, int MT, int NW, int MODE>
-__global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvParams p) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Streaming skinny GEMM for M <= 64 (decode projections).  The weight matrix
+// is cut into units of RG consecutive 16-row tiles x one K part of 4*BW
+// 128-wide blocks; a workgroup (4 waves) owns one unit and wave w the blocks
+// BW*w .. BW*w+BW-1 of the part.  A wave holds the x fragments of its blocks
+// in registers for the whole unit and streams the weight rows tile after tile
+// (the next tile's loads are in flight while the current one is converted and
+// multiplied): 2*BW KB of weights per tile and wave, no x traffic per tile.
+// The four waves' partial tiles are summed through LDS in wave order; with
+// one K part the sum goes through the epilogue, otherwise into fp32 partials
+// [part][M][N] that gemv_finish sums in part order (deterministic, no atomics
+// and no workgroup depends on another).
+//
+// Within a block, lane (row l%16, group g = l/16) holds weight bytes
+// 16g .. 16g+15 and 64+16g .. 64+16g+15 of its row: each 16 B load covers
+// whole 64 B sectors of 16 rows.  The MFMA K order is permuted accordingly
+// and the x fragments follow the same order.
+constexpr int GEMV_MAX_PARTS = 32;  // K parts summed by gemv_finish
+constexpr int GEMV_MAX_RG = 16;     // 16-row tiles per workgroup
+
+template <int MT, int BW, int MODE>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kparts) {
+  // wave index in a scalar register: block ranges, scale loads and the
+  // per-block branches below stay scalar (a vector scale load would make the
+  // compiler wait for every weight load in flight)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 15, lg = lane >> 4;
-  const int tile0 = blockIdx.x * RT;
   const int KB = p.K >> 7;
+  const int ntiles = p.N >> 4;
+  const int part = blockIdx.x % kparts;
+  const int tile_begin = (blockIdx.x / kparts) * rg;
+  const int tile_end = min(tile_begin + rg, ntiles);
+  const int kb0 = part * 4 * BW + wave * BW;            // first block of this wave
+  const int nb = max(0, min(BW, KB - kb0));              // blocks of this wave (wave-uniform)
 
-  const uint8_t *wrow[RT];
-  const float *srow[RT];
-  bool rvalid[RT];
+  // x fragments of the wave's blocks: [block][m tile][MFMA of the block]
+  bf16x8 xf[BW][MT][4];
 #pragma unroll
-  for (int r = 0; r < RT; ++r) {
-    const int nt = (tile0 + r) * 16;
-    rvalid[r] = nt < p.N;
-    const bool seg1 = (MODE == GEMV_QKVA) && nt >= p.n_split;
-    const int ntl = seg1 ? nt - p.n_split : nt;
-    const uint8_t *wb = seg1 ? p.w1 : p.w0;
-    const float *sb = seg1 ? p.s1 : p.s0;
-    wrow[r] = wb + (size_t)(rvalid[r] ? ntl + li : 0) * p.K + lg * 32;
-    srow[r] = sb + (size_t)(rvalid[r] ? (ntl >> 7) : 0) * KB;
-  }
-  const uint16_t *xrow[MT];
-  bool mvalid[MT];
+  for (int j = 0; j < BW; ++j)
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    const int m = t * 16 + li;
-    mvalid[t] = m < p.M;
-    xrow[t] = p.x + (size_t)(mvalid[t] ? m : 0) * p.ldx + lg * 32;
-  }
-
-  f32x4 acc[RT][MT];
-#pragma unroll
-  for (int r = 0; r < RT; ++r)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // block kb + NW is loaded while block kb is computed (a wave otherwise sits
-  // out one memory latency per 2 KB of weights)
-  u32x4 a0[2][RT], a1[2][RT];
-  bf16x8 xb[2][MT][4];
-  auto load_block = [&](int kb, int buf) {
-#pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      if (rvalid[r]) {
-        a0[buf][r] = ldg16_nt(wrow[r] + (size_t)kb * 128);
-        a1[buf][r] = ldg16_nt(wrow[r] + (size_t)kb * 128 + 16);
-      } else {
-        a0[buf][r] = u32x4{0, 0, 0, 0};
-        a1[buf][r] = u32x4{0, 0, 0, 0};
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
+    for (int t = 0; t < MT; ++t) {
+      const int m = t * 16 + li;
+      const bool ok = j < nb && m < p.M;
+      const uint16_t *xr = p.x + (size_t)(ok ? m : 0) * p.ldx + (size_t)(kb0 + (ok ? j : 0)) * 128 + lg * 16;
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        xb[buf][t][u] = mvalid[t] ? as_bf16x8(ldg16(xrow[t] + kb * 128 + u * 8)) : as_bf16x8(u32x4{0, 0, 0, 0});
-  };
-  auto compute_block = [&](int kb, int buf) {
+        xf[j][t][u] = ok ? as_bf16x8(ldg16(xr + (u >> 1) * 64 + (u & 1) * 8)) : as_bf16x8(u32x4{0, 0, 0, 0});
+    }
+
+  __shared__ f32x4 red[2][4][MT][64];
+  // reduced tiles of the unit, epilogue deferred to the end (one round of
+  // epilogue loads - rope table, residual - instead of one per tile)
+  __shared__ f32x4 done[GEMV_MAX_RG][MT][64];
+  // a tile's weights and block scales are loaded together, one tile ahead,
+  // unconditionally (the last trip and absent blocks re-read valid data that
+  // is not used): with no load under a branch the compiler's wait for the
+  // current tile never waits for the next one's loads
+  constexpr int NBUF = 3;  // tiles in flight: the current one and two ahead
+  u32x4 wv[NBUF][BW][2];
+  float sv[NBUF][BW];
+  const uint32_t woff = (uint32_t)(li * p.K + lg * 16);
+  auto load_tile = [&](int tile, int buf) {
+    const int nt = min(tile, tile_end - 1) * 16;
+    const bool seg1 = (MODE == GEMV_QKVA) && nt >= p.n_split;
+    const uint8_t *wb = seg1 ? p.w1 : p.w0;
+    const int nl = seg1 ? nt - p.n_split : nt;
+    // uniform tile base + unsigned 32-bit lane offset: scalar-base loads, no
+    // per-tile address registers
+    const uint8_t *tb = wb + (size_t)nl * p.K;
+    const float *sr = (seg1 ? p.s1 : p.s0) + (size_t)(nl >> 7) * KB;
 #pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      const float s = rvalid[r] ? srow[r][kb] : 0.f;
-      bf16x8 w0, w1, w2, w3;
-      fp8x16_to_bf16x16(a0[buf][r], w0, w1);
-      fp8x16_to_bf16x16(a1[buf][r], w2, w3);
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        f32x4 c = {0.f, 0.f, 0.f, 0.f};
-        c = mfma16(w0, xb[buf][t][0], c);
-        c = mfma16(w1, xb[buf][t][1], c);
-        c = mfma16(w2, xb[buf][t][2], c);
-        c = mfma16(w3, xb[buf][t][3], c);
-        acc[r][t] += s * c;
-      }
+    for (int j = 0; j < BW; ++j) {
+      const int kb = min(kb0 + j, KB - 1);
+      sv[buf][j] = sr[kb];
+      wv[buf][j][0] = ldg16_nt(tb + (size_t)kb * 128 + woff);
+      wv[buf][j][1] = ldg16_nt(tb + (size_t)kb * 128 + 64 + woff);
     }
   };
-  if (wave < KB) load_block(wave, 0);
-  int kb = wave;
-  for (; kb + NW < KB; kb += 2 * NW) {
-    load_block(kb + NW, 1);
-    compute_block(kb, 0);
-    if (kb + 2 * NW < KB) load_block(kb + 2 * NW, 0);
-    compute_block(kb + NW, 1);
+  auto do_tile = [&](int tile, int buf) {
+    load_tile(tile + NBUF - 1, (buf + NBUF - 1) % NBUF);
+    const int nt = tile * 16;
+    f32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < BW; ++j) {
+      if (j < nb) {
+        const float sc = sv[buf][j];
+        bf16x8 w0, w1, w2, w3;
+        fp8x16_to_bf16x16(wv[buf][j][0], w0, w1);
+        fp8x16_to_bf16x16(wv[buf][j][1], w2, w3);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          f32x4 c = {0.f, 0.f, 0.f, 0.f};
+          c = mfma16(w0, xf[j][t][0], c);
+          c = mfma16(w1, xf[j][t][1], c);
+          c = mfma16(w2, xf[j][t][2], c);
+          c = mfma16(w3, xf[j][t][3], c);
+          acc[t] += sc * c;
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) red[tile & 1][wave][t][lane] = acc[t];
+    __syncthreads();
+    // MT * 64 lanes of results (4 outputs each) per tile; thread idx sums the
+    // four waves in order
+    for (int idx = threadIdx.x; idx < MT * 64; idx += 256) {
+      const int t = idx >> 6, ln = idx & 63;
+      const int m = t * 16 + (ln & 15);
+      const int n = nt + 4 * (ln >> 4);
+      if (m >= p.M) continue;
+      f32x4 v = red[tile & 1][0][t][ln];
+      v += red[tile & 1][1][t][ln];
+      v += red[tile & 1][2][t][ln];
+      v += red[tile & 1][3][t][ln];
+      if (kparts == 1) done[tile - tile_begin][t][ln] = v;
+      else *reinterpret_cast<f32x4 *>(p.part + ((size_t)part * p.M + m) * p.N + n) = v;
+    }
+    // red[tile & 1] is rewritten two tiles later, after the next barrier
+  };
+  // NBUF tiles per trip: the register buffer index stays a constant
+  if (tile_begin < tile_end) {
+#pragma unroll
+    for (int b = 0; b < NBUF - 1; ++b) load_tile(tile_begin + b, b);
   }
-  if (kb < KB) compute_block(kb, 0);
+  for (int tile = tile_begin; tile < tile_end; tile += NBUF) {
+    do_tile(tile, 0);
+    if (tile + 1 < tile_end) do_tile(tile + 1, 1);
+    if (tile + 2 < tile_end) do_tile(tile + 2, 2);
+  }
+  if (kparts == 1) {
+    __syncthreads();
+    const int nitems = (tile_end - tile_begin) * MT * 64;
+    for (int idx = threadIdx.x; idx < nitems; idx += 256) {
+      const int tl = idx / (MT * 64), t = (idx >> 6) % MT, ln = idx & 63;
+      const int m = t * 16 + (ln & 15);
+      const int n = (tile_begin + tl) * 16 + 4 * (ln >> 4);
+      if (m < p.M) store4<MODE>(p, m, n, done[tl][t][ln]);
+    }
+  }
+}
 
-  __shared__ f32x4 red[NW][RT * MT][64];
+// Sums the K parts of gemv_kernel in part order and applies the epilogue.
+// All parts are loaded before the first add (independent loads in flight).
+template <int MODE>
+__global__ __launch_bounds__(64) void gemv_finish(GemvParams p, int kparts) {
+  const int64_t total = (int64_t)p.M * (p.N >> 2);
+  const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (i >= total) return;
+  const int m = (int)(i / (p.N >> 2));
+  const int n = (int)(i % (p.N >> 2)) * 4;
+  f32x4 v[GEMV_MAX_PARTS];
 #pragma unroll
-  for (int r = 0; r < RT; ++r)
+  for (int q = 0; q < GEMV_MAX_PARTS; ++q)
+    if (q < kparts) v[q] = *reinterpret_cast<const f32x4 *>(p.part + ((size_t)q * p.M + m) * p.N + n);
+  f32x4 s = v[0];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) red[wave][r * MT + t][lane] = acc[r][t];
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < RT * MT * 64; idx += NW * 64) {
-    const int rt = idx >> 6, ln = idx & 63;
-    const int r = rt / MT, t = rt % MT;
-    const int m = t * 16 + (ln & 15);
-    const int n = (tile0 + r) * 16 + 4 * (ln >> 4);
-    if (m >= p.M || n >= p.N) continue;
-    f32x4 v = red[0][rt][ln];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) v += red[w][rt][ln];
-    store4<MODE>(p, m, n, v);
-  }
+  for (int q = 1; q < GEMV_MAX_PARTS; ++q)
+    if (q < kparts) s += v[q];
+  store4<MODE>(p, m, n, s);
 }
 
 GemvPlan plan_gemv(int M, int N, int K) {
   GemvPlan pl;
-  const int tiles = (N + 15) / 16;
+  const int tiles = N / 16;
   const int KB = K / 128;
-  const int MT = (M + 15) / 16;
-  // two row tiles per wave halve the x traffic once there are enough rows
-  pl.rt = (M > 4 && tiles >= 2 * 256) ? 2 : 1;
-  pl.groups = (tiles + pl.rt - 1) / pl.rt;
-  // waves per workgroup: enough waves in flight to cover the memory latency
-  // (~24 resident waves per CU at this kernel's register count) while every
-  // workgroup stays resident, and at least two K blocks per wave
-  int nw = 16;
-  while (nw > 4 && ((int64_t)pl.groups * nw > 256 * 24 || KB < 2 * nw)) nw /= 2;
-  while (nw > 4 && nw * pl.rt * (MT > 2 ? 4 : MT) > 64) nw /= 2;
-  pl.nw = nw;
+  const int MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  // blocks per wave: x fragments take 16 * BW * MT registers (<= 64).  One K
+  // part when it fits (no finishing pass), else the BW wasting the fewest
+  // wave-blocks, larger BW on ties
+  const int bw_max = MT == 1 ? 4 : (MT == 2 ? 2 : 1);
+  int bw = bw_max;
+  if (KB <= 4 * bw_max) {
+    while (bw > 1 && 4 * (bw / 2) >= KB) bw /= 2;
+  } else {
+    int best_waste = 1 << 30;
+    for (int b = bw_max; b >= 1; b /= 2) {
+      const int waste = ((KB + 4 * b - 1) / (4 * b)) * 4 * b - KB;
+      if (waste < best_waste) {
+        best_waste = waste;
+        bw = b;
+      }
+    }
+  }
+  pl.bw = bw;
+  pl.kparts = (KB + 4 * bw - 1) / (4 * bw);  // launch_gemv rejects more than GEMV_MAX_PARTS
+  // tiles per unit: fewest rounds of 256 workgroups x tiles per unit, then
+  // the largest unit (fewer x reloads); <= 16 tiles
+  int best_rg = 1;
+  int64_t best_cost = INT64_MAX;
+  for (int rg = 1; rg <= GEMV_MAX_RG; ++rg) {
+    const int64_t units = (int64_t)((tiles + rg - 1) / rg) * pl.kparts;
+    const int64_t cost = ((units + 255) / 256) * rg;
+    if (cost <= best_cost) {
+      best_cost = cost;
+      best_rg = rg;
+    }
+  }
+  pl.rg = best_rg;
+  pl.groups = ((tiles + pl.rg - 1) / pl.rg) * pl.kparts;
+  pl.part_bytes = pl.kparts > 1 ? (size_t)pl.kparts * M * N * 4 : 0;
   return pl;
 }
 
-template <int RT, int MT, int NW>
+template <int MT, int BW>
 static void launch_cfg(const GemvParams &p, int mode, const GemvPlan &pl, hipStream_t st) {
   dim3 grid(pl.groups);
   switch (mode) {
-    case GEMV_PLAIN: gemv_kernel<RT, MT, NW, GEMV_PLAIN><<<grid, NW * 64, 0, st>>>(p); break;
-    case GEMV_RESID: gemv_kernel<RT, MT, NW, GEMV_RESID><<<grid, NW * 64, 0, st>>>(p); break;
-    case GEMV_QKVA: gemv_kernel<RT, MT, NW, GEMV_QKVA><<<grid, NW * 64, 0, st>>>(p); break;
-    default: gemv_kernel<RT, MT, NW, GEMV_QROPE><<<grid, NW * 64, 0, st>>>(p); break;
+    case GEMV_PLAIN: gemv_kernel<MT, BW, GEMV_PLAIN><<<grid, 256, 0, st>>>(p, pl.rg, pl.kparts); break;
+    case GEMV_RESID: gemv_kernel<MT, BW, GEMV_RESID><<<grid, 256, 0, st>>>(p, pl.rg, pl.kparts); break;
+    case GEMV_QKVA: gemv_kernel<MT, BW, GEMV_QKVA><<<grid, 256, 0, st>>>(p, pl.rg, pl.kparts); break;
+    default: gemv_kernel<MT, BW, GEMV_QROPE><<<grid, 256, 0, st>>>(p, pl.rg, pl.kparts); break;
   }
-}
-
-template <int RT, int MT>
-static void launch_rt_mt(const GemvParams &p, int mode, const GemvPlan &pl, hipStream_t st) {
-  if (pl.nw == 16) launch_cfg<RT, MT, 16>(p, mode, pl, st);
-  else if (pl.nw == 8) launch_cfg<RT, MT, 8>(p, mode, pl, st);
-  else launch_cfg<RT, MT, 4>(p, mode, pl, st);
-}
-
-template <int RT>
-static void launch_rt(const GemvParams &p, int mode, const GemvPlan &pl, hipStream_t st) {
-  const int MT = (p.M + 15) / 16;
-  if (MT == 1) launch_rt_mt<RT, 1>(p, mode, pl, st);
-  else if (MT == 2) launch_rt_mt<RT, 2>(p, mode, pl, st);
-  else launch_rt_mt<RT, 4>(p, mode, pl, st);
 }
 
 int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t st) {
   if (p0.M < 1 || p0.M > 64) return fail(AMLA_EINVAL, "skinny fp8 GEMM needs 1 <= M <= 64 (got %d)", p0.M);
   if (p0.N % 16 || p0.K % 128)
     return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM needs N %% 16 == 0 and K %% 128 == 0 (N=%d K=%d)", p0.N, p0.K);
-  if (pl.rt == 1) launch_rt<1>(p0, mode, pl, st);
-  else launch_rt<2>(p0, mode, pl, st);
+  if (pl.kparts > GEMV_MAX_PARTS)
+    return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM: K=%d is too long for M=%d (more than %d K parts)", p0.K, p0.M,
+                GEMV_MAX_PARTS);
+  if (pl.kparts > 1 && !p0.part) return fail(AMLA_EWORKSPACE, "skinny fp8 GEMM: missing partial-sum workspace");
+  const int MT = p0.M <= 16 ? 1 : (p0.M <= 32 ? 2 : 4);
+  if (MT == 1) {
+    if (pl.bw == 4) launch_cfg<1, 4>(p0, mode, pl, st);
+    else if (pl.bw == 2) launch_cfg<1, 2>(p0, mode, pl, st);
+    else launch_cfg<1, 1>(p0, mode, pl, st);
+  } else if (MT == 2) {
+    if (pl.bw == 2) launch_cfg<2, 2>(p0, mode, pl, st);
+    else launch_cfg<2, 1>(p0, mode, pl, st);
+  } else {
+    launch_cfg<4, 1>(p0, mode, pl, st);
+  }
+  if (pl.kparts > 1) {
+    const int64_t total = (int64_t)p0.M * (p0.N / 4);
+    const unsigned blocks = (unsigned)((total + 63) / 64);
+    switch (mode) {
+      case GEMV_PLAIN: gemv_finish<GEMV_PLAIN><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
+      case GEMV_RESID: gemv_finish<GEMV_RESID><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
+      case GEMV_QKVA: gemv_finish<GEMV_QKVA><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
+      default: gemv_finish<GEMV_QROPE><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
+    }
+  }
   return check_launch("fp8 skinny GEMM");
 }
 
@@ -379,8 +466,8 @@ int amla_fp8_block_dequant(const void *weight, const float *scale_inv, int64_t n
 }
 
 size_t amla_fp8_linear_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-  (void)m; (void)n; (void)k;
-  return 0;
+  if (m < 1 || m > 64 || n <= 0 || k <= 0 || n % 16 || k % 128 || n > INT32_MAX || k > INT32_MAX) return 0;
+  return plan_gemv((int)m, (int)n, (int)k).part_bytes;
 }
 
 int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void *weight,
@@ -408,11 +495,16 @@ int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void
   p.y = reinterpret_cast<uint16_t *>(y);
   p.ldy = (int)ldy;
   p.seq_len = 1;
-  (void)workspace;
-  (void)workspace_bytes;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (m > 64) return launch_gemm(p, GEMV_PLAIN, st);
-  return launch_gemv(p, GEMV_PLAIN, plan_gemv((int)m, (int)n, (int)k), st);
+  const GemvPlan pl = plan_gemv((int)m, (int)n, (int)k);
+  if (pl.part_bytes) {
+    if (!workspace || workspace_bytes < pl.part_bytes || !aligned16(workspace))
+      return fail(AMLA_EWORKSPACE, "fp8_linear: needs %zu bytes of 16-byte aligned workspace (got %zu)", pl.part_bytes,
+                  workspace ? workspace_bytes : (size_t)0);
+    p.part = reinterpret_cast<float *>(workspace);
+  }
+  return launch_gemv(p, GEMV_PLAIN, pl, st);
 }
 
 int amla_rms_norm(const void *x, int64_t rows, int64_t dim, int64_t ldx, const void *gamma, float eps,

@@ -689,7 +689,7 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
 // ---------------------------------------------------------------- orchestration
 
 struct DecodeLayout {
-  size_t xn, qa, qan, q, qbuf, part_ml, part_o, attn, total;
+  size_t xn, qa, qan, q, qbuf, part_ml, part_o, attn, lin, total;
   GemvPlan pa, pb, po;
   int splits, tiles_per_split;
 };
@@ -717,6 +717,7 @@ static DecodeLayout decode_layout(const amla_mla_args &a) {
   L.part_ml = take((size_t)B * L.splits * a.heads * 2 * 4);
   L.part_o = take((size_t)B * L.splits * a.heads * LORA * 4);
   L.attn = take((size_t)B * a.heads * a.v_dim * 2);
+  L.lin = take(std::max(L.pa.part_bytes, std::max(L.pb.part_bytes, L.po.part_bytes)));  // K-part sums of the linears
   L.total = off;
   return L;
 }
@@ -787,6 +788,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pa.kpe = reinterpret_cast<uint16_t *>(a->kpe_cache);
   pa.ckv_bstride = (int64_t)a->max_seq * LORA; pa.kpe_bstride = (int64_t)a->max_seq * ROPE;
   pa.kv_lora = LORA; pa.rope = ROPE; pa.pos = a->positions; pa.seq_len = 1;
+  pa.part = reinterpret_cast<float *>(ws + L.lin);
   if ((rc = launch_gemv(pa, GEMV_QKVA, L.pa, st))) return rc;
 
   // 2. q_a_layernorm (inference/ops.py:130)
@@ -804,6 +806,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pb.y = q; pb.ldy = pb.N;
   pb.pos = a->positions; pb.seq_len = 1; pb.rope = ROPE; pb.rope_table = a->rope_table;
   pb.head_dim = HD; pb.nope = a->qk_nope;
+  pb.part = reinterpret_cast<float *>(ws + L.lin);
   if ((rc = launch_gemv(pb, GEMV_QROPE, L.pb, st))) return rc;
 
   // 4. absorb W_UK into the query
@@ -845,6 +848,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   po.y = reinterpret_cast<uint16_t *>(a->out); po.ldy = a->hidden;
   po.res = reinterpret_cast<const uint16_t *>(a->residual); po.ldr = a->hidden;
   po.seq_len = 1;
+  po.part = reinterpret_cast<float *>(ws + L.lin);
   rc = launch_gemv(po, a->residual ? GEMV_RESID : GEMV_PLAIN, L.po, st);
   mark(ev, NSTAGE, st);
   return rc;

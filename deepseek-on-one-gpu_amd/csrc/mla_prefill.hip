@@ -383,13 +383,14 @@ __global__ __launch_bounds__(256, 1) void flash_kernel(FlashParams p) {
 
 // ---------------------------------------------------------------- orchestration
 
+// p.part must hold the K-part sums of the skinny plan (PrefillLayout::lin)
 static int run_linear(const GemvParams &p, int mode, hipStream_t st) {
   if (p.M <= 64) return launch_gemv(p, mode, plan_gemv(p.M, p.N, p.K), st);
   return launch_gemm(p, mode, st);
 }
 
 struct PrefillLayout {
-  size_t xn, qa, qan, q, kvn, kpe, kvb, attn, total;
+  size_t xn, qa, qan, q, kvn, kpe, kvb, attn, lin, total;
   int Tmax;
 };
 
@@ -408,6 +409,17 @@ static PrefillLayout prefill_layout(const amla_mla_args &a) {
   L.kpe = take((size_t)L.Tmax * a.qk_rope * 2);
   L.kvb = take((size_t)L.Tmax * a.heads * (a.qk_nope + a.v_dim) * 2);
   L.attn = take(M * a.heads * a.v_dim * 2);
+  // K-part sums of the skinny linears (M <= 64)
+  size_t lin = 0;
+  const int HDv = a.qk_nope + a.v_dim;
+  auto need = [&](int m, int n, int k) {
+    if (m <= 64) lin = std::max(lin, plan_gemv(m, n, k).part_bytes);
+  };
+  need((int)M, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
+  need((int)M, a.heads * HD, a.q_lora);
+  need(L.Tmax, a.heads * HDv, a.kv_lora);
+  need((int)M, a.hidden, a.heads * a.v_dim);
+  L.lin = take(lin);
   L.total = off;
   return L;
 }
@@ -470,6 +482,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   uint16_t *attn = reinterpret_cast<uint16_t *>(ws + L.attn);
 
   GemvParams pa = {};
+  pa.part = reinterpret_cast<float *>(ws + L.lin);
   pa.x = x; pa.M = M; pa.ldx = a->hidden;
   pa.w0 = reinterpret_cast<const uint8_t *>(a->w_q_a); pa.s0 = a->s_q_a;
   pa.w1 = reinterpret_cast<const uint8_t *>(a->w_kv_a); pa.s1 = a->s_kv_a;
@@ -486,6 +499,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
     return rc;
 
   GemvParams pb = {};
+  pb.part = reinterpret_cast<float *>(ws + L.lin);
   pb.x = qan; pb.M = M; pb.ldx = a->q_lora;
   pb.w0 = reinterpret_cast<const uint8_t *>(a->w_q_b); pb.s0 = a->s_q_b;
   pb.N = a->heads * HD; pb.K = a->q_lora; pb.n_split = pb.N;
@@ -508,6 +522,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
     kpe_rope_kernel<<<dim3((T * (P_ROPE / 2) + 255) / 256), 256, 0, st>>>(kpe_b, a->rope_table, T, kpe);
     if ((rc = check_launch("kpe rope"))) return rc;
     GemvParams pk = {};
+    pk.part = reinterpret_cast<float *>(ws + L.lin);
     pk.x = kvn; pk.M = T; pk.ldx = a->kv_lora;
     pk.w0 = reinterpret_cast<const uint8_t *>(a->w_kv_b); pk.s0 = a->s_kv_b;
     pk.N = a->heads * (a->qk_nope + a->v_dim); pk.K = a->kv_lora; pk.n_split = pk.N;
@@ -519,6 +534,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   }
 
   GemvParams po = {};
+  po.part = reinterpret_cast<float *>(ws + L.lin);
   po.x = attn; po.M = M; po.ldx = a->heads * a->v_dim;
   po.w0 = reinterpret_cast<const uint8_t *>(a->w_o); po.s0 = a->s_o;
   po.N = a->hidden; po.K = a->heads * a->v_dim; po.n_split = po.N;

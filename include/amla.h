@@ -45,8 +45,10 @@ int amla_fp8_block_dequant(const void *weight, const float *scale_inv, int64_t n
 /* Replaces fp8_linear(x, weight, scale_inv, out_dtype=bf16), inference/ops.py:15-44:
  *   y[i, j] = bf16( sum_k x[i, k] * f32(weight[j, k]) * scale_inv[j/128, k/128] )
  * fp32 accumulation; x (m, k) bf16 with row stride ldx; y (m, n) bf16 with row
- * stride ldy.  `workspace` is reserved (amla_fp8_linear_workspace_bytes
- * returns 0 in this version; NULL is accepted). */
+ * stride ldy.  For m <= 64 a long K is split over workgroups whose fp32
+ * partial sums need `workspace` (16-byte aligned) of
+ * amla_fp8_linear_workspace_bytes(m, n, k) bytes; when that is 0, NULL is
+ * accepted.  Scratch only: no contents carry between calls. */
 int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void *weight,
                     const float *scale_inv, int64_t n, void *y, int64_t ldy, void *workspace,
                     size_t workspace_bytes, void *stream);
