@@ -39,39 +39,45 @@ constexpr int TT = 32;               // cache rows per tile
 
 // ---------------------------------------------------------------- absorb
 
-// One workgroup per (head, group of 8 sequences).  Thread (dg, cc) sums over
-// 32 rows d of W_UK[h] for 8 latent columns c; four row groups reduce in LDS.
+// One workgroup per (head, 128-column quarter of the latent, group of 8
+// sequences).  Thread (dg, cc) sums rows 8*dg .. 8*dg+7 of W_UK[h] (eight
+// independent 8-byte loads in flight) for 8 latent columns; the 16 row groups
+// reduce through LDS.  W_UK[h] = kv_b rows h*256 .. h*256+127 lie in one
+// 128-row scale block.
 __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict__ q,  // (B, H, 192)
                                                      const uint8_t *__restrict__ wkvb,
                                                      const float *__restrict__ skvb,
                                                      const uint16_t *__restrict__ gamma,
                                                      int B, uint16_t *__restrict__ qbuf) {
   constexpr int BB = 8;
-  const int h = blockIdx.x;
-  const int b0 = blockIdx.y * BB;
+  const int h = blockIdx.x, quarter = blockIdx.y;
+  const int b0 = blockIdx.z * BB;
   const int nb = min(BB, B - b0);
   const int tid = threadIdx.x;
-  const int cc = tid & 63, dg = tid >> 6;
+  const int cc = tid & 15, dg = tid >> 4;
+  const int c0 = quarter * 128 + cc * 8;  // this thread's 8 latent columns
   __shared__ float qn[BB][NOPE];
-  __shared__ f32x4 red[4][BB][64][2];
+  __shared__ f32x4 red[16][BB][16][2];
+  const uint8_t *wp = wkvb + ((size_t)h * (NOPE + VD) + dg * 8) * LORA + c0;
+  u32x2 raw[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) raw[d] = ldg8(wp + (size_t)d * LORA);
   for (int e = tid; e < BB * NOPE; e += 256) {
     const int bb = e / NOPE, d = e % NOPE;
     qn[bb][d] = bb < nb ? bf2f(q[((size_t)(b0 + bb) * HEADS + h) * (NOPE + ROPE) + d]) : 0.f;
   }
   __syncthreads();
-  const uint8_t *wp = wkvb + ((size_t)h * (NOPE + VD) + dg * 32) * LORA + cc * 8;
   f32x4 acc[BB][2];
 #pragma unroll
   for (int bb = 0; bb < BB; ++bb) acc[bb][0] = acc[bb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int d = 0; d < 32; ++d) {
-    const u32x2 raw = ldg8(wp + (size_t)d * LORA);
-    const f32x2 w01 = fp8x2_to_f32<false>(raw.x), w23 = fp8x2_to_f32<true>(raw.x);
-    const f32x2 w45 = fp8x2_to_f32<false>(raw.y), w67 = fp8x2_to_f32<true>(raw.y);
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    const f32x2 w01 = fp8x2_to_f32<false>(raw[d].x), w23 = fp8x2_to_f32<true>(raw[d].x);
+    const f32x2 w45 = fp8x2_to_f32<false>(raw[d].y), w67 = fp8x2_to_f32<true>(raw[d].y);
     const f32x4 wa = {w01.x, w01.y, w23.x, w23.y}, wb = {w45.x, w45.y, w67.x, w67.y};
 #pragma unroll
     for (int bb = 0; bb < BB; ++bb) {
-      const float qv = qn[bb][dg * 32 + d];
+      const float qv = qn[bb][dg * 8 + d];
       acc[bb][0] += qv * wa;
       acc[bb][1] += qv * wb;
     }
@@ -82,25 +88,29 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
     red[dg][bb][cc][1] = acc[bb][1];
   }
   __syncthreads();
-  // 256 threads finish 8 sequences x 64 column groups x 2 halves
-  for (int e = tid; e < BB * 64 * 2; e += 256) {
-    const int bb = e / 128, c64 = (e / 2) % 64, half = e & 1;
-    if (bb >= nb) continue;
-    const f32x4 v = red[0][bb][c64][half] + red[1][bb][c64][half] + red[2][bb][c64][half] +
-                    red[3][bb][c64][half];
-    const float sc = skvb[(size_t)(2 * h) * (LORA / 128) + (c64 * 8) / 128];
-    const int c = c64 * 8 + half * 4;
-    const u32x2 g = *reinterpret_cast<const u32x2 *>(gamma + c);
-    u32x2 o = {pack_bf16(v.x * sc * lo_bf(g.x), v.y * sc * hi_bf(g.x)),
-               pack_bf16(v.z * sc * lo_bf(g.y), v.w * sc * hi_bf(g.y))};
-    *reinterpret_cast<u32x2 *>(qbuf + ((size_t)(b0 + bb) * HEADS + h) * QKD + c) = o;
+  // one thread per (sequence, column group, half): sum the 16 row groups in order
+  {
+    const int bb = tid >> 5, c16 = (tid >> 1) & 15, half = tid & 1;
+    if (bb < nb) {
+      f32x4 v = red[0][bb][c16][half];
+#pragma unroll
+      for (int g = 1; g < 16; ++g) v += red[g][bb][c16][half];
+      const int c = quarter * 128 + c16 * 8 + half * 4;
+      const float sc = skvb[(size_t)(2 * h) * (LORA / 128) + quarter];
+      const u32x2 gm = *reinterpret_cast<const u32x2 *>(gamma + c);
+      u32x2 o = {pack_bf16(v.x * sc * lo_bf(gm.x), v.y * sc * hi_bf(gm.x)),
+                 pack_bf16(v.z * sc * lo_bf(gm.y), v.w * sc * hi_bf(gm.y))};
+      *reinterpret_cast<u32x2 *>(qbuf + ((size_t)(b0 + bb) * HEADS + h) * QKD + c) = o;
+    }
   }
   // rope half of the query: copied next to the absorbed latent query
-  for (int e = tid; e < nb * (ROPE / 2); e += 256) {
-    const int bb = e / (ROPE / 2), j = (e % (ROPE / 2)) * 2;
-    const uint32_t v =
-        *reinterpret_cast<const uint32_t *>(q + ((size_t)(b0 + bb) * HEADS + h) * (NOPE + ROPE) + NOPE + j);
-    *reinterpret_cast<uint32_t *>(qbuf + ((size_t)(b0 + bb) * HEADS + h) * QKD + LORA + j) = v;
+  if (quarter == 0) {
+    for (int e = tid; e < nb * (ROPE / 2); e += 256) {
+      const int bb = e / (ROPE / 2), j = (e % (ROPE / 2)) * 2;
+      const uint32_t v =
+          *reinterpret_cast<const uint32_t *>(q + ((size_t)(b0 + bb) * HEADS + h) * (NOPE + ROPE) + NOPE + j);
+      *reinterpret_cast<uint32_t *>(qbuf + ((size_t)(b0 + bb) * HEADS + h) * QKD + LORA + j) = v;
+    }
   }
 }
 
@@ -116,7 +126,7 @@ struct AttnParams {
   int splits, tiles_per_split;
   float scale_log2;  // softmax scale * log2(e)
   float eps;
-  float *part_o;   // (B, splits, H, 512) sum_t p_t r_t c_t, p relative to the split's reference max
+  uint16_t *part_o;  // (B, splits, H, 512) bf16: sum_t p_t r_t c_t, p relative to the split's reference max
   float *part_ml;  // (B, splits, H, 2) reference max (log2 units) and sum of p; sum < 0 marks a
                    // (split, head) whose scores overflowed the reference (recomputed by the combine)
 };
@@ -504,9 +514,11 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     const size_t row = ((size_t)b * p.splits + split) * HEADS + nt * 16 + li;
-    float *dst = p.part_o + row * LORA + wave * 128 + 4 * lg;
+    uint16_t *dst = p.part_o + row * LORA + wave * 128 + 4 * lg;
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<f32x4 *>(dst + mt * 16) = o[mt][nt];
+    for (int mt = 0; mt < 8; ++mt)
+      *reinterpret_cast<u32x2 *>(dst + mt * 16) =
+          u32x2{pack_bf16(o[mt][nt].x, o[mt][nt].y), pack_bf16(o[mt][nt].z, o[mt][nt].w)};
   }
 }
 
@@ -525,7 +537,7 @@ AMLA_DEV float block_reduce(float v, float *red, bool is_max) {
 
 // Exact online-softmax recomputation of one (split, head) in fp32, used only
 // for heads attn_kernel flagged (a score more than REF_HEADROOM above the
-// split's reference max).  Thread tid owns latent columns tid and tid+256.
+// split's reference max).  Thread tid owns latent columns 2*tid and 2*tid+1.
 AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, int split, float *qs, float *ps, float *red,
                               float &m_out, float &l_out, float &o0, float &o1) {
   const int tid = threadIdx.x;
@@ -573,9 +585,9 @@ AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, int split, floa
     const int n = min(256, t1 - c0);
     for (int j = 0; j < n; ++j) {
       const float w = ps[j];
-      const uint16_t *row = cb + (size_t)(c0 + j) * LORA;
-      a0 += w * bf2f(row[tid]);
-      a1 += w * bf2f(row[tid + 256]);
+      const uint32_t pr = reinterpret_cast<const uint32_t *>(cb + (size_t)(c0 + j) * LORA)[tid];  // columns 2tid, 2tid+1
+      a0 += w * lo_bf(pr);
+      a1 += w * hi_bf(pr);
     }
     __syncthreads();
   }
@@ -618,25 +630,24 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
     const float w = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
     if (tid < ap.splits) wsp[tid] = w;
     L = block_reduce(w * ls, red, false);
-    const float *po = ap.part_o + base * LORA + tid;
-    const size_t stride = (size_t)HEADS * LORA;
+    // thread tid: latent columns 2*tid, 2*tid+1 (one 4-byte bf16 pair per split)
+    const uint32_t *po = reinterpret_cast<const uint32_t *>(ap.part_o + base * LORA) + tid;
+    const size_t stride = (size_t)HEADS * LORA / 2;
     int s = 0;
-    for (; s + 8 <= ap.splits; s += 8) {
-      float v0[8], v1[8];
+    for (; s + 16 <= ap.splits; s += 16) {
+      uint32_t v[16];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        v0[j] = po[(s + j) * stride];
-        v1[j] = po[(s + j) * stride + 256];
-      }
+      for (int j = 0; j < 16; ++j) v[j] = po[(s + j) * stride];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        a0 += wsp[s + j] * v0[j];
-        a1 += wsp[s + j] * v1[j];
+      for (int j = 0; j < 16; ++j) {
+        a0 += wsp[s + j] * lo_bf(v[j]);
+        a1 += wsp[s + j] * hi_bf(v[j]);
       }
     }
     for (; s < ap.splits; ++s) {
-      a0 += wsp[s] * po[s * stride];
-      a1 += wsp[s] * po[s * stride + 256];
+      const uint32_t v = po[s * stride];
+      a0 += wsp[s] * lo_bf(v);
+      a1 += wsp[s] * hi_bf(v);
     }
   } else {
     // rare path: online merge with exact recomputation of flagged splits
@@ -647,8 +658,9 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
       if (l1 < 0.f) {
         recompute_split(ap, b, h, s, qs, ps, red, m1, l1, o0, o1);
       } else {
-        o0 = ap.part_o[row * LORA + tid];
-        o1 = ap.part_o[row * LORA + tid + 256];
+        const uint32_t v = reinterpret_cast<const uint32_t *>(ap.part_o + row * LORA)[tid];
+        o0 = lo_bf(v);
+        o1 = hi_bf(v);
       }
       if (m1 == -INFINITY) continue;  // split past this sequence's context
       const float Mn = fmaxf(M, m1);
@@ -661,8 +673,8 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
     }
   }
   const float inv = 1.f / L;
-  lat[tid] = a0 * inv * bf2f(gamma[tid]);
-  lat[tid + 256] = a1 * inv * bf2f(gamma[tid + 256]);
+  lat[2 * tid] = a0 * inv * bf2f(gamma[2 * tid]);
+  lat[2 * tid + 1] = a1 * inv * bf2f(gamma[2 * tid + 1]);
   __syncthreads();
   // out[v] = sum_c W_UV[h][v][c] * scale * lat[c]; wave handles 32 rows, lane 8 columns
   float lv[8];
@@ -715,7 +727,7 @@ static DecodeLayout decode_layout(const amla_mla_args &a) {
   L.q = take((size_t)B * a.heads * HD * 2);
   L.qbuf = take((size_t)B * a.heads * QKD * 2);
   L.part_ml = take((size_t)B * L.splits * a.heads * 2 * 4);
-  L.part_o = take((size_t)B * L.splits * a.heads * LORA * 4);
+  L.part_o = take((size_t)B * L.splits * a.heads * LORA * 2);
   L.attn = take((size_t)B * a.heads * a.v_dim * 2);
   L.lin = take(std::max(L.pa.part_bytes, std::max(L.pb.part_bytes, L.po.part_bytes)));  // K-part sums of the linears
   L.total = off;
@@ -811,7 +823,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
 
   // 4. absorb W_UK into the query
   mark(ev, 3, st);
-  absorb_kernel<<<dim3(HEADS, (B + 7) / 8), 256, 0, st>>>(
+  absorb_kernel<<<dim3(HEADS, LORA / 128, (B + 7) / 8), 256, 0, st>>>(
       q, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv),
       B, qbuf);
   if ((rc = check_launch("mla absorb"))) return rc;
@@ -827,7 +839,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   ap.splits = L.splits; ap.tiles_per_split = L.tiles_per_split;
   ap.scale_log2 = a->softmax_scale * 1.4426950408889634f;
   ap.eps = a->eps;
-  ap.part_o = reinterpret_cast<float *>(ws + L.part_o);
+  ap.part_o = reinterpret_cast<uint16_t *>(ws + L.part_o);
   ap.part_ml = reinterpret_cast<float *>(ws + L.part_ml);
   attn_kernel<<<dim3(L.splits, B), 256, ATTN_LDS, st>>>(ap);
   if ((rc = check_launch("mla attention"))) return rc;
