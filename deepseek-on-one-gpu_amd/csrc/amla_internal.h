@@ -49,14 +49,16 @@ struct GemvParams {
 };
 
 struct GemvPlan {
-  int bw;            // 128-wide K blocks per wave
+  int kpb;           // 128-wide K blocks per K part
   int kparts;        // K parts (workgroups per row group); > 1 needs GemvParams::part
   int rg;            // 16-row tiles per workgroup
   int groups;        // workgroups
+  size_t lds;        // dynamic LDS bytes per workgroup
   size_t part_bytes; // fp32 partial sums (kparts * M * N * 4) when kparts > 1
 };
 
 GemvPlan plan_gemv(int M, int N, int K);
+size_t gemv_lds_bytes(int M, int MT, int kpb, int rg);
 // Launches the skinny GEMM for M <= 64 (N % 16 == 0, K % 128 == 0, 16-byte aligned rows);
 // p.part must hold plan.part_bytes when plan.kparts > 1.
 int launch_gemv(const GemvParams &p, int mode, const GemvPlan &plan, hipStream_t stream);

@@ -137,29 +137,39 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
 // ---------------------------------------------------------------- skinny GEMM
 
 // Streaming skinny GEMM for M <= 64 (decode projections).  The weight matrix
-// is cut into units of RG consecutive 16-row tiles x one K part of 4*BW
-// 128-wide blocks; a workgroup (4 waves) owns one unit and wave w the blocks
-// BW*w .. BW*w+BW-1 of the part.  A wave holds the x fragments of its blocks
-// in registers for the whole unit and streams the weight rows tile after tile
-// (the next tile's loads are in flight while the current one is converted and
-// multiplied): 2*BW KB of weights per tile and wave, no x traffic per tile.
-// The four waves' partial tiles are summed through LDS in wave order; with
-// one K part the sum goes through the epilogue, otherwise into fp32 partials
-// [part][M][N] that gemv_finish sums in part order (deterministic, no atomics
-// and no workgroup depends on another).
+// is cut into units of RG consecutive 16-row tiles x one K part of KPB
+// 128-wide blocks; a workgroup (4 waves) owns one unit.
+//   * x[:, part] is staged in LDS once per workgroup (bf16, 16 B padded rows);
+//   * weight tiles stream HBM -> LDS with LDS-DMA (global_load_lds, no
+//     registers), NBUF-1 tiles ahead; one copy moves 512 contiguous bytes of
+//     two rows, so every row is read in long runs;
+//   * the 4 waves split the part's blocks of a tile (block b -> wave b % 4),
+//     read the MFMA fragments from LDS, convert fp8 -> bf16 in registers and
+//     sum their partial tiles through LDS in wave order.
+// With one K part the sums go through the epilogue (deferred to the end of the
+// unit: one round of epilogue loads), otherwise into fp32 partials
+// [part][M][N] that gemv_finish sums in part order (deterministic, no atomics,
+// no workgroup depends on another).
 //
-// Within a block, lane (row l%16, group g = l/16) holds weight bytes
-// 16g .. 16g+15 and 64+16g .. 64+16g+15 of its row: each 16 B load covers
-// whole 64 B sectors of 16 rows.  The MFMA K order is permuted accordingly
-// and the x fragments follow the same order.
+// Weight tile layout in LDS: segment s (512 B of K) of row pair i (rows 2i,
+// 2i+1) is one 1 KB DMA copy at ((s * 8 + i) * 1024); row 2i+j's half at +512j;
+// inside a row's 512 B, 16 B chunk c sits at (c & ~7) | ((c ^ row) & 7), so the
+// 16 rows of a fragment read hit distinct banks.
+// MFMA K order inside a 128-wide block: lane (row l%16, group g = l/16) holds
+// weight chunks g and 4+g (bytes 16g.., 64+16g..) = K slots 0-7, 8-15 (first
+// chunk) and 64.., 72.. (second); x fragments follow the same order.
 constexpr int GEMV_MAX_PARTS = 32;  // K parts summed by gemv_finish
 constexpr int GEMV_MAX_RG = 16;     // 16-row tiles per workgroup
+constexpr int GEMV_KPB = 16;        // max 128-wide blocks per K part (2 KB of a row)
+constexpr int GEMV_NBUF = 3;        // weight tiles resident: current + two in flight
 
-template <int MT, int BW, int MODE>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kparts) {
-  // wave index in a scalar register: block ranges, scale loads and the
-  // per-block branches below stay scalar (a vector scale load would make the
-  // compiler wait for every weight load in flight)
+// LDS: [NBUF][16 rows][ceil4(kpb) * 128] weights | [M][kpb * 256 + 16] x |
+//      [2][4 waves][MT][64] f32x4 partial tiles | [rg][MT][64] f32x4 results
+__host__ __device__ inline int gemv_kpb4(int kpb) { return (kpb + 3) & ~3; }
+__host__ __device__ inline int gemv_xrow(int kpb) { return kpb * 256 + 16; }
+
+template <int MT, int MODE>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kparts, int kpb) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 15, lg = lane >> 4;
   const int KB = p.K >> 7;
@@ -167,115 +177,147 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
   const int part = blockIdx.x % kparts;
   const int tile_begin = (blockIdx.x / kparts) * rg;
   const int tile_end = min(tile_begin + rg, ntiles);
-  const int kb0 = part * 4 * BW + wave * BW;            // first block of this wave
-  const int nb = max(0, min(BW, KB - kb0));              // blocks of this wave (wave-uniform)
+  const int kb_begin = part * kpb;
+  const int nbp = min(kpb, KB - kb_begin);  // blocks of this part
+  const int nseg = (nbp + 3) >> 2;          // 512 B segments per row
+  const int XROW = gemv_xrow(kpb);
+  const int TILE_BYTES = 16 * gemv_kpb4(kpb) * 128;
 
-  // x fragments of the wave's blocks: [block][m tile][MFMA of the block]
-  bf16x8 xf[BW][MT][4];
-#pragma unroll
-  for (int j = 0; j < BW; ++j)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const int m = t * 16 + li;
-      const bool ok = j < nb && m < p.M;
-      const uint16_t *xr = p.x + (size_t)(ok ? m : 0) * p.ldx + (size_t)(kb0 + (ok ? j : 0)) * 128 + lg * 16;
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        xf[j][t][u] = ok ? as_bf16x8(ldg16(xr + (u >> 1) * 64 + (u & 1) * 8)) : as_bf16x8(u32x4{0, 0, 0, 0});
-    }
+  extern __shared__ __align__(16) uint8_t gsm[];
+  uint8_t *const wbuf = gsm;
+  uint8_t *const xs = gsm + GEMV_NBUF * TILE_BYTES;
+  f32x4 *const red = reinterpret_cast<f32x4 *>(xs + p.M * XROW);
+  f32x4 *const done = red + 2 * 4 * MT * 64;
 
-  __shared__ f32x4 red[2][4][MT][64];
-  // reduced tiles of the unit, epilogue deferred to the end (one round of
-  // epilogue loads - rope table, residual - instead of one per tile)
-  __shared__ f32x4 done[GEMV_MAX_RG][MT][64];
-  // a tile's weights and block scales are loaded together, one tile ahead,
-  // unconditionally (the last trip and absent blocks re-read valid data that
-  // is not used): with no load under a branch the compiler's wait for the
-  // current tile never waits for the next one's loads
-  constexpr int NBUF = 3;  // tiles in flight: the current one and two ahead
-  u32x4 wv[NBUF][BW][2];
-  float sv[NBUF][BW];
-  const uint32_t woff = (uint32_t)(li * p.K + lg * 16);
-  auto load_tile = [&](int tile, int buf) {
+  // weight copies of one tile: row pairs i = 2*wave, 2*wave+1, every segment
+  auto dma_tile = [&](int tile, int buf) {
     const int nt = min(tile, tile_end - 1) * 16;
     const bool seg1 = (MODE == GEMV_QKVA) && nt >= p.n_split;
-    const uint8_t *wb = seg1 ? p.w1 : p.w0;
-    const int nl = seg1 ? nt - p.n_split : nt;
-    // uniform tile base + unsigned 32-bit lane offset: scalar-base loads, no
-    // per-tile address registers
-    const uint8_t *tb = wb + (size_t)nl * p.K;
-    const float *sr = (seg1 ? p.s1 : p.s0) + (size_t)(nl >> 7) * KB;
+    const uint8_t *wb = (seg1 ? p.w1 : p.w0) + (size_t)(seg1 ? nt - p.n_split : nt) * p.K;
+    uint8_t *tb = wbuf + buf * TILE_BYTES;
+    for (int s = 0; s < nseg; ++s) {
 #pragma unroll
-    for (int j = 0; j < BW; ++j) {
-      const int kb = min(kb0 + j, KB - 1);
-      sv[buf][j] = sr[kb];
-      wv[buf][j][0] = ldg16_nt(tb + (size_t)kb * 128 + woff);
-      wv[buf][j][1] = ldg16_nt(tb + (size_t)kb * 128 + 64 + woff);
+      for (int ii = 0; ii < 2; ++ii) {
+        const int i = wave * 2 + ii;
+        const int row = 2 * i + (lane >> 5);
+        const int cl = lane & 31;                                 // LDS chunk in the row's 512 B
+        const int cg = (cl & ~7) | ((cl ^ row) & 7);              // global chunk stored there
+        const int kb = min(kb_begin + s * 4 + (cg >> 3), KB - 1);  // 128 B block (clamped: unused)
+        const uint32_t off = (uint32_t)(row * p.K + kb * 128 + (cg & 7) * 16);
+        __builtin_amdgcn_global_load_lds(wb + off, (__attribute__((address_space(3))) void *)(tb + (s * 8 + i) * 1024),
+                                         16, 0, 0);
+      }
     }
   };
-  auto do_tile = [&](int tile, int buf) {
-    load_tile(tile + NBUF - 1, (buf + NBUF - 1) % NBUF);
+  // LDS-only barrier: __syncthreads would also wait for every copy in flight
+  auto lds_barrier = [&]() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // x[:, part] -> LDS (only rows < M; the fragments of rows >= M are zeros)
+  for (int idx = threadIdx.x; idx < p.M * nbp * 16; idx += 256) {
+    const int m = idx / (nbp * 16), c = idx % (nbp * 16);
+    *reinterpret_cast<u32x4 *>(xs + m * XROW + c * 16) =
+        ldg16(p.x + (size_t)m * p.ldx + (size_t)kb_begin * 128 + c * 8);
+  }
+  if (tile_begin < tile_end) {
+#pragma unroll
+    for (int b = 0; b < GEMV_NBUF - 1; ++b) dma_tile(tile_begin + b, b);
+  }
+
+  for (int tile = tile_begin, it = 0; tile < tile_end; ++tile, ++it) {
+    const int buf = it % GEMV_NBUF;
     const int nt = tile * 16;
+    // block scales of this wave's blocks through the scalar cache (constant
+    // address space: the scales are never written here), so waiting for them
+    // is not waiting for the weight copies in flight
+    const bool seg1 = (MODE == GEMV_QKVA) && nt >= p.n_split;
+    const __attribute__((address_space(4))) float *srow =
+        (const __attribute__((address_space(4))) float *)((seg1 ? p.s1 : p.s0) +
+                                                          (size_t)((seg1 ? nt - p.n_split : nt) >> 7) * KB + kb_begin);
+    float scw[GEMV_KPB / 4];
+#pragma unroll
+    for (int j = 0; j < GEMV_KPB / 4; ++j) scw[j] = srow[min(wave + 4 * j, nbp - 1)];
+    // this tile's copies landed (the next tile's may stay in flight), then
+    // every wave's part of it is visible
+    if (nseg == 4) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (nseg == 3) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    else if (nseg == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    lds_barrier();
+    dma_tile(tile + GEMV_NBUF - 1, (it + GEMV_NBUF - 1) % GEMV_NBUF);  // into the buffer read last trip
+
+    const uint8_t *tb = wbuf + buf * TILE_BYTES;
     f32x4 acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < BW; ++j) {
-      if (j < nb) {
-        const float sc = sv[buf][j];
-        bf16x8 w0, w1, w2, w3;
-        fp8x16_to_bf16x16(wv[buf][j][0], w0, w1);
-        fp8x16_to_bf16x16(wv[buf][j][1], w2, w3);
+    for (int j = 0; j < GEMV_KPB / 4; ++j) {
+      const int bl = wave + 4 * j;
+      if (bl < nbp) {
+        const int s = bl >> 2, bq = bl & 3;  // segment, block inside it
+        const uint8_t *rp = tb + (s * 8 + (li >> 1)) * 1024 + (li & 1) * 512;
+        const u32x4 w0 = *reinterpret_cast<const u32x4 *>(rp + ((bq * 8) | ((lg ^ li) & 7)) * 16);
+        const u32x4 w1 = *reinterpret_cast<const u32x4 *>(rp + ((bq * 8) | (((4 + lg) ^ li) & 7)) * 16);
+        bf16x8 a0, a1, a2, a3;
+        fp8x16_to_bf16x16(w0, a0, a1);
+        fp8x16_to_bf16x16(w1, a2, a3);
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
+          const int m = t * 16 + li;
+          bf16x8 x0, x1, x2, x3;
+          if (m < p.M) {
+            const uint8_t *xr = xs + m * XROW + bl * 256 + lg * 32;
+            x0 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xr));
+            x1 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xr + 16));
+            x2 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xr + 128));
+            x3 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xr + 144));
+          } else {
+            x0 = x1 = x2 = x3 = as_bf16x8(u32x4{0, 0, 0, 0});
+          }
           f32x4 c = {0.f, 0.f, 0.f, 0.f};
-          c = mfma16(w0, xf[j][t][0], c);
-          c = mfma16(w1, xf[j][t][1], c);
-          c = mfma16(w2, xf[j][t][2], c);
-          c = mfma16(w3, xf[j][t][3], c);
-          acc[t] += sc * c;
+          c = mfma16(a0, x0, c);
+          c = mfma16(a1, x1, c);
+          c = mfma16(a2, x2, c);
+          c = mfma16(a3, x3, c);
+          acc[t] += scw[j] * c;
         }
       }
     }
+    f32x4 *rb = red + (it & 1) * 4 * MT * 64;
 #pragma unroll
-    for (int t = 0; t < MT; ++t) red[tile & 1][wave][t][lane] = acc[t];
-    __syncthreads();
-    // MT * 64 lanes of results (4 outputs each) per tile; thread idx sums the
-    // four waves in order
+    for (int t = 0; t < MT; ++t) rb[(wave * MT + t) * 64 + lane] = acc[t];
+    lds_barrier();
     for (int idx = threadIdx.x; idx < MT * 64; idx += 256) {
       const int t = idx >> 6, ln = idx & 63;
-      const int m = t * 16 + (ln & 15);
-      const int n = nt + 4 * (ln >> 4);
-      if (m >= p.M) continue;
-      f32x4 v = red[tile & 1][0][t][ln];
-      v += red[tile & 1][1][t][ln];
-      v += red[tile & 1][2][t][ln];
-      v += red[tile & 1][3][t][ln];
-      if (kparts == 1) done[tile - tile_begin][t][ln] = v;
-      else *reinterpret_cast<f32x4 *>(p.part + ((size_t)part * p.M + m) * p.N + n) = v;
+      f32x4 v = rb[(0 * MT + t) * 64 + ln];
+      v += rb[(1 * MT + t) * 64 + ln];
+      v += rb[(2 * MT + t) * 64 + ln];
+      v += rb[(3 * MT + t) * 64 + ln];
+      done[(it * MT + t) * 64 + ln] = v;
     }
-    // red[tile & 1] is rewritten two tiles later, after the next barrier
-  };
-  // NBUF tiles per trip: the register buffer index stays a constant
-  if (tile_begin < tile_end) {
-#pragma unroll
-    for (int b = 0; b < NBUF - 1; ++b) load_tile(tile_begin + b, b);
+    // red[it & 1] is rewritten two tiles later, after the next two barriers
   }
-  for (int tile = tile_begin; tile < tile_end; tile += NBUF) {
-    do_tile(tile, 0);
-    if (tile + 1 < tile_end) do_tile(tile + 1, 1);
-    if (tile + 2 < tile_end) do_tile(tile + 2, 2);
+  lds_barrier();
+  // results of the unit: epilogue (one K part) or fp32 partial sums
+  const int nitems = (tile_end - tile_begin) * MT * 64;
+  for (int idx = threadIdx.x; idx < nitems; idx += 256) {
+    const int tl = idx / (MT * 64), t = (idx >> 6) % MT, ln = idx & 63;
+    const int m = t * 16 + (ln & 15);
+    const int n = (tile_begin + tl) * 16 + 4 * (ln >> 4);
+    if (m >= p.M) continue;
+    const f32x4 v = done[(tl * MT + t) * 64 + ln];
+    if (kparts == 1) store4<MODE>(p, m, n, v);
+    else *reinterpret_cast<f32x4 *>(p.part + ((size_t)part * p.M + m) * p.N + n) = v;
   }
-  if (kparts == 1) {
-    __syncthreads();
-    const int nitems = (tile_end - tile_begin) * MT * 64;
-    for (int idx = threadIdx.x; idx < nitems; idx += 256) {
-      const int tl = idx / (MT * 64), t = (idx >> 6) % MT, ln = idx & 63;
-      const int m = t * 16 + (ln & 15);
-      const int n = (tile_begin + tl) * 16 + 4 * (ln >> 4);
-      if (m < p.M) store4<MODE>(p, m, n, done[tl][t][ln]);
-    }
-  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last trips' (unused) copies land before exit
+}
+
+size_t gemv_lds_bytes(int M, int MT, int kpb, int rg) {
+  return (size_t)GEMV_NBUF * 16 * gemv_kpb4(kpb) * 128 + (size_t)M * gemv_xrow(kpb) + 2 * 4 * MT * 64 * 16 +
+         (size_t)rg * MT * 64 * 16;
 }
 
 // Sums the K parts of gemv_kernel in part order and applies the epilogue.
@@ -303,30 +345,26 @@ GemvPlan plan_gemv(int M, int N, int K) {
   const int tiles = N / 16;
   const int KB = K / 128;
   const int MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-  // blocks per wave: x fragments take 16 * BW * MT registers (<= 64).  One K
-  // part when it fits (no finishing pass), else the BW wasting the fewest
-  // wave-blocks, larger BW on ties
-  const int bw_max = MT == 1 ? 4 : (MT == 2 ? 2 : 1);
-  int bw = bw_max;
-  if (KB <= 4 * bw_max) {
-    while (bw > 1 && 4 * (bw / 2) >= KB) bw /= 2;
-  } else {
-    int best_waste = 1 << 30;
-    for (int b = bw_max; b >= 1; b /= 2) {
-      const int waste = ((KB + 4 * b - 1) / (4 * b)) * 4 * b - KB;
-      if (waste < best_waste) {
-        best_waste = waste;
-        bw = b;
-      }
-    }
+  // K part: whole K when it fits (no finishing pass), else the largest block
+  // count <= GEMV_KPB (multiple of 4) that splits K into equal parts; both
+  // within the LDS budget with one tile per unit
+  constexpr size_t LDS_MAX = 160 * 1024;
+  int kmax = GEMV_KPB;
+  while (kmax > 4 && gemv_lds_bytes(M, MT, kmax, 1) > LDS_MAX) kmax -= 4;
+  int kpb = KB <= kmax ? KB : 0;
+  if (!kpb) {
+    for (int c = kmax; c >= 4; c -= 4)
+      if (KB % c == 0) { kpb = c; break; }
+    if (!kpb) kpb = kmax;
   }
-  pl.bw = bw;
-  pl.kparts = (KB + 4 * bw - 1) / (4 * bw);  // launch_gemv rejects more than GEMV_MAX_PARTS
+  pl.kpb = kpb;
+  pl.kparts = (KB + kpb - 1) / kpb;
   // tiles per unit: fewest rounds of 256 workgroups x tiles per unit, then
-  // the largest unit (fewer x reloads); <= 16 tiles
+  // the largest unit (fewer x stagings), within the LDS budget
   int best_rg = 1;
   int64_t best_cost = INT64_MAX;
   for (int rg = 1; rg <= GEMV_MAX_RG; ++rg) {
+    if (gemv_lds_bytes(M, MT, kpb, rg) > LDS_MAX) break;
     const int64_t units = (int64_t)((tiles + rg - 1) / rg) * pl.kparts;
     const int64_t cost = ((units + 255) / 256) * rg;
     if (cost <= best_cost) {
@@ -336,18 +374,30 @@ GemvPlan plan_gemv(int M, int N, int K) {
   }
   pl.rg = best_rg;
   pl.groups = ((tiles + pl.rg - 1) / pl.rg) * pl.kparts;
+  pl.lds = gemv_lds_bytes(M, MT, kpb, pl.rg);
   pl.part_bytes = pl.kparts > 1 ? (size_t)pl.kparts * M * N * 4 : 0;
   return pl;
 }
 
-template <int MT, int BW>
-static void launch_cfg(const GemvParams &p, int mode, const GemvPlan &pl, hipStream_t st) {
-  dim3 grid(pl.groups);
+template <int MT, int MODE>
+static int launch_cfg(const GemvParams &p, const GemvPlan &pl, hipStream_t st) {
+  static bool attr_set = false;  // raise the dynamic LDS limit once per process
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void *)gemv_kernel<MT, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    attr_set = true;
+  }
+  gemv_kernel<MT, MODE><<<dim3(pl.groups), 256, pl.lds, st>>>(p, pl.rg, pl.kparts, pl.kpb);
+  return 0;
+}
+
+template <int MT>
+static void launch_mt(const GemvParams &p, int mode, const GemvPlan &pl, hipStream_t st) {
   switch (mode) {
-    case GEMV_PLAIN: gemv_kernel<MT, BW, GEMV_PLAIN><<<grid, 256, 0, st>>>(p, pl.rg, pl.kparts); break;
-    case GEMV_RESID: gemv_kernel<MT, BW, GEMV_RESID><<<grid, 256, 0, st>>>(p, pl.rg, pl.kparts); break;
-    case GEMV_QKVA: gemv_kernel<MT, BW, GEMV_QKVA><<<grid, 256, 0, st>>>(p, pl.rg, pl.kparts); break;
-    default: gemv_kernel<MT, BW, GEMV_QROPE><<<grid, 256, 0, st>>>(p, pl.rg, pl.kparts); break;
+    case GEMV_PLAIN: launch_cfg<MT, GEMV_PLAIN>(p, pl, st); break;
+    case GEMV_RESID: launch_cfg<MT, GEMV_RESID>(p, pl, st); break;
+    case GEMV_QKVA: launch_cfg<MT, GEMV_QKVA>(p, pl, st); break;
+    default: launch_cfg<MT, GEMV_QROPE>(p, pl, st); break;
   }
 }
 
@@ -360,16 +410,9 @@ int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t 
                 GEMV_MAX_PARTS);
   if (pl.kparts > 1 && !p0.part) return fail(AMLA_EWORKSPACE, "skinny fp8 GEMM: missing partial-sum workspace");
   const int MT = p0.M <= 16 ? 1 : (p0.M <= 32 ? 2 : 4);
-  if (MT == 1) {
-    if (pl.bw == 4) launch_cfg<1, 4>(p0, mode, pl, st);
-    else if (pl.bw == 2) launch_cfg<1, 2>(p0, mode, pl, st);
-    else launch_cfg<1, 1>(p0, mode, pl, st);
-  } else if (MT == 2) {
-    if (pl.bw == 2) launch_cfg<2, 2>(p0, mode, pl, st);
-    else launch_cfg<2, 1>(p0, mode, pl, st);
-  } else {
-    launch_cfg<4, 1>(p0, mode, pl, st);
-  }
+  if (MT == 1) launch_mt<1>(p0, mode, pl, st);
+  else if (MT == 2) launch_mt<2>(p0, mode, pl, st);
+  else launch_mt<4>(p0, mode, pl, st);
   if (pl.kparts > 1) {
     const int64_t total = (int64_t)p0.M * (p0.N / 4);
     const unsigned blocks = (unsigned)((total + 63) / 64);

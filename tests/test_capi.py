@@ -90,7 +90,7 @@ def test_workspace_queries():
     a.kv_lora, a.qk_nope, a.qk_rope, a.v_dim = 512, 128, 64, 128
     a.max_seq = a.rope_rows = a.max_context = 32768
     n = L.amla_mla_decode_workspace_bytes(ctypes.byref(a))
-    assert 32 * 8 * 128 * 512 * 4 <= n < 200 << 20
+    assert 32 * 8 * 128 * 512 * 2 <= n < 200 << 20   # bf16 split partials dominate
 
 
 def test_python_api_rejects_cpu_tensors():
