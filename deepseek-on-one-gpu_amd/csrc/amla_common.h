@@ -21,6 +21,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -85,6 +86,17 @@ AMLA_DEV u32x4 ldg16_nt(const void *p) {
 }
 
 AMLA_DEV bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// LDS address operand of __builtin_amdgcn_global_load_lds
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
+
+// Wait until at most N of this wave's vector memory operations are in flight
+// (global_load_lds copies included).
+template <int N>
+AMLA_DEV void wait_vmcnt() {
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
+}
 
 // Butterfly reductions inside a wave.
 AMLA_DEV float wave_sum(float v) {

@@ -151,8 +151,6 @@ constexpr int ATTN_LDS_BYTES = P_OFF + HEADS * PROW;
 constexpr int TILE_DMA = 11;  // copies per wave per tile: 8 latent rows, 1 block of rope keys, 2 table blocks
 constexpr float REF_HEADROOM = 64.f;      // p = 2^(s - m_ref) <= 2^64: no overflow anywhere
 
-#define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
-
 // Wave w copies rows 8w .. 8w+7 of the tile straight into LDS (no VGPRs):
 // every global_load_lds_dwordx4 writes 64 lanes x 16 B contiguously at its
 // LDS base.  Row indices are wave-uniform (scalar bases, one lane offset).
@@ -240,11 +238,6 @@ AMLA_DEV void prepare_own_rows(uint8_t *stage, const uint8_t *tab, int wave, int
   *reinterpret_cast<u32x4 *>(rp + (LORA + q * 8) * 2) = k;
 }
 
-template <int N>
-AMLA_DEV void wait_vmcnt() {
-  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
-}
 
 // sum / max over the four lanes l, l^16, l^32, l^48 (lane swaps, no LDS)
 AMLA_DEV float sum_lane_groups(float v) {

@@ -192,11 +192,20 @@ int launch_gemm(const GemvParams &p, int mode, hipStream_t st) {
 // ---------------------------------------------------------------- K10 causal flash attention
 
 constexpr int P_NOPE = 128, P_ROPE = 64, P_QK = 192, P_V = 128, P_H = 128;
-constexpr int P_KT = 32;                // keys per tile
-constexpr int P_KLD = P_QK + 8;         // t-major key row (bf16)
-constexpr int P_VLD = P_KT + 4;         // v-major value row (bf16)
-constexpr int P_QW = 64;                // queries per wave
-constexpr int P_QB = 4 * P_QW;          // queries per workgroup
+constexpr int P_KVROW = P_H * (P_NOPE + P_V) * 2;  // bytes per kv_b output row (all heads)
+constexpr int F_KT = 64;                           // keys per tile
+constexpr int F_NQG = 1;                           // groups of 32 queries per wave
+constexpr int F_QW = 32 * F_NQG;                   // queries per wave
+constexpr int F_NW = 8;                            // waves per workgroup (two per SIMD)
+constexpr int F_QB = F_NW * F_QW;                  // queries per workgroup
+constexpr int F_RPW = F_KT / F_NW;                 // key rows each wave copies per tile
+constexpr int F_NST = 3;                           // LDS stages (copies run two tiles ahead)
+// one stage: k_nope rows (256 B), rope-key rows (128 B), value rows (256 B);
+// 16-byte chunks swizzled per row so that the fragment reads hit distinct banks
+constexpr int F_NOPE = 0, F_RPE = F_KT * 256, F_VAL = F_RPE + F_KT * 128;
+constexpr int F_STAGE = F_VAL + F_KT * 256;        // 40 KB
+constexpr int F_LDS = F_NST * F_STAGE;
+constexpr int F_DMA = 5 * F_RPW / 8;               // copies per wave per tile
 
 struct FlashParams {
   const uint16_t *q;      // (rows, H, 192): row = b*S + s, q_pe already rotated
@@ -204,180 +213,405 @@ struct FlashParams {
   const uint16_t *kpe;    // (Tmax, 64) rotated rope keys
   uint16_t *out;          // (rows, H*128)
   const int32_t *pos;
-  int b, S;
+  int b, S, nqb;  // nqb: query blocks of 256 per head
   float scale_log2;
 };
 
-struct FlashRegs {
-  u32x4 kn[2];  // key row tid/8: nope elements (tid%8)*16 .. +15
-  u32x4 kr;     // key row tid/8: rope elements (tid%8)*8 .. +7
-  u32x2 v[4];   // keys 4*(tid/32) .. +3, v columns 4*(tid%32) .. +3
+// Wave w copies key rows F_RPW w .. +F_RPW-1 of the tile (k_nope, value and rope key)
+// straight into LDS: each global_load_lds writes 64 lanes x 16 B contiguously,
+// so the swizzle is applied to the source chunk each lane fetches.  Slot
+// (row, c) holds chunk c ^ (row & 7) of a k_nope or rope-key row and chunk
+// c ^ 2(row & 3) of a value row.  Inside the keys in use the row bases are
+// scalar and each lane adds a fixed offset; the tile that crosses Tlim
+// clamps rows to Tlim - 1 per lane (in bounds; their scores are masked).
+struct FlashLane {
+  uint32_t nope[2];  // lane offset of k_nope copies j even / odd (row r16 of 4, swizzled chunk)
+  uint32_t val;      // lane offset of value copies
+  uint32_t rope;     // lane offset of rope-key copies (row r8 of 8)
 };
 
-AMLA_DEV void flash_load(const FlashParams &p, int h, int t0, int Tlim, FlashRegs &R) {
-  const int tid = threadIdx.x;
-  const int kr = tid >> 3, kc = tid & 7;
-  const int t = t0 + kr;
-  if (t < Tlim) {
-    const uint16_t *src = p.kvb + (size_t)t * (P_H * 256) + h * 256 + kc * 16;
-    R.kn[0] = ldg16(src);
-    R.kn[1] = ldg16(src + 8);
-    R.kr = ldg16(p.kpe + (size_t)t * P_ROPE + kc * 8);
-  } else {
-    R.kn[0] = R.kn[1] = R.kr = u32x4{0, 0, 0, 0};
-  }
-  const int vr = tid >> 5, vc = tid & 31;
+AMLA_DEV FlashLane flash_lane(int lane) {
+  const int r16 = lane >> 4, c16 = lane & 15, r8 = lane >> 3, c8 = lane & 7;
+  FlashLane fl;
+  fl.nope[0] = r16 * P_KVROW + 16 * (c16 ^ r16);
+  fl.nope[1] = r16 * P_KVROW + 16 * (c16 ^ (4 + r16));
+  fl.val = r16 * P_KVROW + P_NOPE * 2 + 16 * (c16 ^ (2 * r16));
+  fl.rope = r8 * (P_ROPE * 2) + 16 * (c8 ^ r8);
+  return fl;
+}
+
+AMLA_DEV void flash_dma(const FlashParams &p, int h, int t0, int Tlim, uint8_t *stage, int wave, int lane,
+                        const FlashLane &fl) {
+  const char *kv = reinterpret_cast<const char *>(p.kvb) + h * ((P_NOPE + P_V) * 2);
+  const char *kr = reinterpret_cast<const char *>(p.kpe);
+  if (t0 + F_KT <= Tlim) {
+    const char *kvw = kv + (size_t)(t0 + F_RPW * wave) * P_KVROW;
+    const char *krw = kr + (size_t)(t0 + F_RPW * wave) * (P_ROPE * 2);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tv = t0 + vr * 4 + j;
-    R.v[j] = tv < Tlim ? ldg8(p.kvb + (size_t)tv * (P_H * 256) + h * 256 + P_NOPE + vc * 4) : u32x2{0, 0};
+    for (int j = 0; j < F_RPW / 4; ++j) {
+      const int row = F_RPW * wave + 4 * j;
+      __builtin_amdgcn_global_load_lds(kvw + (size_t)(4 * j) * P_KVROW + fl.nope[j & 1],
+                                       LDS_PTR(stage + F_NOPE + row * 256), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(kvw + (size_t)(4 * j) * P_KVROW + fl.val, LDS_PTR(stage + F_VAL + row * 256),
+                                       16, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < F_RPW / 8; ++j)
+      __builtin_amdgcn_global_load_lds(krw + 8 * j * (P_ROPE * 2) + fl.rope,
+                                       LDS_PTR(stage + F_RPE + (F_RPW * wave + 8 * j) * 128), 16, 0, 0);
+    return;
+  }
+  const int r16 = lane >> 4, c16 = lane & 15, r8 = lane >> 3, c8 = lane & 7;
+  const int last = Tlim - 1;
+#pragma unroll
+  for (int j = 0; j < F_RPW / 4; ++j) {
+    const int row = F_RPW * wave + 4 * j;
+    const int t = min(t0 + row + r16, last);
+    const char *src = kv + (size_t)t * P_KVROW;
+    __builtin_amdgcn_global_load_lds(src + 16 * (c16 ^ (4 * (j & 1) + r16)), LDS_PTR(stage + F_NOPE + row * 256), 16,
+                                     0, 0);
+    __builtin_amdgcn_global_load_lds(src + P_NOPE * 2 + 16 * (c16 ^ (2 * r16)), LDS_PTR(stage + F_VAL + row * 256),
+                                     16, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < F_RPW / 8; ++j) {
+    const int row = F_RPW * wave + 8 * j;
+    const int t = min(t0 + row + r8, last);
+    __builtin_amdgcn_global_load_lds(kr + (size_t)t * (P_ROPE * 2) + 16 * (c8 ^ r8), LDS_PTR(stage + F_RPE + row * 128),
+                                     16, 0, 0);
   }
 }
 
-AMLA_DEV void flash_store(const FlashRegs &R, uint16_t *Ks, uint16_t *Vs) {
-  const int tid = threadIdx.x;
-  const int kr = tid >> 3, kc = tid & 7;
-  *reinterpret_cast<u32x4 *>(Ks + kr * P_KLD + kc * 16) = R.kn[0];
-  *reinterpret_cast<u32x4 *>(Ks + kr * P_KLD + kc * 16 + 8) = R.kn[1];
-  *reinterpret_cast<u32x4 *>(Ks + kr * P_KLD + P_NOPE + kc * 8) = R.kr;
-  const int vr = tid >> 5, vc = tid & 31;
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const uint32_t d0 = R.v[0][q], d1 = R.v[1][q], d2 = R.v[2][q], d3 = R.v[3][q];
-    const int c = vc * 4 + q * 2;
-    u32x2 even = {__builtin_amdgcn_perm(d1, d0, 0x05040100u), __builtin_amdgcn_perm(d3, d2, 0x05040100u)};
-    u32x2 odd = {__builtin_amdgcn_perm(d1, d0, 0x07060302u), __builtin_amdgcn_perm(d3, d2, 0x07060302u)};
-    *reinterpret_cast<u32x2 *>(Vs + c * P_VLD + vr * 4) = even;
-    *reinterpret_cast<u32x2 *>(Vs + (c + 1) * P_VLD + vr * 4) = odd;
-  }
+AMLA_DEV f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Grid (H, query blocks).  Wave w handles queries qb*256 + 64w .. +63 of one
-// head: S^T = K (keys x 192) . Q^T with keys as the MFMA M dimension, so each
-// lane holds 8 scores of one query, which are the B operand of
-// O^T (128 x queries) += V^T (128 x keys) . P^T.
-__global__ __launch_bounds__(256, 1) void flash_kernel(FlashParams p) {
-  const int h = blockIdx.x;
-  const int qblk = gridDim.y - 1 - blockIdx.y;  // heaviest causal blocks first
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int li = lane & 15, lg = lane >> 4;
+// Grid H x (query blocks of 256), 256 threads, 120 KB of LDS: one workgroup
+// per CU.  Wave w handles queries qb*256 + 64w .. +63 of head h, in two
+// groups of 32.  Per 64-key tile:
+//   S^T (keys x queries) = K (keys x 192) . Q^T     32x32x16 MFMAs, A = K rows
+//   online softmax in registers: lane l holds 16 keys of query l%32 per
+//     32-key group (the other 16 sit in lane l^32)
+//   O^T (128 x queries) += V^T (128 x keys) . P^T   B = P straight from the
+//     score registers, A = V^T by transpose reads
+// The running max moves only when a score exceeds it by more than 2^8, so the
+// O rescale is rare; exp2 arguments stay <= 8 and the final 1/l is exact.
+__global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
+  extern __shared__ __align__(16) uint8_t fsm[];
+  // Workgroup i runs on XCD i % 8 (round-robin dispatch): XCD x takes heads
+  // x*H/8 .. +H/8-1, one head at a time with all its query blocks, heaviest
+  // first, so a head's keys and values are read from HBM about once per XCD
+  // and shared through that XCD's L2.
+  const int nqb = p.nqb;
+  const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
+  const int h = xcd * (P_H / 8) + k / nqb;
+  const int qblk = nqb - 1 - k % nqb;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j32 = lane & 31, hh = lane >> 5;
   const int pos0 = p.pos[p.b];
-  const int s_begin = qblk * P_QB;
-  const int s_wave = s_begin + wave * P_QW;
-  const int s_last_blk = min(s_begin + P_QB, p.S) - 1;
-  const int Tlim = pos0 + s_last_blk + 1;   // keys needed by this block
-  const int ntiles = (Tlim + P_KT - 1) / P_KT;
+  const int s_begin = qblk * F_QB;
+  const int s_wave = s_begin + wave * F_QW;
+  const int s_last_blk = min(s_begin + F_QB, p.S) - 1;
+  const int Tlim = pos0 + s_last_blk + 1;  // keys needed by this block
+  const int ntiles = (Tlim + F_KT - 1) / F_KT;
+  const bool wave_active = s_wave < p.S;
+  const int wave_last_pos = pos0 + min(s_wave + F_QW, p.S) - 1;
+  const float sl2 = p.scale_log2;
 
-  __shared__ __align__(16) uint16_t Ks[2][P_KT * P_KLD];
-  __shared__ __align__(16) uint16_t Vs[2][P_V * P_VLD];
+  const FlashLane fl = flash_lane(lane);
+  flash_dma(p, h, 0, Tlim, fsm, wave, lane, fl);
 
-  bf16x8 qf[4][P_QK / 32];
+  // Q^T fragments: column = query s_wave + 32 qg + j32, dims 16 ks + 8 hh .. +7
+  bf16x8 qf[F_NQG][P_QK / 16];
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int s = min(s_wave + nt * 16 + li, p.S - 1);
-    const uint16_t *qr = p.q + ((size_t)(p.b * p.S + s) * P_H + h) * P_QK + 8 * lg;
+  for (int qg = 0; qg < F_NQG; ++qg) {
+    const int s = min(s_wave + 32 * qg + j32, p.S - 1);
+    const uint16_t *qr = p.q + ((size_t)(p.b * p.S + s) * P_H + h) * P_QK + 8 * hh;
 #pragma unroll
-    for (int ks = 0; ks < P_QK / 32; ++ks) qf[nt][ks] = as_bf16x8(ldg16(qr + ks * 32));
+    for (int ks = 0; ks < P_QK / 16; ++ks) qf[qg][ks] = as_bf16x8(ldg16(qr + 16 * ks));
   }
-  f32x4 o[P_V / 16][4];
+  if (ntiles > 1) flash_dma(p, h, F_KT, Tlim, fsm + F_STAGE, wave, lane, fl);
+  f32x16 o[4][F_NQG];
+  float m_run[F_NQG], l_run[F_NQG];
 #pragma unroll
-  for (int vt = 0; vt < P_V / 16; ++vt)
+  for (int qg = 0; qg < F_NQG; ++qg) {
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) o[vt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[4], l_run[4];
+    for (int vt = 0; vt < 4; ++vt)
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) { m_run[nt] = -INFINITY; l_run[nt] = 0.f; }
+      for (int r = 0; r < 16; ++r) o[vt][qg][r] = 0.f;
+    m_run[qg] = -INFINITY;
+    l_run[qg] = 0.f;
+  }
 
-  FlashRegs R;
-  flash_load(p, h, 0, Tlim, R);
-  flash_store(R, Ks[0], Vs[0]);
-  __syncthreads();
-  const int wave_last_pos = pos0 + min(s_wave + P_QW, p.S) - 1;
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int buf = tile & 1;
-    const bool more = tile + 1 < ntiles;
-    if (more) flash_load(p, h, (tile + 1) * P_KT, Tlim, R);
-    const int t0 = tile * P_KT;
-    if (t0 <= wave_last_pos && s_wave < p.S) {
-      const uint16_t *K = Ks[buf];
-      const uint16_t *V = Vs[buf];
-      f32x4 sc[2][4];
+  // per-lane LDS offsets.  K fragment (A of S^T): key row 32 kg + j32, chunk
+  // (2 ks + hh) ^ (j32 & 7).  V^T by ds_read_b64_tr_b16: in a 16-lane group g,
+  // lane L addresses value row t + L/4 and columns c0 + 4 (L%4) .. +3 with
+  // c0 = 32 vt + 16 (g & 1), and receives column c0 + L of rows t .. t+3.
+  const int x7 = j32 & 7;
+  const int L16 = lane & 15, g16 = lane >> 4;
+  const int vrow = L16 >> 2;
+  int koff[4], roff[4];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+  for (int k4 = 0; k4 < 4; ++k4) {
+    koff[k4] = F_NOPE + j32 * 256 + 16 * ((2 * k4 + hh) ^ x7);
+    roff[k4] = F_RPE + j32 * 128 + 16 * ((2 * k4 + hh) ^ x7);
+  }
+  int voff[2];  // vt even / odd (bit 2 of the chunk index meets the swizzle)
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) sc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int par = 0; par < 2; ++par) {
+    const int chunk = 4 * par + 2 * (g16 & 1) + ((L16 & 3) >> 1);
+    voff[par] = F_VAL + (4 * hh + vrow) * 256 + 16 * (chunk ^ (2 * vrow)) + 8 * (L16 & 1);
+  }
+
+  // ---- software pipeline over 32-key groups g (tile g/2, half g%2).  Step
+  // A of g computes S_{g+1} while exponentiating group g; step B accumulates
+  // PV_g while masking and maximising group g+1, then moves the running max
+  // (rare O rescale).  Even groups live in scA, odd ones in scB.  Every wave
+  // runs all groups of the block; groups past its queries are fully masked.
+  const uint32_t lds0 = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t *)fsm));
+  uint32_t kb[4], rb[4], vb0, vb1;
+  f32x16 scA[F_NQG], scB[F_NQG];
+  u32x4 pb[F_NQG][2];  // [qg][16-key step]: bf16 P of the group being accumulated
+  float nm[F_NQG];     // -running max (scaled) per query group
+  float mx[F_NQG];
+  int lim0[F_NQG];     // query position - first key of the lane's rows, for group 0
 #pragma unroll
-      for (int ks = 0; ks < P_QK / 32; ++ks) {
+  for (int qg = 0; qg < F_NQG; ++qg) lim0[qg] = pos0 + s_wave + 32 * qg + j32 - 4 * hh;
+  constexpr int FD = 4;
+
+#define FL_KBASE(STG)                                      \
+  {                                                        \
+    const uint32_t sb_ = lds0 + (STG) * F_STAGE;           \
+    _Pragma("unroll") for (int k4 = 0; k4 < 4; ++k4) {     \
+      kb[k4] = sb_ + koff[k4];                             \
+      rb[k4] = sb_ + roff[k4];                             \
+    }                                                      \
+  }
+#define FL_VBASE(STG)                                      \
+  {                                                        \
+    const uint32_t sb_ = lds0 + (STG) * F_STAGE;           \
+    vb0 = sb_ + voff[0];                                   \
+    vb1 = sb_ + voff[1];                                   \
+  }
+#define FL_RDK(D, KS, KG)                                                                      \
+  asm volatile("ds_read_b128 %0, %1 offset:%2"                                                \
+               : "=v"(D)                                                                      \
+               : "v"((KS) < 8 ? kb[(KS) & 3] : rb[(KS) & 3]),                                 \
+                 "i"((KS) < 8 ? ((KS) >> 2) * 128 + (KG) * 8192 : (KG) * 4096)                \
+               : "memory")
+  // exp slice q4 of query group QG of SCE (rows 4 q4 .. +3) -> pb, l.  The
+  // empty asm statements pin each slice between the MFMAs it is meant to
+  // overlap (IR passes would otherwise sink it next to its first use).
+#define FL_EXP(SCE, QG, Q4)                                                                         \
+  {                                                                                                \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                                \
+      SCE[QG][4 * (Q4) + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(SCE[QG][4 * (Q4) + i], sl2, nm[QG])); \
+      asm volatile("" : "+v"(SCE[QG][4 * (Q4) + i]));                                               \
+    }                                                                                              \
+    if ((Q4) & 1) {                                                                                \
+      const int b_ = 8 * ((Q4) >> 1);                                                              \
+      const u32x4 pk_ = {pack_bf16(SCE[QG][b_], SCE[QG][b_ + 1]), pack_bf16(SCE[QG][b_ + 2], SCE[QG][b_ + 3]), \
+                         pack_bf16(SCE[QG][b_ + 4], SCE[QG][b_ + 5]), pack_bf16(SCE[QG][b_ + 6], SCE[QG][b_ + 7])}; \
+      pb[QG][(Q4) >> 1] = pk_;                                                                     \
+      asm volatile("" : "+v"(pb[QG][(Q4) >> 1]));                                                  \
+      _Pragma("unroll") for (int i = 0; i < 8; ++i) l_run[QG] += SCE[QG][b_ + i];                    \
+      asm volatile("" : "+v"(l_run[QG]));                                                          \
+    }                                                                                              \
+  }
+  // S^T of one 32-key group (half KG of the stage in kb/rb) into SC; with
+  // DOEXP, the exp of SCE rides along (8 slices over the first 8 K steps)
+#define FL_S(SC, KG, SCE, DOEXP)                                                                   \
+  {                                                                                                \
+    u32x4 ka[FD];                                                                                  \
+    _Pragma("unroll") for (int d = 0; d < FD; ++d) FL_RDK(ka[d], d, KG);                          \
+    _Pragma("unroll") for (int ks = 0; ks < 12; ++ks) {                                            \
+      const int c = ks % FD;                                                                       \
+      const int later = (11 - ks) < (FD - 1) ? (11 - ks) : (FD - 1);                              \
+      if (later == 3) asm volatile("s_waitcnt lgkmcnt(3)" : "+v"(ka[c])::"memory");               \
+      else if (later == 2) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(ka[c])::"memory");          \
+      else if (later == 1) asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(ka[c])::"memory");          \
+      else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ka[c])::"memory");                          \
+      _Pragma("unroll") for (int qg = 0; qg < F_NQG; ++qg) {                                       \
+        if (ks == 0)                                                                               \
+          asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0"                          \
+                       : "=&v"(SC[qg])                                                             \
+                       : "v"(ka[c]), "a"(qf[qg][ks]));                                             \
+        else                                                                                       \
+          asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"                                    \
+                       : "+v"(SC[qg])                                                              \
+                       : "v"(ka[c]), "a"(qf[qg][ks]));                                             \
+      }                                                                                            \
+      if (ks + FD < 12) FL_RDK(ka[c], ks + FD, KG);                                               \
+      __builtin_amdgcn_sched_barrier(0);                                                           \
+      if ((DOEXP) && ks < 4 * F_NQG) FL_EXP(SCE, ks >> 2, ks & 3);                                 \
+      __builtin_amdgcn_sched_barrier(0);                                                           \
+    }                                                                                              \
+    /* MFMA results are read by VALU code the compiler schedules: cover the */                     \
+    /* write-to-read wait states of the asm MFMAs above */                                         \
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");                                   \
+    _Pragma("unroll") for (int qg = 0; qg < F_NQG; ++qg) asm volatile("" : "+v"(SC[qg]));            \
+  }
+  // mask (keys of group GI past the lane's query) and max slice I of SCN
+#define FL_MAXS(SCN, I, GI, MASKED)                                                                \
+  {                                                                                                \
+    const int qg_ = (I) >> 2, r0_ = 4 * ((I) & 3);                                                 \
+    if (MASKED) {                                                                                  \
+      const int lim_ = lim0[qg_] - 32 * (GI);                                                      \
+      _Pragma("unroll") for (int i = 0; i < 4; ++i) if (8 * ((r0_ + i) >> 2) + ((r0_ + i) & 3) > lim_) \
+          SCN[qg_][r0_ + i] = -INFINITY;                                                           \
+    }                                                                                              \
+    mx[qg_] = __builtin_fmaxf(__builtin_fmaxf(mx[qg_], SCN[qg_][r0_]), SCN[qg_][r0_ + 1]);        \
+    mx[qg_] = __builtin_fmaxf(__builtin_fmaxf(mx[qg_], SCN[qg_][r0_ + 2]), SCN[qg_][r0_ + 3]);    \
+    asm volatile("" : "+v"(mx[qg_]));                                                              \
+  }
+#define FL_TR(D, BASE, OFS)                                                                          \
+  asm volatile(                                                                                     \
+      "ds_read_b64_tr_b16 %0, %4 offset:%5\n\tds_read_b64_tr_b16 %1, %4 offset:%6\n\t"              \
+      "ds_read_b64_tr_b16 %2, %4 offset:%7\n\tds_read_b64_tr_b16 %3, %4 offset:%8"                  \
+      : "=&v"(D[0]), "=&v"(D[1]), "=&v"(D[2]), "=&v"(D[3])                                          \
+      : "v"(BASE), "i"(OFS), "i"(OFS + 2048), "i"(OFS + 4096), "i"(OFS + 6144)                      \
+      : "memory")
+#define FL_WAIT(N, D) \
+  asm volatile("s_waitcnt lgkmcnt(" #N ")" : "+v"(D[0]), "+v"(D[1]), "+v"(D[2]), "+v"(D[3])::"memory")
+  // PV of one 16-key step kk of 32-column block VT, then max slice 2 VT + kk of SCN
+#define FL_PVSTEP(VT, D, KK, SCN, GI, DOMAX, MASKED)                                                  \
+  {                                                                                                  \
+    const bf16x8 a_ = as_bf16x8(u32x4{D[2 * (KK)].x, D[2 * (KK)].y, D[2 * (KK) + 1].x, D[2 * (KK) + 1].y}); \
+    _Pragma("unroll") for (int qg = 0; qg < F_NQG; ++qg) o[VT][qg] = mfma32(a_, as_bf16x8(pb[qg][KK]), o[VT][qg]); \
+    __builtin_amdgcn_sched_barrier(0);                                                               \
+    if ((DOMAX) && 2 * (VT) + (KK) < 4 * F_NQG) FL_MAXS(SCN, 2 * (VT) + (KK), GI, MASKED);          \
+    __builtin_amdgcn_sched_barrier(0);                                                               \
+  }
+  // O^T += V^T P^T for the group in half KG of the stage in vb0/vb1 (three
+  // column blocks of transpose reads in flight); with DOMAX the mask/max of
+  // SCN (group GI) rides along
+#define FL_PV(KG, SCN, GI, DOMAX, MASKED)                                                             \
+  {                                                                                                  \
+    if (DOMAX) _Pragma("unroll") for (int qg = 0; qg < F_NQG; ++qg) mx[qg] = -INFINITY;              \
+    u32x2 tv[3][4];                                                                                  \
+    FL_TR(tv[0], vb0, (KG) * 8192);                                                                  \
+    FL_TR(tv[1], vb1, (KG) * 8192);                                                                  \
+    FL_TR(tv[2], vb0, (KG) * 8192 + 128);                                                            \
+    FL_WAIT(8, tv[0]);                                                                               \
+    FL_PVSTEP(0, tv[0], 0, SCN, GI, DOMAX, MASKED);                                                  \
+    FL_PVSTEP(0, tv[0], 1, SCN, GI, DOMAX, MASKED);                                                  \
+    FL_TR(tv[0], vb1, (KG) * 8192 + 128);                                                            \
+    FL_WAIT(8, tv[1]);                                                                               \
+    FL_PVSTEP(1, tv[1], 0, SCN, GI, DOMAX, MASKED);                                                  \
+    FL_PVSTEP(1, tv[1], 1, SCN, GI, DOMAX, MASKED);                                                  \
+    FL_WAIT(4, tv[2]);                                                                               \
+    FL_PVSTEP(2, tv[2], 0, SCN, GI, DOMAX, MASKED);                                                  \
+    FL_PVSTEP(2, tv[2], 1, SCN, GI, DOMAX, MASKED);                                                  \
+    FL_WAIT(0, tv[0]);                                                                               \
+    FL_PVSTEP(3, tv[0], 0, SCN, GI, DOMAX, MASKED);                                                  \
+    FL_PVSTEP(3, tv[0], 1, SCN, GI, DOMAX, MASKED);                                                  \
+  }
+  // running max after the group's scores are maximised; O and l rescale when it moves
+#define FL_MAXFIN()                                                                                 \
+  {                                                                                                \
+    bool grow_[F_NQG], any_ = false;                                                               \
+    float mn_[F_NQG];                                                                              \
+    _Pragma("unroll") for (int qg = 0; qg < F_NQG; ++qg) {                                         \
+      const auto sw_ = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx[qg]), __float_as_uint(mx[qg]), false, false); \
+      mn_[qg] = __builtin_fmaxf(__uint_as_float(sw_[0]), __uint_as_float(sw_[1])) * sl2;           \
+      grow_[qg] = mn_[qg] > m_run[qg] + 8.f;                                                       \
+      any_ = any_ || grow_[qg];                                                                    \
+    }                                                                                              \
+    if (__builtin_amdgcn_ballot_w64(any_)) {                                                       \
+      _Pragma("unroll") for (int qg = 0; qg < F_NQG; ++qg) {                                       \
+        const float alpha_ = grow_[qg] ? __builtin_amdgcn_exp2f(m_run[qg] - mn_[qg]) : 1.f;        \
+        m_run[qg] = grow_[qg] ? mn_[qg] : m_run[qg];                                               \
+        l_run[qg] *= alpha_;                                                                       \
+        _Pragma("unroll") for (int vt = 0; vt < 4; ++vt) o[vt][qg] *= alpha_;                     \
+      }                                                                                            \
+    }                                                                                              \
+    _Pragma("unroll") for (int qg = 0; qg < F_NQG; ++qg) nm[qg] = -m_run[qg];                      \
+  }
+
+  // prologue: tile 0 landed; S_0 and its max
+  if (ntiles > 1) wait_vmcnt<F_DMA>();
+  else wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  FL_KBASE(0);
+  FL_S(scA, 0, scB, 0);
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8 *>(K + (mt * 16 + li) * P_KLD + ks * 32 + 8 * lg);
+  for (int qg = 0; qg < F_NQG; ++qg) mx[qg] = -INFINITY;
+  {
+    const bool diag = 31 > pos0 + s_wave;
 #pragma unroll
-          for (int nt = 0; nt < 4; ++nt) sc[mt][nt] = mfma16(a, qf[nt][ks], sc[mt][nt]);
-        }
-      }
-      bf16x8 pf[4];
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const int qpos = pos0 + s_wave + nt * 16 + li;
-        float sv[8];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int t = t0 + mt * 16 + 4 * lg + r;
-            const float v = (t <= qpos) ? sc[mt][nt][r] * p.scale_log2 : -INFINITY;
-            sv[mt * 4 + r] = v;
-            mx = fmaxf(mx, v);
-          }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run[nt], mx);
-        const float alpha = (m_run[nt] == -INFINITY) ? 0.f : exp2f(m_run[nt] - m_new);
-        float pv[8], lsum = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          pv[e] = (sv[e] == -INFINITY) ? 0.f : exp2f(sv[e] - m_new);
-          lsum += pv[e];
-        }
-        l_run[nt] = l_run[nt] * alpha + lsum;
-        m_run[nt] = m_new;
-        if (__any(alpha != 1.f)) {
-#pragma unroll
-          for (int vt = 0; vt < P_V / 16; ++vt) o[vt][nt] *= alpha;
-        }
-        u32x4 pk = {pack_bf16(pv[0], pv[1]), pack_bf16(pv[2], pv[3]), pack_bf16(pv[4], pv[5]),
-                    pack_bf16(pv[6], pv[7])};
-        pf[nt] = as_bf16x8(pk);
-      }
-#pragma unroll
-      for (int vt = 0; vt < P_V / 16; ++vt) {
-        const uint16_t *vr = V + (vt * 16 + li) * P_VLD + 4 * lg;
-        const u32x2 lo = *reinterpret_cast<const u32x2 *>(vr);
-        const u32x2 hi = *reinterpret_cast<const u32x2 *>(vr + 16);
-        const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) o[vt][nt] = mfma16(a, pf[nt], o[vt][nt]);
-      }
+    for (int i = 0; i < 4 * F_NQG; ++i) FL_MAXS(scA, i, 0, diag);
+  }
+  FL_MAXFIN();
+
+  int stg = 0;  // stage of tile j
+  for (int j = 0; j < ntiles; ++j) {
+    const int g = 2 * j;
+    // ---- group g (even): S_{g+1} (same tile, half 1) || exp of scA; PV_g || max of scB
+    FL_S(scB, 1, scA, 1);
+    FL_VBASE(stg);
+    {
+      const bool diag = 32 * (g + 1) + 31 > pos0 + s_wave;
+      FL_PV(0, scB, g + 1, 1, diag);
     }
-    if (more) flash_store(R, Ks[buf ^ 1], Vs[buf ^ 1]);
-    __syncthreads();
+    FL_MAXFIN();
+    // ---- group g+1 (odd): S_{g+2} (tile j+1, half 0) || exp of scB; PV_{g+1} || max of scA.
+    // After the last tile S_{g+2} re-reads the current stage and is discarded.
+    const bool more = j + 1 < ntiles;
+    int stn = stg;
+    if (more) {
+      // tile j+1 landed in every wave; tile j-1's stage is free for tile j+2
+      wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      stn = stg == F_NST - 1 ? 0 : stg + 1;
+      if (j + 2 < ntiles)
+        flash_dma(p, h, (j + 2) * F_KT, Tlim, fsm + (stn == F_NST - 1 ? 0 : stn + 1) * F_STAGE, wave, lane, fl);
+    }
+    FL_KBASE(stn);
+    FL_S(scA, 0, scB, 1);
+    {
+      const bool diag = 32 * (g + 2) + 31 > pos0 + s_wave;
+      FL_PV(1, scA, g + 2, 1, diag);
+    }
+    if (more) FL_MAXFIN();
+    stg = stn;
   }
-  // normalise and store: lane holds query col nt*16+li, v rows vt*16 + 4*lg .. +3
+#undef FL_KBASE
+#undef FL_VBASE
+#undef FL_RDK
+#undef FL_EXP
+#undef FL_S
+#undef FL_MAXS
+#undef FL_TR
+#undef FL_WAIT
+#undef FL_PVSTEP
+#undef FL_PV
+#undef FL_MAXFIN
+  wait_vmcnt<0>();
+
+  // normalise and store: lane holds query 32 qg + j32, values 32 vt + 8 (r/4) + 4 hh + r%4
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    float l = l_run[nt];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    const int s = s_wave + nt * 16 + li;
-    if (s >= p.S) continue;
+  for (int qg = 0; qg < F_NQG; ++qg) {
+    float l = l_run[qg];
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+      l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    const int s = s_wave + 32 * qg + j32;
+    if (!wave_active || s >= p.S) continue;
     const float inv = 1.f / l;
-    uint16_t *dst = p.out + (size_t)(p.b * p.S + s) * (P_H * P_V) + h * P_V + 4 * lg;
+    uint16_t *dst = p.out + (size_t)(p.b * p.S + s) * (P_H * P_V) + h * P_V + 4 * hh;
 #pragma unroll
-    for (int vt = 0; vt < P_V / 16; ++vt) {
-      const f32x4 v = o[vt][nt] * inv;
-      *reinterpret_cast<u32x2 *>(dst + vt * 16) = u32x2{pack_bf16(v.x, v.y), pack_bf16(v.z, v.w)};
-    }
+    for (int vt = 0; vt < 4; ++vt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const f32x16 &v = o[vt][qg];
+        *reinterpret_cast<u32x2 *>(dst + 32 * vt + 8 * q4) =
+            u32x2{pack_bf16(v[4 * q4] * inv, v[4 * q4 + 1] * inv), pack_bf16(v[4 * q4 + 2] * inv, v[4 * q4 + 3] * inv)};
+      }
   }
 }
 
@@ -529,7 +763,13 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
     pk.y = kvb; pk.ldy = pk.N; pk.seq_len = 1;
     if ((rc = run_linear(pk, GEMV_PLAIN, st))) return rc;
     fp.b = b;
-    flash_kernel<<<dim3(P_H, (S + P_QB - 1) / P_QB), 256, 0, st>>>(fp);
+    static bool flash_attr = false;  // dynamic LDS above 64 KB
+    if (!flash_attr) {
+      (void)hipFuncSetAttribute((const void *)flash_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, F_LDS);
+      flash_attr = true;
+    }
+    fp.nqb = (S + F_QB - 1) / F_QB;
+    flash_kernel<<<dim3(P_H * fp.nqb), F_NW * 64, F_LDS, st>>>(fp);
     if ((rc = check_launch("flash attention"))) return rc;
   }
 
