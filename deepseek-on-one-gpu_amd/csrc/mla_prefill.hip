@@ -7,12 +7,10 @@
 // per call (one GEMM), and causal flash attention runs per head with
 // d_qk = 128 + 64 (the rope key shared by all heads) and d_v = 128.
 //
-// GEMM (K3): C[m, n] = sum_k X[m, k] W[n, k] scale_inv[n/128, k/128].
-//   Workgroup tile 128 (weight rows n) x 128 (activation rows m), K step 64,
-//   double-buffered in LDS; fp8 weights are converted exactly to bf16 when
-//   staged.  The weight tile spans one 128-row scale block, so the scale of a
-//   128-wide K block is one scalar per workgroup: MFMAs accumulate the block
-//   into a fresh fp32 tile which is then added to the result times that scale.
+// GEMM (K3): C[m, n] = sum_k X[m, k] W[n, k] scale_inv[n/128, k/128], with
+//   256 x 256 workgroup tiles, LDS-DMA staging of fp8 weights and bf16
+//   activations, exact in-register fp8 -> bf16 conversion, 32x32x16 MFMAs and
+//   a running-scale accumulator for the 128 x 128 block scales.
 #include <math.h>
 
 #include <algorithm>
@@ -67,108 +65,176 @@ AMLA_DEV void pstore4(const GemvParams &p, int m, int n, f32x4 v) {
 
 // ---------------------------------------------------------------- K3 GEMM
 
-constexpr int G_BN = 128, G_BM = 128, G_BK = 64;
-constexpr int G_LD = G_BK + 8;  // bf16 per LDS row (16 B pad)
+AMLA_DEV f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+
+// Workgroup tile 256 weight rows (n) x 256 activation rows (m), K stage 64,
+// three LDS stages filled by direct global-to-LDS copies: fp8 weight rows
+// (64 B) and bf16 activation rows (128 B), 16-byte chunks swizzled per row
+// (chunk c of weight row r at c ^ ((r >> 1) & 3), of activation row r at
+// c ^ (r & 7)) so the fragment reads hit distinct banks.  Eight waves (two
+// per SIMD), each 128 (n) x 64 (m) with 32x32x16 MFMAs; weight fragments are
+// converted exactly from fp8 to bf16 in registers.
+//
+// Block scales: a wave's 128 weight rows are one scale block, so the scale of
+// a 128-wide K block is one number s_kb for the whole wave tile.  The
+// accumulator is kept in units of the current block's scale: entering block
+// kb it is multiplied by s_{kb-1} / s_kb, and the result is acc * s_last.
+// This equals sum_kb s_kb * partial_kb up to fp32 rounding of the ratios
+// (~1e-5 relative over 128 blocks, far below the bf16 output rounding).  A
+// block with s_kb == 0 dequantises to zero and is skipped.
+constexpr int G_BN = 256, G_BM = 256, G_BK = 64, G_NST = 3, G_NW = 8;
+constexpr int G_WOFF = 0, G_XOFF = G_BN * G_BK;  // fp8 weight rows, then bf16 activation rows
+constexpr int G_STAGE = G_BN * G_BK + G_BM * G_BK * 2;
+constexpr int G_LDS = G_NST * G_STAGE;           // 144 KB
+constexpr int G_DMA = G_STAGE / 1024 / G_NW;     // copies per wave per stage
 
 template <int MODE>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemvParams p) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int li = lane & 15, lg = lane >> 4;
+__global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p) {
+  extern __shared__ __align__(16) uint8_t gsm[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave & 1, wm = wave >> 1;
-  const int nb = blockIdx.x;  // 128-row weight block == scale row block
-  const int m0 = blockIdx.y * G_BM;
-  const int KB = p.K >> 7;
-
-  __shared__ __align__(16) uint16_t Ws[2][G_BN * G_LD];
-  __shared__ __align__(16) uint16_t Xs[2][G_BM * G_LD];
-
-  const int n0 = nb * G_BN;
+  const int j32 = lane & 31, hh = lane >> 5;
+  const int n0 = blockIdx.x * G_BN, m0 = blockIdx.y * G_BM;
   const bool seg1 = (MODE == GEMV_QKVA) && n0 >= p.n_split;
   const uint8_t *W = seg1 ? p.w1 : p.w0;
   const float *S = seg1 ? p.s1 : p.s0;
   const int nl0 = seg1 ? n0 - p.n_split : n0;
-  const int nrows = (seg1 ? p.N - p.n_split : p.n_split) - nl0;  // valid rows of this segment from nl0
-  const float *srow = S + (size_t)(nl0 >> 7) * KB;
+  const int nvalid = (seg1 ? p.N - p.n_split : p.n_split) - nl0;  // rows of this segment from nl0
+  const int KB = p.K >> 7;
+  const bool wave_rows = wn * 128 < nvalid;
+  const __attribute__((address_space(4))) float *srow = (const __attribute__((address_space(4))) float *)(
+      S + (size_t)((nl0 + min(wn * 128, nvalid - 1)) >> 7) * KB);
 
-  // loader roles: weight row tid/2 (32 bytes at (tid&1)*32), x row tid/2 (32 elements)
-  const int lr = tid >> 1, lh = tid & 1;
-  const bool wvalid = lr < nrows;
-  const uint8_t *wsrc = W + (size_t)(wvalid ? nl0 + lr : 0) * p.K + lh * 32;
-  const bool xvalid = m0 + lr < p.M;
-  const uint16_t *xsrc = p.x + (size_t)(xvalid ? m0 + lr : 0) * p.ldx + lh * 32;
-
-  u32x4 wreg[2], xreg[4];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) wreg[j] = wvalid ? ldg16(wsrc + k0 + j * 16) : u32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) xreg[j] = xvalid ? ldg16(xsrc + k0 + j * 8) : u32x4{0, 0, 0, 0};
-  };
-  auto sstore = [&](int buf) {
-    uint16_t *wd = &Ws[buf][lr * G_LD + lh * 32];
+  // copies: wave w fills weight rows 32w .. +31 (two copies of 16 rows) and
+  // activation rows 32w .. +31 (four copies of 8 rows) of each stage
+  const bool wfull = nvalid >= G_BN, xfull = m0 + G_BM <= p.M;
+  const uint32_t wlane = (uint32_t)(lane >> 2) * p.K + 16 * ((lane & 3) ^ ((lane >> 3) & 3));
+  const uint32_t xlane = (uint32_t)(lane >> 3) * p.ldx * 2 + 16 * ((lane & 7) ^ (lane >> 3));
+  auto dma = [&](int it, uint8_t *st) {
+    const int k0 = it * G_BK;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      bf16x8 lo, hi;
-      fp8x16_to_bf16x16(wreg[j], lo, hi);
-      *reinterpret_cast<bf16x8 *>(wd + j * 16) = lo;
-      *reinterpret_cast<bf16x8 *>(wd + j * 16 + 8) = hi;
+      const int r0 = 32 * wave + 16 * j;
+      const uint8_t *src;
+      if (wfull) {
+        src = W + (size_t)(nl0 + r0) * p.K + k0 + wlane;
+      } else {
+        const int r = min(r0 + (lane >> 2), nvalid - 1);
+        src = W + (size_t)(nl0 + r) * p.K + k0 + 16 * ((lane & 3) ^ ((lane >> 3) & 3));
+      }
+      __builtin_amdgcn_global_load_lds(src, LDS_PTR(st + G_WOFF + r0 * G_BK), 16, 0, 0);
     }
-    uint16_t *xd = &Xs[buf][lr * G_LD + lh * 32];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4 *>(xd + j * 8) = xreg[j];
-  };
-
-  f32x4 acc[4][4], blk[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = blk[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int iters = p.K / G_BK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int it = 0; it < iters; ++it) {
-    const int buf = it & 1;
-    if (it + 1 < iters) gload((it + 1) * G_BK);
-    const uint16_t *wb = Ws[buf];
-    const uint16_t *xb = Xs[buf];
-#pragma unroll
-    for (int ks = 0; ks < G_BK / 32; ++ks) {
-      bf16x8 a[4], bm[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a[i] = *reinterpret_cast<const bf16x8 *>(wb + (wn * 64 + i * 16 + li) * G_LD + ks * 32 + 8 * lg);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bm[j] = *reinterpret_cast<const bf16x8 *>(xb + (wm * 64 + j * 16 + li) * G_LD + ks * 32 + 8 * lg);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) blk[i][j] = mfma16(a[i], bm[j], blk[i][j]);
-    }
-    if (it & 1) {  // end of a 128-wide K block: apply its scale
-      const float sk = srow[it >> 1];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc[i][j] += sk * blk[i][j];
-          blk[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-    if (it + 1 < iters) sstore(buf ^ 1);
-    __syncthreads();
-  }
-  // C layout: lane holds m = mt*16 + li, n = nt*16 + 4*lg .. +3
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int n = n0 + wn * 64 + i * 16 + 4 * lg;
-    if (n >= p.N) continue;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int m = m0 + wm * 64 + j * 16 + li;
-      if (m < p.M) pstore4<MODE>(p, m, n, acc[i][j]);
+      const int r0 = 32 * wave + 8 * j;
+      const uint8_t *src;
+      if (xfull) {
+        src = reinterpret_cast<const uint8_t *>(p.x + (size_t)(m0 + r0) * p.ldx + k0) + xlane;
+      } else {
+        const int r = min(m0 + r0 + (lane >> 3), p.M - 1);
+        src = reinterpret_cast<const uint8_t *>(p.x + (size_t)r * p.ldx + k0) + 16 * ((lane & 7) ^ (lane >> 3));
+      }
+      __builtin_amdgcn_global_load_lds(src, LDS_PTR(st + G_XOFF + r0 * (G_BK * 2)), 16, 0, 0);
+    }
+  };
+
+  // fragment offsets: weight rows wn*128 + 32 g + j32, chunk (2 pr + hh) of
+  // the 64-byte row (K 32 pr + 16 hh .. +15, two MFMA steps of 8); activation
+  // rows wm*64 + 32 j + j32, chunks 4 pr + 2 hh + s (K 32 pr + 16 hh + 8 s ..)
+  uint32_t aoff[2], boff[2][2];
+#pragma unroll
+  for (int pr = 0; pr < 2; ++pr) {
+    aoff[pr] = G_WOFF + (wn * 128 + j32) * G_BK + 16 * ((2 * pr + hh) ^ ((j32 >> 1) & 3));
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+      boff[pr][st] = G_XOFF + (wm * 64 + j32) * (G_BK * 2) + 16 * ((4 * pr + 2 * hh + st) ^ (j32 & 7));
+  }
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[g][j][r] = 0.f;
+  float s_run = 0.f;
+  bool skip = false;
+
+  const int iters = p.K / G_BK;
+  dma(0, gsm);
+  if (iters > 1) dma(1, gsm + G_STAGE);
+  int stg = 0;
+  for (int it = 0; it < iters; ++it) {
+    if (it + 1 < iters) wait_vmcnt<G_DMA>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (it + 2 < iters) dma(it + 2, gsm + (stg == 0 ? 2 : stg - 1) * G_STAGE);
+    if ((it & 1) == 0) {
+      const float sk = srow[it >> 1];
+      skip = sk == 0.f;
+      if (!skip) {
+        if (s_run != 0.f) {
+          const float r = __fdiv_rn(s_run, sk);
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[g][j] *= r;
+        }
+        s_run = sk;
+      }
+    }
+    if (!skip) {
+      const uint8_t *st = gsm + stg * G_STAGE;
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {
+        u32x4 araw[4], bx[2][2];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) araw[g] = *reinterpret_cast<const u32x4 *>(st + aoff[pr] + g * 32 * G_BK);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2)
+            bx[j][s2] = *reinterpret_cast<const u32x4 *>(st + boff[pr][s2] + j * 32 * (G_BK * 2));
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+            const uint32_t w0 = araw[g][2 * s2], w1 = araw[g][2 * s2 + 1];
+            const bf16x2_t c0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.f, false);
+            const bf16x2_t c1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.f, true);
+            const bf16x2_t c2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.f, false);
+            const bf16x2_t c3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.f, true);
+            const bf16x8 a = {c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[g][j] = mfma32(a, as_bf16x8(bx[j][s2]), acc[g][j]);
+          }
+      }
+    }
+    stg = stg == G_NST - 1 ? 0 : stg + 1;
+  }
+
+  // C[n][m]: lane holds m = 32 j + j32 of its rows, n = 32 g + 8 q + 4 hh .. +3
+  if (wave_rows) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int m = m0 + wm * 64 + 32 * j + j32;
+      if (m >= p.M) continue;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n0 + wn * 128 + 32 * g + 8 * q + 4 * hh;
+          if (n < p.N)
+            pstore4<MODE>(p, m, n,
+                          f32x4{acc[g][j][4 * q], acc[g][j][4 * q + 1], acc[g][j][4 * q + 2], acc[g][j][4 * q + 3]} *
+                              s_run);
+        }
     }
   }
 }
@@ -176,15 +242,25 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemvParams p) {
 size_t gemm_ws_bytes(int, int, int) { return 0; }
 
 int launch_gemm(const GemvParams &p, int mode, hipStream_t st) {
-  if (p.K % 128 || p.N % 16) return fail(AMLA_EUNSUPPORTED, "fp8 GEMM needs K %% 128 == 0 and N %% 16 == 0");
-  if (mode == GEMV_QKVA ? (p.n_split % 128) : 0)
-    return fail(AMLA_EUNSUPPORTED, "fp8 GEMM: q_lora must be a multiple of 128");
+  if (p.K % 128 || p.N % 4) return fail(AMLA_EUNSUPPORTED, "fp8 GEMM needs K %% 128 == 0 and N %% 4 == 0");
+  if (p.ldx % 8) return fail(AMLA_EUNSUPPORTED, "fp8 GEMM needs 16-byte aligned activation rows");
+  if (mode == GEMV_QKVA && p.n_split % G_BN)
+    return fail(AMLA_EUNSUPPORTED, "fp8 GEMM: q_lora must be a multiple of 256");
+  static bool attr_set[4] = {false, false, false, false};  // dynamic LDS above 64 KB, once per mode
+  const void *fn = mode == GEMV_PLAIN  ? (const void *)gemm_kernel<GEMV_PLAIN>
+                   : mode == GEMV_RESID ? (const void *)gemm_kernel<GEMV_RESID>
+                   : mode == GEMV_QKVA  ? (const void *)gemm_kernel<GEMV_QKVA>
+                                        : (const void *)gemm_kernel<GEMV_QROPE>;
+  if (!attr_set[mode & 3]) {
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS);
+    attr_set[mode & 3] = true;
+  }
   dim3 grid((p.N + G_BN - 1) / G_BN, (p.M + G_BM - 1) / G_BM);
   switch (mode) {
-    case GEMV_PLAIN: gemm_kernel<GEMV_PLAIN><<<grid, 256, 0, st>>>(p); break;
-    case GEMV_RESID: gemm_kernel<GEMV_RESID><<<grid, 256, 0, st>>>(p); break;
-    case GEMV_QKVA: gemm_kernel<GEMV_QKVA><<<grid, 256, 0, st>>>(p); break;
-    default: gemm_kernel<GEMV_QROPE><<<grid, 256, 0, st>>>(p); break;
+    case GEMV_PLAIN: gemm_kernel<GEMV_PLAIN><<<grid, G_NW * 64, G_LDS, st>>>(p); break;
+    case GEMV_RESID: gemm_kernel<GEMV_RESID><<<grid, G_NW * 64, G_LDS, st>>>(p); break;
+    case GEMV_QKVA: gemm_kernel<GEMV_QKVA><<<grid, G_NW * 64, G_LDS, st>>>(p); break;
+    default: gemm_kernel<GEMV_QROPE><<<grid, G_NW * 64, G_LDS, st>>>(p); break;
   }
   return check_launch("fp8 GEMM");
 }
@@ -280,10 +356,6 @@ AMLA_DEV void flash_dma(const FlashParams &p, int h, int t0, int Tlim, uint8_t *
     __builtin_amdgcn_global_load_lds(kr + (size_t)t * (P_ROPE * 2) + 16 * (c8 ^ r8), LDS_PTR(stage + F_RPE + row * 128),
                                      16, 0, 0);
   }
-}
-
-AMLA_DEV f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 // Grid H x (query blocks of 256), 256 threads, 120 KB of LDS: one workgroup
