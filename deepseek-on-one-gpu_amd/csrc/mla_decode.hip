@@ -590,61 +590,117 @@ AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, int split, floa
   o1 = a1;
 }
 
-// Grid (H, B): blockIdx.x = head, so one head's workgroups (all sequences)
-// land on the same XCD (XCD = workgroup id mod 8) and share W_UV[h] in L2.
-// Merges the splits with an online max (exact recomputation for flagged
-// ones), folds kv_a_layernorm gamma, then out[v] = W_UV[h][v] . lat.
+// Grid (H, ceil(B / 4)): workgroup (h, g) finishes sequences 4g .. 4g+3 of
+// head h, so W_UV[h] is read once per four sequences.
+//   wave w merges the splits of sequence 4g + w (lane: latent columns
+//     8l .. 8l+7, one 16-byte load per split), online max over the splits;
+//   a sequence with a flagged split is merged by the whole workgroup with
+//     exact recomputation of the flagged splits (rare);
+//   lat = O / l times kv_a_layernorm gamma and W_UV's block scale, as bf16;
+//   out[b][v] = W_UV[h][v] . lat[b] by 16x16x32 MFMAs: A = W_UV rows (fp8
+//     converted exactly), B = lat of the four sequences (columns 4.. zero);
+//     wave w produces rows v = 32w .. 32w+31.
 __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const uint8_t *__restrict__ wkvb,
                                                          const float *__restrict__ skvb,
-                                                         const uint16_t *__restrict__ gamma,
+                                                         const uint16_t *__restrict__ gamma, int B,
                                                          uint16_t *__restrict__ attn) {
-  const int h = blockIdx.x, b = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  __shared__ float lat[LORA];
+  constexpr int SQ = 4;     // sequences per workgroup
+  constexpr int LROW = LORA + 8;  // bf16 per lat row in LDS (16 B pad)
+  const int h = blockIdx.x, b0 = blockIdx.y * SQ;
+  const int nb = min(SQ, B - b0);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __shared__ __align__(16) uint16_t latb[SQ][LROW];
+  __shared__ float wsp[SQ][256 + 16];
   __shared__ float qs[QKD];
   __shared__ float ps[256];
   __shared__ float red[4];
-  __shared__ float wsp[256];
-  __shared__ int s_flag;
-  const size_t base = (size_t)b * ap.splits * HEADS + h;
-  float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
-  // fast path: every split carries a valid (m, l, O); max, weights, then a
-  // weighted sum with independent loads (splits <= 256)
-  float ms = -INFINITY, ls = 0.f;
-  if (tid < ap.splits) {
-    ms = ap.part_ml[(base + (size_t)tid * HEADS) * 2];
-    ls = ap.part_ml[(base + (size_t)tid * HEADS) * 2 + 1];
-  }
-  if (tid == 0) s_flag = 0;
-  __syncthreads();
-  if (ls < 0.f) s_flag = 1;
-  M = block_reduce(ms, red, true);
-  if (!s_flag) {
-    const float w = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
-    if (tid < ap.splits) wsp[tid] = w;
-    L = block_reduce(w * ls, red, false);
-    // thread tid: latent columns 2*tid, 2*tid+1 (one 4-byte bf16 pair per split)
-    const uint32_t *po = reinterpret_cast<const uint32_t *>(ap.part_o + base * LORA) + tid;
-    const size_t stride = (size_t)HEADS * LORA / 2;
-    int s = 0;
-    for (; s + 16 <= ap.splits; s += 16) {
-      uint32_t v[16];
+  __shared__ int s_flag[SQ];
+  float bsc[4];  // W_UV block scales of the four 128-column blocks
 #pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] = po[(s + j) * stride];
+  for (int q = 0; q < 4; ++q) bsc[q] = skvb[(size_t)(2 * h + 1) * (LORA / 128) + q];
+
+  // W_UV rows of this wave (rows v = 32w .. 32w+31, 8 bytes per lane and K
+  // step) are loaded first: nothing they feed depends on the merge
+  const int li = lane & 15, lg = lane >> 4;
+  const uint8_t *wr = wkvb + ((size_t)h * (NOPE + VD) + NOPE + 32 * wave + li) * LORA + 8 * lg;
+  u32x2 wa[2][LORA / 32];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        a0 += wsp[s + j] * lo_bf(v[j]);
-        a1 += wsp[s + j] * hi_bf(v[j]);
+  for (int vt = 0; vt < 2; ++vt)
+#pragma unroll
+    for (int ks = 0; ks < LORA / 32; ++ks) wa[vt][ks] = ldg8(wr + (size_t)vt * 16 * LORA + ks * 32);
+
+  // ---- fast merge: wave w, sequence b0 + w.  The first 16 splits' partial
+  // rows are in flight while the max and the weights are formed.
+  if (wave < nb) {
+    const int b = b0 + wave;
+    const size_t base = (size_t)b * ap.splits * HEADS + h;
+    const u32x4 *po = reinterpret_cast<const u32x4 *>(ap.part_o + base * LORA) + lane;
+    const size_t stride = (size_t)HEADS * LORA / 8;
+    const int nsp = ap.splits;
+    u32x4 v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = po[(size_t)min(j, nsp - 1) * stride];
+    float mloc = -INFINITY;
+    bool badl = false;
+    for (int s = lane; s < nsp; s += 64) {
+      mloc = fmaxf(mloc, ap.part_ml[(base + (size_t)s * HEADS) * 2]);
+      badl = badl || ap.part_ml[(base + (size_t)s * HEADS) * 2 + 1] < 0.f;
+    }
+    const float M = wave_max(mloc);
+    const bool flagged = __builtin_amdgcn_ballot_w64(badl) != 0;
+    if (lane == 0) s_flag[wave] = flagged;
+    if (!flagged) {
+      // weights, zero past the last split up to a multiple of 16
+      float lloc = 0.f;
+      const int nsp16 = (nsp + 15) & ~15;
+      for (int s = lane; s < nsp16; s += 64) {
+        float w = 0.f;
+        if (s < nsp) {
+          const float ms = ap.part_ml[(base + (size_t)s * HEADS) * 2];
+          w = ms == -INFINITY ? 0.f : exp2f(ms - M);
+          lloc += w * ap.part_ml[(base + (size_t)s * HEADS) * 2 + 1];
+        }
+        wsp[wave][s] = w;
       }
+      const float L = wave_sum(lloc);
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < nsp; s += 16) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float w = wsp[wave][s + j];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            acc[2 * e] += w * lo_bf(v[j][e]);
+            acc[2 * e + 1] += w * hi_bf(v[j][e]);
+          }
+        }
+        if (s + 16 < nsp) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) v[j] = po[(size_t)min(s + 16 + j, nsp - 1) * stride];
+        }
+      }
+      const float inv = 1.f / L;
+      const float sc = bsc[(8 * lane) / 128];
+      const u32x4 gm = *reinterpret_cast<const u32x4 *>(gamma + 8 * lane);
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = pack_bf16(acc[2 * e] * inv * lo_bf(gm[e]) * sc, acc[2 * e + 1] * inv * hi_bf(gm[e]) * sc);
+      *reinterpret_cast<u32x4 *>(&latb[wave][8 * lane]) = o;
     }
-    for (; s < ap.splits; ++s) {
-      const uint32_t v = po[s * stride];
-      a0 += wsp[s] * lo_bf(v);
-      a1 += wsp[s] * hi_bf(v);
-    }
-  } else {
-    // rare path: online merge with exact recomputation of flagged splits
-    M = -INFINITY;
+  } else if (wave < SQ && lane == 0) {
+    s_flag[wave] = 0;
+  }
+  __syncthreads();
+
+  // ---- rare path: sequences with a flagged split, merged by the whole
+  // workgroup (thread tid: latent columns 2 tid, 2 tid + 1)
+  for (int bb = 0; bb < nb; ++bb) {
+    if (!s_flag[bb]) continue;
+    const int b = b0 + bb;
+    const size_t base = (size_t)b * ap.splits * HEADS + h;
+    float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
     for (int s = 0; s < ap.splits; ++s) {
       const size_t row = base + (size_t)s * HEADS;
       float m1 = ap.part_ml[row * 2], l1 = ap.part_ml[row * 2 + 1], o0, o1;
@@ -664,30 +720,37 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
       L = L * fo + l1 * fn;
       M = Mn;
     }
+    const float inv = 1.f / L;
+    const float sc = bsc[(2 * tid) / 128];
+    const uint32_t gm = reinterpret_cast<const uint32_t *>(gamma)[tid];
+    reinterpret_cast<uint32_t *>(&latb[bb][0])[tid] = pack_bf16(a0 * inv * lo_bf(gm) * sc, a1 * inv * hi_bf(gm) * sc);
+    __syncthreads();
   }
-  const float inv = 1.f / L;
-  lat[2 * tid] = a0 * inv * bf2f(gamma[2 * tid]);
-  lat[2 * tid + 1] = a1 * inv * bf2f(gamma[2 * tid + 1]);
-  __syncthreads();
-  // out[v] = sum_c W_UV[h][v][c] * scale * lat[c]; wave handles 32 rows, lane 8 columns
-  float lv[8];
+
+  // ---- out = W_UV[h] . lat: wave w, rows 32w .. 32w+31 (two 16-row tiles), 16 K steps of 32
+  f32x4 c[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  const bool bvalid = li < nb;
+  const uint16_t *lr = &latb[bvalid ? li : 0][8 * lg];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) lv[j] = lat[lane * 8 + j];
-  const float sc = skvb[(size_t)(2 * h + 1) * (LORA / 128) + (lane * 8) / 128];
-  const uint8_t *wrow = wkvb + ((size_t)h * (NOPE + VD) + NOPE) * LORA + lane * 8;
-  u32x2 wv[32];  // all 32 rows in flight at once
+  for (int ks = 0; ks < LORA / 32; ++ks) {
+    const u32x4 bl = bvalid ? *reinterpret_cast<const u32x4 *>(lr + ks * 32) : u32x4{0, 0, 0, 0};
 #pragma unroll
-  for (int j = 0; j < 32; ++j) wv[j] = ldg8(wrow + (size_t)(wave * 32 + j) * LORA);
+    for (int vt = 0; vt < 2; ++vt) {
+      typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+      const bf16x2_t c0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[vt][ks].x, 1.f, false);
+      const bf16x2_t c1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[vt][ks].x, 1.f, true);
+      const bf16x2_t c2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[vt][ks].y, 1.f, false);
+      const bf16x2_t c3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[vt][ks].y, 1.f, true);
+      const bf16x8 a = {c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
+      c[vt] = mfma16(a, as_bf16x8(bl), c[vt]);
+    }
+  }
+  // C: lane holds sequence b0 + li, rows v = 16 vt + 4 lg .. +3 of the wave's 32
+  if (bvalid) {
+    uint16_t *dst = attn + (size_t)(b0 + li) * HEADS * VD + h * VD + 32 * wave + 4 * lg;
 #pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    const int v = wave * 32 + j;
-    const u32x2 raw = wv[j];
-    const f32x2 w01 = fp8x2_to_f32<false>(raw.x), w23 = fp8x2_to_f32<true>(raw.x);
-    const f32x2 w45 = fp8x2_to_f32<false>(raw.y), w67 = fp8x2_to_f32<true>(raw.y);
-    float a = w01.x * lv[0] + w01.y * lv[1] + w23.x * lv[2] + w23.y * lv[3] + w45.x * lv[4] +
-              w45.y * lv[5] + w67.x * lv[6] + w67.y * lv[7];
-    a = wave_sum(a * sc);
-    if (lane == 0) attn[(size_t)b * HEADS * VD + h * VD + v] = f2bf(a);
+    for (int vt = 0; vt < 2; ++vt)
+      *reinterpret_cast<u32x2 *>(dst + 16 * vt) = u32x2{pack_bf16(c[vt].x, c[vt].y), pack_bf16(c[vt].z, c[vt].w)};
   }
 }
 
@@ -840,8 +903,9 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   // 6. merge splits, W_UV
   mark(ev, 5, st);
   uint16_t *attn = reinterpret_cast<uint16_t *>(ws + L.attn);
-  combine_uv_kernel<<<dim3(HEADS, B), 256, 0, st>>>(ap, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b,
-                                                     reinterpret_cast<const uint16_t *>(a->gamma_kv), attn);
+  combine_uv_kernel<<<dim3(HEADS, (B + 3) / 4), 256, 0, st>>>(ap, reinterpret_cast<const uint8_t *>(a->w_kv_b),
+                                                              a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv),
+                                                              B, attn);
   if ((rc = check_launch("mla combine"))) return rc;
 
   // 7. o_proj (+ residual in layer mode)
