@@ -244,19 +244,19 @@ def main():
         extras["decode_ctx4096_b1_us_per_layer"] = round(us4, 2)
         extras["decode_ctx4096_b1_hbm_gbs"] = round(decode_layer_bytes(1, 4096) / (us4 * 1e-6) / 1e9, 1)
         del c4
-        # prefill 4096 tokens, one layer (rotating over 4 layers' weights)
+        # prefill 4096 tokens, one layer (rotating over up to 4 layers' weights)
         S = 4096
         hp = synth.randn((1, S, CFG.hidden_size), synth.seed_of("bench", "prefill"), 1.0, dev).to(torch.bfloat16)
         cp = (torch.zeros(1, S, 512, dtype=torch.bfloat16, device=dev), torch.zeros(1, S, 64, dtype=torch.bfloat16, device=dev))
         ropep = ops.precompute_rope_freqs(CFG, S, dev)
         for i in range(2):
-            ops.mla_attention(hp, stack[i].attn_weights, cp, 0, ropep, CFG)
+            ops.mla_attention(hp, stack[i % len(stack)].attn_weights, cp, 0, ropep, CFG)
         torch.cuda.synchronize()
         reps = 8
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         for i in range(reps):
-            ops.mla_attention(hp, stack[i % 4].attn_weights, cp, 0, ropep, CFG)
+            ops.mla_attention(hp, stack[i % min(4, len(stack))].attn_weights, cp, 0, ropep, CFG)
         e.record()
         torch.cuda.synchronize()
         pms = s.elapsed_time(e) / reps
