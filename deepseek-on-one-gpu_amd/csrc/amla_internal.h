@@ -46,6 +46,8 @@ struct GemvParams {
   const float *rope_table;
   int head_dim, nope;   // QROPE
   float *part;          // fp32 partial sums of the K parts (GemvPlan::part_bytes), else unused
+  const uint16_t *xgamma;  // skinny GEMM only: RMSNorm x (gamma, eps) while staging it, else null
+  float xeps;
 };
 
 struct GemvPlan {

@@ -216,15 +216,52 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
     asm volatile("" ::: "memory");
   };
 
-  // x[:, part] -> LDS (only rows < M; the fragments of rows >= M are zeros)
-  for (int idx = threadIdx.x; idx < p.M * nbp * 16; idx += 256) {
-    const int m = idx / (nbp * 16), c = idx % (nbp * 16);
-    *reinterpret_cast<u32x4 *>(xs + m * XROW + c * 16) =
-        ldg16(p.x + (size_t)m * p.ldx + (size_t)kb_begin * 128 + c * 8);
-  }
+  // the first weight tiles are in flight while x is staged
   if (tile_begin < tile_end) {
 #pragma unroll
     for (int b = 0; b < GEMV_NBUF - 1; ++b) dma_tile(tile_begin + b, b);
+  }
+  // fused RMSNorm of x (xgamma set): r_m = rsqrt(mean(x_m^2) + eps) over the
+  // whole row, one wave per row; the staged values are then rounded as
+  // rms_norm rounds them: bf16(bf16(x * r) * gamma) (inference/ops.py:10-12)
+  float *const rn = reinterpret_cast<float *>(done + rg * MT * 64);
+  if (p.xgamma) {
+    for (int m = wave; m < p.M; m += 4) {
+      const uint16_t *xr = p.x + (size_t)m * p.ldx;
+      float ss = 0.f;
+      const int nc = p.K >> 3;  // 16-byte chunks of the row
+      for (int c0 = 0; c0 < nc; c0 += 8 * 64) {
+        u32x4 v[8];  // eight independent loads in flight
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int c = c0 + j * 64 + lane;
+          v[j] = c < nc ? ldg16(xr + c * 8) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            ss = __builtin_fmaf(lo_bf(v[j][e]), lo_bf(v[j][e]), ss);
+            ss = __builtin_fmaf(hi_bf(v[j][e]), hi_bf(v[j][e]), ss);
+          }
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) rn[m] = rsqrtf(ss / (float)p.K + p.xeps);
+    }
+    lds_barrier();
+  }
+  // x[:, part] -> LDS (only rows < M; the fragments of rows >= M are zeros)
+  for (int idx = threadIdx.x; idx < p.M * nbp * 16; idx += 256) {
+    const int m = idx / (nbp * 16), c = idx % (nbp * 16);
+    u32x4 v = ldg16(p.x + (size_t)m * p.ldx + (size_t)kb_begin * 128 + c * 8);
+    if (p.xgamma) {
+      const float r = rn[m];
+      const u32x4 g = ldg16(p.xgamma + (size_t)kb_begin * 128 + c * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = pack_bf16(round_bf16(lo_bf(v[e]) * r) * lo_bf(g[e]), round_bf16(hi_bf(v[e]) * r) * hi_bf(g[e]));
+    }
+    *reinterpret_cast<u32x4 *>(xs + m * XROW + c * 16) = v;
   }
 
   for (int tile = tile_begin, it = 0; tile < tile_end; ++tile, ++it) {
@@ -317,7 +354,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
 
 size_t gemv_lds_bytes(int M, int MT, int kpb, int rg) {
   return (size_t)GEMV_NBUF * 16 * gemv_kpb4(kpb) * 128 + (size_t)M * gemv_xrow(kpb) + 2 * 4 * MT * 64 * 16 +
-         (size_t)rg * MT * 64 * 16;
+         (size_t)rg * MT * 64 * 16 + (size_t)M * 4;
 }
 
 // Sums the K parts of gemv_kernel in part order and applies the epilogue.
