@@ -358,6 +358,28 @@ AMLA_DEV void flash_dma(const FlashParams &p, int h, int t0, int Tlim, uint8_t *
   }
 }
 
+// Copy PIECE (0 .. F_DMA-1) of a tile wholly inside the keys in use: k_nope
+// copies, then value copies, then rope-key copies (the order of flash_dma).
+AMLA_DEV void flash_dma_piece(const FlashParams &p, int h, int t0, uint8_t *stage, int wave, const FlashLane &fl,
+                              int piece) {
+  constexpr int NJ = F_RPW / 4;
+  const char *kvw = reinterpret_cast<const char *>(p.kvb) + h * ((P_NOPE + P_V) * 2) + (size_t)(t0 + F_RPW * wave) * P_KVROW;
+  if (piece < NJ) {
+    const int j = piece;
+    __builtin_amdgcn_global_load_lds(kvw + (size_t)(4 * j) * P_KVROW + fl.nope[j & 1],
+                                     LDS_PTR(stage + F_NOPE + (F_RPW * wave + 4 * j) * 256), 16, 0, 0);
+  } else if (piece < 2 * NJ) {
+    const int j = piece - NJ;
+    __builtin_amdgcn_global_load_lds(kvw + (size_t)(4 * j) * P_KVROW + fl.val,
+                                     LDS_PTR(stage + F_VAL + (F_RPW * wave + 4 * j) * 256), 16, 0, 0);
+  } else {
+    const int j = piece - 2 * NJ;
+    const char *krw = reinterpret_cast<const char *>(p.kpe) + (size_t)(t0 + F_RPW * wave) * (P_ROPE * 2);
+    __builtin_amdgcn_global_load_lds(krw + 8 * j * (P_ROPE * 2) + fl.rope,
+                                     LDS_PTR(stage + F_RPE + (F_RPW * wave + 8 * j) * 128), 16, 0, 0);
+  }
+}
+
 // Grid H x (query blocks of 256), 256 threads, 120 KB of LDS: one workgroup
 // per CU.  Wave w handles queries qb*256 + 64w .. +63 of head h, in two
 // groups of 32.  Per 64-key tile:
@@ -494,7 +516,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
   }
   // S^T of one 32-key group (half KG of the stage in kb/rb) into SC; with
   // DOEXP, the exp of SCE rides along (8 slices over the first 8 K steps)
-#define FL_S(SC, KG, SCE, DOEXP)                                                                   \
+#define FL_S(SC, KG, SCE, DOEXP, DMAT, DMAST)                                                       \
   {                                                                                                \
     u32x4 ka[FD];                                                                                  \
     _Pragma("unroll") for (int d = 0; d < FD; ++d) FL_RDK(ka[d], d, KG);                          \
@@ -516,6 +538,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
                        : "v"(ka[c]), "a"(qf[qg][ks]));                                             \
       }                                                                                            \
       if (ks + FD < 12) FL_RDK(ka[c], ks + FD, KG);                                               \
+      if ((DMAT) >= 0 && ks < F_DMA) flash_dma_piece(p, h, (DMAT) * F_KT, DMAST, wave, fl, ks);     \
       __builtin_amdgcn_sched_barrier(0);                                                           \
       if ((DOEXP) && ks < 4 * F_NQG) FL_EXP(SCE, ks >> 2, ks & 3);                                 \
       __builtin_amdgcn_sched_barrier(0);                                                           \
@@ -608,7 +631,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   FL_KBASE(0);
-  FL_S(scA, 0, scB, 0);
+  FL_S(scA, 0, scB, 0, -1, fsm);
 #pragma unroll
   for (int qg = 0; qg < F_NQG; ++qg) mx[qg] = -INFINITY;
   {
@@ -622,7 +645,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
   for (int j = 0; j < ntiles; ++j) {
     const int g = 2 * j;
     // ---- group g (even): S_{g+1} (same tile, half 1) || exp of scA; PV_g || max of scB
-    FL_S(scB, 1, scA, 1);
+    FL_S(scB, 1, scA, 1, -1, fsm);
     FL_VBASE(stg);
     {
       const bool diag = 32 * (g + 1) + 31 > pos0 + s_wave;
@@ -633,17 +656,20 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
     // After the last tile S_{g+2} re-reads the current stage and is discarded.
     const bool more = j + 1 < ntiles;
     int stn = stg;
+    int dmat = -1;  // tile whose copies go out one per score step below (wholly inside the keys in use)
     if (more) {
       // tile j+1 landed in every wave; tile j-1's stage is free for tile j+2
       wait_vmcnt<0>();
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       stn = stg == F_NST - 1 ? 0 : stg + 1;
-      if (j + 2 < ntiles)
-        flash_dma(p, h, (j + 2) * F_KT, Tlim, fsm + (stn == F_NST - 1 ? 0 : stn + 1) * F_STAGE, wave, lane, fl);
+      if (j + 2 < ntiles) {
+        if ((j + 3) * F_KT <= Tlim) dmat = j + 2;
+        else flash_dma(p, h, (j + 2) * F_KT, Tlim, fsm + (stn == F_NST - 1 ? 0 : stn + 1) * F_STAGE, wave, lane, fl);
+      }
     }
     FL_KBASE(stn);
-    FL_S(scA, 0, scB, 1);
+    FL_S(scA, 0, scB, 1, dmat, fsm + (stn == F_NST - 1 ? 0 : stn + 1) * F_STAGE);
     {
       const bool diag = 32 * (g + 2) + 31 > pos0 + s_wave;
       FL_PV(1, scA, g + 2, 1, diag);
