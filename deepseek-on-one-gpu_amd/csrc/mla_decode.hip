@@ -19,7 +19,8 @@
 //                the caches
 //   gemv  QROPE: q = q_a_layernorm(q_a) W_qb^T (norm fused into the staging
 //                of q_a); RoPE on the q_pe rows at pos[b]
-//   absorb     : qt = gamma_kv * W_UK^T q_nope  -> qbuf (B, H, 576) with q_pe
+//   absorb     : qt = gamma_kv * W_UK^T q_nope  -> qbuf (B, H, 576) with q_pe,
+//                stored in attn_kernel's fragment order
 //   attn       : split over context, online softmax, bf16 partial O, (m, l)
 //   combine_uv : merge splits, gamma_kv, W_UV -> (B, H*128) bf16
 //   gemv  PLAIN/RESID : wo
@@ -37,6 +38,16 @@ constexpr int HEADS = 128;
 constexpr int NOPE = 128;
 constexpr int VD = 128;
 constexpr int TT = 32;               // cache rows per tile
+
+// The absorbed query buffer holds, per sequence, the (H, 576) query matrix in
+// the order attn_kernel's B fragments are loaded: for wave w (heads 32w ..
+// 32w+31), head block nt (16 heads), K step ks (32 columns) and lane l, the
+// 8 columns 32ks + 8(l/16) .. +7 of head 32w + 16nt + l%16 are 16 contiguous
+// bytes, and one wave-wide 16-byte load reads 1 KB contiguously.
+AMLA_DEV size_t qfrag_index(int b, int h, int c) {
+  const int lane = (h & 15) + 16 * ((c & 31) >> 3);
+  return ((((size_t)b * (HEADS / 16) + (h >> 4)) * (QKD / 32) + (c >> 5)) * 64 + lane) * 8 + (c & 7);
+}
 
 // ---------------------------------------------------------------- absorb
 
@@ -101,7 +112,7 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
       const u32x2 gm = *reinterpret_cast<const u32x2 *>(gamma + c);
       u32x2 o = {pack_bf16(v.x * sc * lo_bf(gm.x), v.y * sc * hi_bf(gm.x)),
                  pack_bf16(v.z * sc * lo_bf(gm.y), v.w * sc * hi_bf(gm.y))};
-      *reinterpret_cast<u32x2 *>(qbuf + ((size_t)(b0 + bb) * HEADS + h) * QKD + c) = o;
+      *reinterpret_cast<u32x2 *>(qbuf + qfrag_index(b0 + bb, h, c)) = o;  // 4 columns in one 8-column group
     }
   }
   // rope half of the query: copied next to the absorbed latent query
@@ -110,7 +121,7 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
       const int bb = e / (ROPE / 2), j = (e % (ROPE / 2)) * 2;
       const uint32_t v =
           *reinterpret_cast<const uint32_t *>(q + ((size_t)(b0 + bb) * HEADS + h) * (NOPE + ROPE) + NOPE + j);
-      *reinterpret_cast<uint32_t *>(qbuf + ((size_t)(b0 + bb) * HEADS + h) * QKD + LORA + j) = v;
+      *reinterpret_cast<uint32_t *>(qbuf + qfrag_index(b0 + bb, h, LORA + j)) = v;
     }
   }
 }
@@ -118,7 +129,7 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
 // ---------------------------------------------------------------- attention
 
 struct AttnParams {
-  const uint16_t *qbuf;  // (B, H, 576) bf16: absorbed latent query | rotated rope query
+  const uint16_t *qbuf;  // B x (H, 576) bf16 in fragment order (qfrag_index): absorbed latent query | rotated rope query
   const uint16_t *ckv;   // cache (B_alloc, max_seq, 512)
   const uint16_t *kpe;   // cache (B_alloc, max_seq, 64)
   int64_t ckv_bstride, kpe_bstride;  // elements per sequence
@@ -149,42 +160,50 @@ constexpr int TAB_BYTES = TT * ROPE * 4;
 constexpr int P_OFF = TAB_OFF + 2 * TAB_BYTES;
 constexpr int PROW = TT * 2 + 16;  // bf16 probabilities of one head, 80 B rows (conflict-free 16 B reads)
 constexpr int ATTN_LDS_BYTES = P_OFF + HEADS * PROW;
+constexpr int OROW = LORA * 2 + 32;  // LDS row of one head's partial O at the end (bf16, padded)
+static_assert(HEADS * OROW <= ATTN_LDS_BYTES, "partial O staging must fit the attention LDS");
 constexpr int TILE_DMA = 11;  // copies per wave per tile: 8 latent rows, 1 block of rope keys, 2 table blocks
 constexpr float REF_HEADROOM = 64.f;      // p = 2^(s - m_ref) <= 2^64: no overflow anywhere
 
-// Wave w copies rows 8w .. 8w+7 of the tile straight into LDS (no VGPRs):
+// Wave w copies rows 8w .. 8w+7 of a tile straight into LDS (no VGPRs):
 // every global_load_lds_dwordx4 writes 64 lanes x 16 B contiguously at its
 // LDS base.  Row indices are wave-uniform (scalar bases, one lane offset).
 // Rows past the context re-read row T-1 (in bounds; their scores are masked).
-AMLA_DEV void dma_rows(const AttnParams &p, int b, int tile, int T, uint8_t *stage, int wave, int lane) {
+// Piece 0..7: latent row 8w + piece; 8: the 8 rows' raw rope keys; 9, 10: the
+// (cos, sin) table rows of the 8 rows (2 x 1 KB), into the table block of the
+// tile's parity.  The tile loop issues one piece per score step: a burst of
+// LDS copies stalls the issuing wave for tens of cycles per copy.
+AMLA_DEV void dma_piece(const AttnParams &p, int b, int tile, int T, uint8_t *smem, uint8_t *stage, int wave, int lane,
+                        int piece) {
   const int t0 = tile * TT + wave * 8;
-  const char *cb = reinterpret_cast<const char *>(p.ckv + (size_t)b * p.ckv_bstride);
-  int voff;
-  asm volatile("v_lshlrev_b32 %0, 4, %1" : "=v"(voff) : "v"(lane));  // lane * 16, kept out of loop-invariant hoisting
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const int t = min(t0 + r, T - 1);
-    __builtin_amdgcn_global_load_lds(cb + (size_t)t * (LORA * 2) + voff, LDS_PTR(stage + (wave * 8 + r) * (KROW * 2)),
-                                     16, 0, 0);
+  const int t0c = min(t0, T - 1);
+  // lane-derived offsets are unsigned (scalar base + 32-bit lane offset
+  // addressing) and recomputed per copy, not held across the loop
+  uint32_t ln;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
+  if (piece < 8) {
+    const char *cb = reinterpret_cast<const char *>(p.ckv + (size_t)b * p.ckv_bstride);
+    const int t = min(t0 + piece, T - 1);
+    __builtin_amdgcn_global_load_lds(cb + (size_t)t * (LORA * 2) + ln * 16u,
+                                     LDS_PTR(stage + (wave * 8 + piece) * (KROW * 2)), 16, 0, 0);
+  } else if (piece == 8) {
+    const char *kb = reinterpret_cast<const char *>(p.kpe + (size_t)b * p.kpe_bstride) + (size_t)t0c * (ROPE * 2);
+    const uint32_t row = static_cast<uint32_t>(min(t0 + static_cast<int>(ln >> 3), T - 1) - t0c);
+    __builtin_amdgcn_global_load_lds(kb + row * (ROPE * 2) + (ln & 7u) * 16u, LDS_PTR(stage + K_BYTES + wave * 1024), 16,
+                                     0, 0);
+  } else {
+    const char *tb = reinterpret_cast<const char *>(p.rope_table) + (size_t)t0c * (ROPE * 4);
+    const uint32_t e = static_cast<uint32_t>(piece - 9) * 64u + ln;
+    const uint32_t row = static_cast<uint32_t>(min(t0 + static_cast<int>(e >> 4), T - 1) - t0c);
+    __builtin_amdgcn_global_load_lds(
+        tb + row * (ROPE * 4) + (e & 15u) * 16u,
+        LDS_PTR(smem + TAB_OFF + (tile & 1) * TAB_BYTES + wave * 2048 + (piece - 9) * 1024), 16, 0, 0);
   }
-  const int last = T - 1 - t0;
-  const char *kb = reinterpret_cast<const char *>(p.kpe + (size_t)b * p.kpe_bstride) + (size_t)t0 * (ROPE * 2);
-  const int off = min(lane >> 3, last) * (ROPE * 2) + (lane & 7) * 16;
-  __builtin_amdgcn_global_load_lds(kb + off, LDS_PTR(stage + K_BYTES + wave * 1024), 16, 0, 0);
 }
 
-// (cos, sin) of the 8 rows wave w rotates: 8 x 256 B in two copies.
-AMLA_DEV void dma_table(const AttnParams &p, int tile, int T, uint8_t *smem, int wave, int lane) {
-  const int t0 = tile * TT + wave * 8;
-  const int last = T - 1 - t0;
-  const char *tb = reinterpret_cast<const char *>(p.rope_table) + (size_t)t0 * (ROPE * 4);
+AMLA_DEV void dma_tile(const AttnParams &p, int b, int tile, int T, uint8_t *smem, uint8_t *stage, int wave, int lane) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int e = j * 64 + lane;
-    const int off = min(e >> 4, last) * (ROPE * 4) + (e & 15) * 16;
-    __builtin_amdgcn_global_load_lds(tb + off, LDS_PTR(smem + TAB_OFF + (tile & 1) * TAB_BYTES + wave * 2048 + j * 1024),
-                                     16, 0, 0);
-  }
+  for (int piece = 0; piece < TILE_DMA; ++piece) dma_piece(p, b, tile, T, smem, stage, wave, lane, piece);
 }
 
 AMLA_DEV uint32_t rot_pair(uint32_t x, float c, float s) {
@@ -210,27 +229,35 @@ AMLA_DEV float dpp_f32(float v) {
 //     goes to the stage's rt array; the latent row stays raw;
 //   the rope key is rotated in fp32 and rounded to bf16 (inference/ops.py:93-97).
 AMLA_DEV void prepare_own_rows(uint8_t *stage, const uint8_t *tab, int wave, int lane, float eps) {
-  const int row = wave * 8 + (lane >> 3), q = lane & 7;
+  int ln;  // lane-derived addresses are recomputed here, not held across the tile loop
+  asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
+  const int row = wave * 8 + (ln >> 3), q = ln & 7;
   uint8_t *rp = stage + row * (KROW * 2);
-  u32x4 v[8];
+  // two batches of four 16-byte reads keep the register footprint small
+  float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const u32x4 *>(rp + (q + 8 * i) * 16);
+  for (int h = 0; h < 2; ++h) {
+    u32x4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const u32x4 *>(rp + (q + 8 * (4 * h + i)) * 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ss = dot2_bf16(v[i].x, ss);
+      ss = dot2_bf16(v[i].y, ss);
+      ss = dot2_bf16(v[i].z, ss);
+      ss = dot2_bf16(v[i].w, ss);
+    }
+    asm volatile("" ::: "memory");
+  }
   const u32x4 raw = *reinterpret_cast<const u32x4 *>(stage + K_BYTES + row * (ROPE * 2) + q * 16);
   const f32x4 c0 = *reinterpret_cast<const f32x4 *>(tab + row * (ROPE * 4) + q * 32);
   const f32x4 c1 = *reinterpret_cast<const f32x4 *>(tab + row * (ROPE * 4) + q * 32 + 16);
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    ss = dot2_bf16(v[i].x, ss);
-    ss = dot2_bf16(v[i].y, ss);
-    ss = dot2_bf16(v[i].z, ss);
-    ss = dot2_bf16(v[i].w, ss);
-  }
   // sum over the 8 lanes of the row: quad xor 1, xor 2, then the other quad
   ss += dpp_f32<0xB1>(ss);   // quad_perm [1,0,3,2]
   ss += dpp_f32<0x4E>(ss);   // quad_perm [2,3,0,1]
   ss += dpp_f32<0x141>(ss);  // row_half_mirror
-  if (q == 0) *reinterpret_cast<float *>(stage + RT_OFF + row * 4) = rsqrtf(ss * (1.f / LORA) + eps);
+  // v_rsq_f32 directly: the argument is at least eps, far from the denormal range
+  if (q == 0) *reinterpret_cast<float *>(stage + RT_OFF + row * 4) = __builtin_amdgcn_rsqf(ss * (1.f / LORA) + eps);
   u32x4 k;
   k.x = rot_pair(raw.x, c0.x, c0.y);
   k.y = rot_pair(raw.y, c0.z, c0.w);
@@ -297,9 +324,9 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   bf16x8 qf[2][QKD / 32];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    const uint16_t *qr = p.qbuf + ((size_t)b * HEADS + head0 + nt * 16 + li) * QKD + 8 * lg;
+    const uint16_t *qr = p.qbuf + qfrag_index(b, head0 + nt * 16, 0) + lane * 8;
 #pragma unroll
-    for (int ks = 0; ks < QKD / 32; ++ks) qf[nt][ks] = as_bf16x8(ldg16(qr + ks * 32));
+    for (int ks = 0; ks < QKD / 32; ++ks) qf[nt][ks] = as_bf16x8(ldg16(qr + ks * 512));
   }
 
   f32x4 o[8][8];  // O^T: latent 128*wave + 16*mt + .., heads 16*nt + ..
@@ -311,11 +338,9 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   bool bad[2] = {false, false};
 
   if (tb < te) {
-    dma_table(p, tb, T, smem, wave, lane);
-    dma_rows(p, b, tb, T, smem, wave, lane);
+    dma_tile(p, b, tb, T, smem, smem, wave, lane);
     if (tb + 1 < te) {
-      dma_table(p, tb + 1, T, smem, wave, lane);
-      dma_rows(p, b, tb + 1, T, smem + STAGE_BYTES, wave, lane);
+      dma_tile(p, b, tb + 1, T, smem, smem + STAGE_BYTES, wave, lane);
       wait_vmcnt<TILE_DMA>();
     } else {
       wait_vmcnt<0>();
@@ -326,27 +351,24 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
     for (int tile = tb; tile < te; ++tile) {
       const int it = tile - tb;
       uint8_t *const cur = smem + (it % NST) * STAGE_BYTES;
-      // copies of the tile after next (the table block only ever holds this
-      // wave's rows: no barrier needed for it)
-      if (tile + 2 < te) {
-        dma_table(p, tile + 2, T, smem, wave, lane);
-        dma_rows(p, b, tile + 2, T, smem + ((it + 2) % NST) * STAGE_BYTES, wave, lane);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+      // copies of the tile after next, one per score step below (its stage was
+      // last read in the previous tile; the table block only ever holds this
+      // wave's rows)
+      const bool dma_next = tile + 2 < te;
+      uint8_t *const nst = smem + ((it + 2) % NST) * STAGE_BYTES;
       const uint16_t *K = reinterpret_cast<const uint16_t *>(cur);
 
-      // ---- scores: 18 K steps, A fragments SD steps ahead
+      // ---- scores: 18 K steps, A fragments SD steps ahead.  The MFMAs are
+      // inline asm with VGPR accumulators (the O accumulators own the AGPRs);
+      // the compiler does not track their hazards, so the VALU touches of sc
+      // below are preceded by explicit wait states.
       constexpr int NSTEP = QKD / 32;
-      constexpr int SD = 3;
+      constexpr int SD = 4;
       const uint32_t kaddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
           (__attribute__((address_space(3))) const uint16_t *)(K + li * KROW + 8 * lg)));
 #define AMLA_RDA(dst, S, MT) \
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(kaddr), "i"(((MT) * 16 * KROW + (S) * 32) * 2))
       f32x4 sc[2][2];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) sc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
       // r_t of the lane's C-layout rows 4*lg + r (mt 0) and 16 + 4*lg + r (mt 1)
       f32x4 rc[2];
       rc[0] = *reinterpret_cast<const f32x4 *>(cur + RT_OFF + (4 * lg) * 4);
@@ -361,27 +383,37 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       for (int ks = 0; ks < NSTEP; ++ks) {
         const int c = ks % SD;
         const int later = (NSTEP - 1 - ks) < (SD - 1) ? (NSTEP - 1 - ks) : (SD - 1);  // steps issued after ks
-        if (later == 2) asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
+        if (later == 3) asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
+        else if (later == 2) asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
         else if (later == 1) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
         else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
         if (ks == LORA / 32) {
-          // latent part complete: apply r_t before the rope K steps
+          // latent part complete: apply r_t before the rope K steps (MFMA
+          // write -> VALU read, then VALU write -> MFMA read wait states)
+          asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory");
 #pragma unroll
           for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) sc[mt][nt] *= rc[mt];
+          asm volatile("s_nop 4" : "+v"(sc[0][0]), "+v"(sc[0][1]), "+v"(sc[1][0]), "+v"(sc[1][1])::"memory");
         }
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          const bf16x8 a = as_bf16x8(ab[c][mt]);
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) sc[mt][nt] = mfma16(a, qf[nt][ks], sc[mt][nt]);
-        }
+          for (int nt = 0; nt < 2; ++nt) {
+            if (ks == 0)
+              asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=v"(sc[mt][nt]) : "v"(ab[c][mt]), "v"(qf[nt][ks]));
+            else
+              asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(sc[mt][nt]) : "v"(ab[c][mt]), "v"(qf[nt][ks]));
+          }
         if (ks + SD < NSTEP) {
           AMLA_RDA(ab[c][0], ks + SD, 0);
           AMLA_RDA(ab[c][1], ks + SD, 1);
         }
+        if (ks < TILE_DMA && dma_next) dma_piece(p, b, tile + 2, T, smem, nst, wave, lane, ks);
       }
+      // the softmax reads sc: MFMA write -> VALU read wait states
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sc[0][0]), "+v"(sc[0][1]), "+v"(sc[1][0]), "+v"(sc[1][1])::"memory");
 #undef AMLA_RDA
       __builtin_amdgcn_sched_barrier(0);
 
@@ -470,7 +502,8 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
         }
         const bf16x8 a = as_bf16x8(u32x4{t0[c].x, t0[c].y, t1[c].x, t1[c].y});
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) o[mt][nt] = mfma16(a, as_bf16x8(pb[nt]), o[mt][nt]);
+        for (int nt = 0; nt < 8; ++nt)  // accumulators pinned to AGPRs (only these MFMAs touch them in the loop)
+          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(o[mt][nt]) : "v"(a), "v"(pb[nt]));
         if (mt + PV_DEPTH < 8) AMLA_TR(t0[c], t1[c], mt + PV_DEPTH);
       }
 #undef AMLA_TR
@@ -491,6 +524,9 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
     }
   }
 
+  // the accumulators' last MFMA writes are read by VALU code below: cover the
+  // MFMA write-to-read wait states the compiler does not see for inline asm
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   // ---- partial results of this split: (m, l) of the wave's heads, O of its
   // latent columns for every head
 #pragma unroll
@@ -505,14 +541,21 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       p.part_ml[row * 2 + 1] = bad[nt] ? -1.f : l;
     }
   }
+  // O goes out through LDS (the loop's last barrier follows its last LDS read
+  // and every copy has landed): head rows of 512 bf16, then 1 KB contiguous
+  // per wave-wide store
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) {
-    const size_t row = ((size_t)b * p.splits + split) * HEADS + nt * 16 + li;
-    uint16_t *dst = p.part_o + row * LORA + wave * 128 + 4 * lg;
+  for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt)
-      *reinterpret_cast<u32x2 *>(dst + mt * 16) =
+      *reinterpret_cast<u32x2 *>(smem + (nt * 16 + li) * OROW + (wave * 128 + mt * 16 + 4 * lg) * 2) =
           u32x2{pack_bf16(o[mt][nt].x, o[mt][nt].y), pack_bf16(o[mt][nt].z, o[mt][nt].w)};
+  __syncthreads();
+  uint8_t *const dst = reinterpret_cast<uint8_t *>(p.part_o + ((size_t)b * p.splits + split) * HEADS * LORA);
+#pragma unroll 8
+  for (int i = 0; i < HEADS * LORA * 2 / (256 * 16); ++i) {
+    const int chunk = i * 256 + tid, head = chunk >> 6, c16 = chunk & 63;
+    *reinterpret_cast<u32x4 *>(dst + (size_t)chunk * 16) = *reinterpret_cast<const u32x4 *>(smem + head * OROW + c16 * 16);
   }
 }
 
@@ -539,7 +582,7 @@ AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, int split, floa
   const int t0 = split * p.tiles_per_split * TT;
   const int t1 = min(t0 + p.tiles_per_split * TT, T);
   __syncthreads();
-  for (int c = tid; c < QKD; c += 256) qs[c] = bf2f(p.qbuf[((size_t)b * HEADS + h) * QKD + c]);
+  for (int c = tid; c < QKD; c += 256) qs[c] = bf2f(p.qbuf[qfrag_index(b, h, c)]);
   __syncthreads();
   const uint16_t *cb = p.ckv + (size_t)b * p.ckv_bstride;
   const uint16_t *kb = p.kpe + (size_t)b * p.kpe_bstride;
@@ -563,7 +606,7 @@ AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, int split, floa
         const uint32_t rk = rot_pair(kv, cs, sn);
         dp += lo_bf(rk) * qs[LORA + 2 * i] + hi_bf(rk) * qs[LORA + 2 * i + 1];
       }
-      rt = rsqrtf(ss * (1.f / LORA) + p.eps);
+      rt = __builtin_amdgcn_rsqf(ss * (1.f / LORA) + p.eps);
       sv = p.scale_log2 * (rt * dl + dp);
     }
     const float mc = block_reduce(sv, red, true);
