@@ -46,8 +46,6 @@ struct GemvParams {
   const float *rope_table;
   int head_dim, nope;   // QROPE
   float *part;          // fp32 partial sums of the K parts (GemvPlan::part_bytes), else unused
-  const uint16_t *xgamma;  // skinny GEMM only: RMSNorm x (gamma, eps) while staging it, else null
-  float xeps;
 };
 
 struct GemvPlan {
@@ -63,7 +61,13 @@ GemvPlan plan_gemv(int M, int N, int K);
 size_t gemv_lds_bytes(int M, int MT, int kpb, int rg);
 // Launches the skinny GEMM for M <= 64 (N % 16 == 0, K % 128 == 0, 16-byte aligned rows);
 // p.part must hold plan.part_bytes when plan.kparts > 1.
-int launch_gemv(const GemvParams &p, int mode, const GemvPlan &plan, hipStream_t stream);
+// finish = false leaves the fp32 K-part sums in p.part (plan.kparts > 1) for
+// the caller's own finishing kernel.
+int launch_gemv(const GemvParams &p, int mode, const GemvPlan &plan, hipStream_t stream, bool finish = true);
+// QKVA finish with the q_a RMSNorm fused: sums the K parts, writes the kv_a
+// rows into the caches and rms_norm(q_a, gamma, eps) (both roundings of
+// inference/ops.py:12) into p.y; one workgroup per row.
+int launch_qkva_finish_norm(const GemvParams &p, int kparts, const uint16_t *gamma, float eps, hipStream_t stream);
 
 // Large-M fp8 GEMM with the same modes (M > 64).
 size_t gemm_ws_bytes(int M, int N, int K);

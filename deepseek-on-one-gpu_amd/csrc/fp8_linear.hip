@@ -161,16 +161,22 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
 constexpr int GEMV_MAX_PARTS = 32;  // K parts summed by gemv_finish
 constexpr int GEMV_MAX_RG = 16;     // 16-row tiles per workgroup
 constexpr int GEMV_KPB = 16;        // max 128-wide blocks per K part (2 KB of a row)
-constexpr int GEMV_NBUF = 3;        // weight tiles resident: current + two in flight
+// Weight tiles resident (current + NBUF-1 in flight).  With M <= 16 (MT 1)
+// the x fragments live in registers instead of LDS, which leaves room for one
+// more tile in flight.
+__host__ __device__ constexpr int gemv_nbuf(int MT) { return MT == 1 ? 4 : 3; }
 
-// LDS: [NBUF][16 rows][ceil4(kpb) * 128] weights | [M][kpb * 256 + 16] x |
+// LDS: [NBUF][16 rows][ceil4(kpb) * 128] weights | [M][kpb * 256 + 16] x (MT > 1) |
 //      [2][4 waves][MT][64] f32x4 partial tiles | [rg][MT][64] f32x4 results
 __host__ __device__ inline int gemv_kpb4(int kpb) { return (kpb + 3) & ~3; }
 __host__ __device__ inline int gemv_xrow(int kpb) { return kpb * 256 + 16; }
 
 template <int MT, int MODE>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kparts, int kpb) {
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  constexpr bool XREG = MT == 1;
+  constexpr int NBUF = gemv_nbuf(MT);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
   const int KB = p.K >> 7;
   const int ntiles = p.N >> 4;
@@ -185,8 +191,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
 
   extern __shared__ __align__(16) uint8_t gsm[];
   uint8_t *const wbuf = gsm;
-  uint8_t *const xs = gsm + GEMV_NBUF * TILE_BYTES;
-  f32x4 *const red = reinterpret_cast<f32x4 *>(xs + p.M * XROW);
+  uint8_t *const xs = gsm + NBUF * TILE_BYTES;
+  f32x4 *const red = reinterpret_cast<f32x4 *>(xs + (XREG ? 0 : p.M * XROW));
   f32x4 *const done = red + 2 * 4 * MT * 64;
 
   // weight copies of one tile: row pairs i = 2*wave, 2*wave+1, every segment
@@ -216,56 +222,37 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
     asm volatile("" ::: "memory");
   };
 
-  // the first weight tiles are in flight while x is staged
+  // the first weight tiles are in flight while x is read
   if (tile_begin < tile_end) {
 #pragma unroll
-    for (int b = 0; b < GEMV_NBUF - 1; ++b) dma_tile(tile_begin + b, b);
+    for (int b = 0; b < NBUF - 1; ++b) dma_tile(tile_begin + b, b);
   }
-  // fused RMSNorm of x (xgamma set): r_m = rsqrt(mean(x_m^2) + eps) over the
-  // whole row, one wave per row; the staged values are then rounded as
-  // rms_norm rounds them: bf16(bf16(x * r) * gamma) (inference/ops.py:10-12)
-  float *const rn = reinterpret_cast<float *>(done + rg * MT * 64);
-  if (p.xgamma) {
-    for (int m = wave; m < p.M; m += 4) {
-      const uint16_t *xr = p.x + (size_t)m * p.ldx;
-      float ss = 0.f;
-      const int nc = p.K >> 3;  // 16-byte chunks of the row
-      for (int c0 = 0; c0 < nc; c0 += 8 * 64) {
-        u32x4 v[8];  // eight independent loads in flight
+
+  // MT 1: this wave's x fragments (blocks wave + 4j of the part, row li; rows
+  // >= M are zeros), in the MFMA K order of the weight fragments below
+  constexpr int NJ = GEMV_KPB / 4;
+  u32x4 xr[XREG ? NJ : 1][4];
+  if constexpr (XREG) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int c = c0 + j * 64 + lane;
-          v[j] = c < nc ? ldg16(xr + c * 8) : u32x4{0, 0, 0, 0};
-        }
+    for (int j = 0; j < NJ; ++j) {
+      const int bl = wave + 4 * j;
+      const bool ok = bl < nbp && li < p.M;
+      const uint16_t *xp = p.x + (size_t)li * p.ldx + (size_t)(kb_begin + bl) * 128 + lg * 16;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            ss = __builtin_fmaf(lo_bf(v[j][e]), lo_bf(v[j][e]), ss);
-            ss = __builtin_fmaf(hi_bf(v[j][e]), hi_bf(v[j][e]), ss);
-          }
-      }
-      ss = wave_sum(ss);
-      if (lane == 0) rn[m] = rsqrtf(ss / (float)p.K + p.xeps);
+      for (int q = 0; q < 4; ++q) xr[j][q] = ok ? ldg16(xp + (q & 1) * 8 + (q >> 1) * 64) : u32x4{0, 0, 0, 0};
     }
-    lds_barrier();
   }
-  // x[:, part] -> LDS (only rows < M; the fragments of rows >= M are zeros)
-  for (int idx = threadIdx.x; idx < p.M * nbp * 16; idx += 256) {
-    const int m = idx / (nbp * 16), c = idx % (nbp * 16);
-    u32x4 v = ldg16(p.x + (size_t)m * p.ldx + (size_t)kb_begin * 128 + c * 8);
-    if (p.xgamma) {
-      const float r = rn[m];
-      const u32x4 g = ldg16(p.xgamma + (size_t)kb_begin * 128 + c * 8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        v[e] = pack_bf16(round_bf16(lo_bf(v[e]) * r) * lo_bf(g[e]), round_bf16(hi_bf(v[e]) * r) * hi_bf(g[e]));
+
+  if constexpr (!XREG) {
+    // x[:, part] -> LDS (only rows < M; the fragments of rows >= M are zeros)
+    for (int idx = tid; idx < p.M * nbp * 16; idx += 256) {
+      const int m = idx / (nbp * 16), c = idx % (nbp * 16);
+      *reinterpret_cast<u32x4 *>(xs + m * XROW + c * 16) = ldg16(p.x + (size_t)m * p.ldx + (size_t)kb_begin * 128 + c * 8);
     }
-    *reinterpret_cast<u32x4 *>(xs + m * XROW + c * 16) = v;
   }
 
   for (int tile = tile_begin, it = 0; tile < tile_end; ++tile, ++it) {
-    const int buf = it % GEMV_NBUF;
+    const int buf = it % NBUF;
     const int nt = tile * 16;
     // block scales of this wave's blocks through the scalar cache (constant
     // address space: the scales are never written here), so waiting for them
@@ -274,24 +261,31 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
     const __attribute__((address_space(4))) float *srow =
         (const __attribute__((address_space(4))) float *)((seg1 ? p.s1 : p.s0) +
                                                           (size_t)((seg1 ? nt - p.n_split : nt) >> 7) * KB + kb_begin);
-    float scw[GEMV_KPB / 4];
+    float scw[NJ];
 #pragma unroll
-    for (int j = 0; j < GEMV_KPB / 4; ++j) scw[j] = srow[min(wave + 4 * j, nbp - 1)];
-    // this tile's copies landed (the next tile's may stay in flight), then
-    // every wave's part of it is visible
-    if (nseg == 4) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else if (nseg == 3) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-    else if (nseg == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    for (int j = 0; j < NJ; ++j) scw[j] = srow[min(wave + 4 * j, nbp - 1)];
+    // this tile's copies landed (the later tiles' may stay in flight: 2*nseg
+    // copies per wave per tile), then every wave's part of it is visible
+    if constexpr (NBUF == 4) {
+      if (nseg == 4) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+      else if (nseg == 3) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+      else if (nseg == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    } else {
+      if (nseg == 4) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else if (nseg == 3) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+      else if (nseg == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    }
     lds_barrier();
-    dma_tile(tile + GEMV_NBUF - 1, (it + GEMV_NBUF - 1) % GEMV_NBUF);  // into the buffer read last trip
+    dma_tile(tile + NBUF - 1, (it + NBUF - 1) % NBUF);  // into the buffer read last trip
 
     const uint8_t *tb = wbuf + buf * TILE_BYTES;
     f32x4 acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < GEMV_KPB / 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int bl = wave + 4 * j;
       if (bl < nbp) {
         const int s = bl >> 2, bq = bl & 3;  // segment, block inside it
@@ -305,12 +299,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
         for (int t = 0; t < MT; ++t) {
           const int m = t * 16 + li;
           bf16x8 x0, x1, x2, x3;
-          if (m < p.M) {
-            const uint8_t *xr = xs + m * XROW + bl * 256 + lg * 32;
-            x0 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xr));
-            x1 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xr + 16));
-            x2 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xr + 128));
-            x3 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xr + 144));
+          if constexpr (XREG) {
+            x0 = as_bf16x8(xr[j][0]);
+            x1 = as_bf16x8(xr[j][1]);
+            x2 = as_bf16x8(xr[j][2]);
+            x3 = as_bf16x8(xr[j][3]);
+          } else if (m < p.M) {
+            const uint8_t *xp = xs + m * XROW + bl * 256 + lg * 32;
+            x0 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xp));
+            x1 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xp + 16));
+            x2 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xp + 128));
+            x3 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xp + 144));
           } else {
             x0 = x1 = x2 = x3 = as_bf16x8(u32x4{0, 0, 0, 0});
           }
@@ -327,7 +326,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
 #pragma unroll
     for (int t = 0; t < MT; ++t) rb[(wave * MT + t) * 64 + lane] = acc[t];
     lds_barrier();
-    for (int idx = threadIdx.x; idx < MT * 64; idx += 256) {
+    for (int idx = tid; idx < MT * 64; idx += 256) {
       const int t = idx >> 6, ln = idx & 63;
       f32x4 v = rb[(0 * MT + t) * 64 + ln];
       v += rb[(1 * MT + t) * 64 + ln];
@@ -340,7 +339,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
   lds_barrier();
   // results of the unit: epilogue (one K part) or fp32 partial sums
   const int nitems = (tile_end - tile_begin) * MT * 64;
-  for (int idx = threadIdx.x; idx < nitems; idx += 256) {
+  for (int idx = tid; idx < nitems; idx += 256) {
     const int tl = idx / (MT * 64), t = (idx >> 6) % MT, ln = idx & 63;
     const int m = t * 16 + (ln & 15);
     const int n = (tile_begin + tl) * 16 + 4 * (ln >> 4);
@@ -353,8 +352,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
 }
 
 size_t gemv_lds_bytes(int M, int MT, int kpb, int rg) {
-  return (size_t)GEMV_NBUF * 16 * gemv_kpb4(kpb) * 128 + (size_t)M * gemv_xrow(kpb) + 2 * 4 * MT * 64 * 16 +
-         (size_t)rg * MT * 64 * 16 + (size_t)M * 4;
+  return (size_t)gemv_nbuf(MT) * 16 * gemv_kpb4(kpb) * 128 + (MT == 1 ? 0 : (size_t)M * gemv_xrow(kpb)) +
+         2 * 4 * MT * 64 * 16 + (size_t)rg * MT * 64 * 16;
 }
 
 // Sums the K parts of gemv_kernel in part order and applies the epilogue.
@@ -375,6 +374,77 @@ __global__ __launch_bounds__(64) void gemv_finish(GemvParams p, int kparts) {
   for (int q = 1; q < GEMV_MAX_PARTS; ++q)
     if (q < kparts) s += v[q];
   store4<MODE>(p, m, n, s);
+}
+
+// One workgroup per row m: sums the K parts of every output of the row in
+// part order, stores the kv_a columns (n >= n_split) into the caches, and
+// normalises the bf16 q_a columns: r = rsqrt(mean(q_a^2) + eps),
+// y = bf16(bf16(q_a * r) * gamma)  (inference/ops.py:10-12, :130).
+constexpr int QKVA_FIN_MAXG = 3;  // float4 groups per thread: N <= 3 * 4 * 256
+__global__ __launch_bounds__(256) void qkva_finish_norm_kernel(GemvParams p, int kparts, const uint16_t *gamma,
+                                                               float eps) {
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const int ng = p.N >> 2;
+  f32x4 v[QKVA_FIN_MAXG];
+  float ss = 0.f;
+  // every part of every group in flight before the first add (parts in
+  // batches of 8)
+  f32x4 s[QKVA_FIN_MAXG];
+#pragma unroll
+  for (int i = 0; i < QKVA_FIN_MAXG; ++i) s[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int q0 = 0; q0 < kparts; q0 += 8) {
+    f32x4 t[QKVA_FIN_MAXG][8];
+#pragma unroll
+    for (int i = 0; i < QKVA_FIN_MAXG; ++i) {
+      const int g = tid + 256 * i;
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        t[i][q] = (g < ng && q0 + q < kparts)
+                      ? *reinterpret_cast<const f32x4 *>(p.part + ((size_t)(q0 + q) * p.M + m) * p.N + 4 * g)
+                      : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < QKVA_FIN_MAXG; ++i)
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (q0 + q < kparts) s[i] += t[i][q];  // part order
+  }
+#pragma unroll
+  for (int i = 0; i < QKVA_FIN_MAXG; ++i) {
+    const int g = tid + 256 * i;
+    v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (g < ng) {
+      if (4 * g >= p.n_split) {
+        store4<GEMV_QKVA>(p, m, 4 * g, s[i]);
+      } else {
+        v[i] = f32x4{round_bf16(s[i].x), round_bf16(s[i].y), round_bf16(s[i].z), round_bf16(s[i].w)};  // q_a as stored (bf16)
+        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  __shared__ float part[4];
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  const float r = __builtin_amdgcn_rsqf(((part[0] + part[1]) + (part[2] + part[3])) / (float)p.n_split + eps);
+#pragma unroll
+  for (int i = 0; i < QKVA_FIN_MAXG; ++i) {
+    const int n = 4 * (tid + 256 * i);
+    if (n < p.n_split) {
+      const u32x2 gm = *reinterpret_cast<const u32x2 *>(gamma + n);
+      const u32x2 o = {pack_bf16(round_bf16(v[i].x * r) * lo_bf(gm.x), round_bf16(v[i].y * r) * hi_bf(gm.x)),
+                       pack_bf16(round_bf16(v[i].z * r) * lo_bf(gm.y), round_bf16(v[i].w * r) * hi_bf(gm.y))};
+      *reinterpret_cast<u32x2 *>(p.y + (size_t)m * p.ldy + n) = o;
+    }
+  }
+}
+
+int launch_qkva_finish_norm(const GemvParams &p, int kparts, const uint16_t *gamma, float eps, hipStream_t st) {
+  if (p.N > QKVA_FIN_MAXG * 4 * 256 || p.N % 4 || p.n_split % 4)
+    return fail(AMLA_EUNSUPPORTED, "q_a/kv_a finish: N=%d exceeds %d or is not a multiple of 4", p.N,
+                QKVA_FIN_MAXG * 4 * 256);
+  qkva_finish_norm_kernel<<<dim3((unsigned)p.M), 256, 0, st>>>(p, kparts, gamma, eps);
+  return check_launch("q_a/kv_a finish");
 }
 
 GemvPlan plan_gemv(int M, int N, int K) {
@@ -438,7 +508,7 @@ static void launch_mt(const GemvParams &p, int mode, const GemvPlan &pl, hipStre
   }
 }
 
-int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t st) {
+int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t st, bool finish) {
   if (p0.M < 1 || p0.M > 64) return fail(AMLA_EINVAL, "skinny fp8 GEMM needs 1 <= M <= 64 (got %d)", p0.M);
   if (p0.N % 16 || p0.K % 128)
     return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM needs N %% 16 == 0 and K %% 128 == 0 (N=%d K=%d)", p0.N, p0.K);
@@ -450,7 +520,7 @@ int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t 
   if (MT == 1) launch_mt<1>(p0, mode, pl, st);
   else if (MT == 2) launch_mt<2>(p0, mode, pl, st);
   else launch_mt<4>(p0, mode, pl, st);
-  if (pl.kparts > 1) {
+  if (pl.kparts > 1 && finish) {
     const int64_t total = (int64_t)p0.M * (p0.N / 4);
     const unsigned blocks = (unsigned)((total + 63) / 64);
     switch (mode) {
@@ -467,33 +537,71 @@ int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t 
 
 // One workgroup per row: fp32 sum of squares, r = rsqrt(mean + eps),
 // y = bf16(bf16(x * r) * gamma)  (the two roundings of inference/ops.py:12).
+// Rows of up to RMS_VEC_MAXC * 256 16-byte chunks are read once, every load
+// in flight together, and kept in registers for the output pass; other
+// shapes take the element-wise loop.
+constexpr int RMS_VEC_MAXC = 8;
+template <bool VEC>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t *__restrict__ x, int64_t dim,
                                                        int64_t ldx, const uint16_t *__restrict__ gamma,
                                                        float eps, uint16_t *__restrict__ y,
                                                        int64_t ldy) {
   const uint16_t *xr = x + blockIdx.x * ldx;
   uint16_t *yr = y + blockIdx.x * ldy;
-  float ss = 0.f;
-  for (int64_t j = threadIdx.x; j < dim; j += 256) {
-    const float v = bf2f(xr[j]);
-    ss += v * v;
-  }
-  ss = wave_sum(ss);
+  const int tid = threadIdx.x;
   __shared__ float part[4];
-  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
-  __syncthreads();
-  const float tot = part[0] + part[1] + part[2] + part[3];
-  const float r = rsqrtf(tot / (float)dim + eps);
-  for (int64_t j = threadIdx.x; j < dim; j += 256) {
-    const float nv = round_bf16(bf2f(xr[j]) * r);
-    yr[j] = f2bf(nv * bf2f(gamma[j]));
+  float ss = 0.f;
+  if constexpr (VEC) {
+    const int nc = (int)(dim >> 3);
+    u32x4 v[RMS_VEC_MAXC];
+#pragma unroll
+    for (int i = 0; i < RMS_VEC_MAXC; ++i) {
+      const int c = tid + 256 * i;
+      v[i] = c < nc ? ldg16(xr + c * 8) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < RMS_VEC_MAXC; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss += lo_bf(v[i][e]) * lo_bf(v[i][e]) + hi_bf(v[i][e]) * hi_bf(v[i][e]);
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    const float r = rsqrtf(((part[0] + part[1]) + (part[2] + part[3])) / (float)dim + eps);
+#pragma unroll
+    for (int i = 0; i < RMS_VEC_MAXC; ++i) {
+      const int c = tid + 256 * i;
+      if (c < nc) {
+        const u32x4 g = ldg16(gamma + c * 8);
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = pack_bf16(round_bf16(lo_bf(v[i][e]) * r) * lo_bf(g[e]), round_bf16(hi_bf(v[i][e]) * r) * hi_bf(g[e]));
+        *reinterpret_cast<u32x4 *>(yr + c * 8) = o;
+      }
+    }
+  } else {
+    for (int64_t j = tid; j < dim; j += 256) {
+      const float v = bf2f(xr[j]);
+      ss += v * v;
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    const float r = rsqrtf(((part[0] + part[1]) + (part[2] + part[3])) / (float)dim + eps);
+    for (int64_t j = tid; j < dim; j += 256) {
+      const float nv = round_bf16(bf2f(xr[j]) * r);
+      yr[j] = f2bf(nv * bf2f(gamma[j]));
+    }
   }
 }
 
 int launch_rms_norm(const uint16_t *x, int64_t rows, int64_t dim, int64_t ldx, const uint16_t *gamma,
                     float eps, uint16_t *y, int64_t ldy, hipStream_t st) {
   if (rows == 0) return AMLA_OK;
-  rms_norm_kernel<<<dim3((unsigned)rows), 256, 0, st>>>(x, dim, ldx, gamma, eps, y, ldy);
+  const bool vec = dim % 8 == 0 && dim <= RMS_VEC_MAXC * 256 * 8 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16(x) &&
+                   aligned16(y) && aligned16(gamma);
+  if (vec) rms_norm_kernel<true><<<dim3((unsigned)rows), 256, 0, st>>>(x, dim, ldx, gamma, eps, y, ldy);
+  else rms_norm_kernel<false><<<dim3((unsigned)rows), 256, 0, st>>>(x, dim, ldx, gamma, eps, y, ldy);
   return check_launch("rms_norm");
 }
 

@@ -14,11 +14,10 @@
 // fly, once per row instead of once per row and head.
 //
 // Launch sequence per layer:
-//   gemv  QKVA : q_a and kv_a from hidden (input RMSNorm fused into the
-//                staging of hidden in layer mode); kv_a goes straight into
-//                the caches
-//   gemv  QROPE: q = q_a_layernorm(q_a) W_qb^T (norm fused into the staging
-//                of q_a); RoPE on the q_pe rows at pos[b]
+//   rms_norm   : input RMSNorm of hidden (layer mode only)
+//   gemv  QKVA : fp32 K-part sums of q_a | kv_a from hidden
+//   finish     : kv_a straight into the caches, q_a_layernorm(q_a) fused
+//   gemv  QROPE: q = q_a_norm W_qb^T; RoPE on the q_pe rows at pos[b]
 //   absorb     : qt = gamma_kv * W_UK^T q_nope  -> qbuf (B, H, 576) with q_pe,
 //                stored in attn_kernel's fragment order
 //   attn       : split over context, online softmax, bf16 partial O, (m, l)
@@ -801,7 +800,7 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
 // ---------------------------------------------------------------- orchestration
 
 struct DecodeLayout {
-  size_t qa, q, qbuf, part_ml, part_o, attn, lin, total;
+  size_t xn, qa, q, qbuf, part_ml, part_o, attn, lin, total;
   GemvPlan pa, pb, po;
   int splits, tiles_per_split;
 };
@@ -821,6 +820,7 @@ static DecodeLayout decode_layout(const amla_mla_args &a) {
   L.splits = (ntiles + L.tiles_per_split - 1) / L.tiles_per_split;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes, 256); return o; };
+  L.xn = take((size_t)B * a.hidden * 2);
   L.qa = take((size_t)B * a.q_lora * 2);
   L.q = take((size_t)B * a.heads * HD * 2);
   L.qbuf = take((size_t)B * a.heads * QKD * 2);
@@ -878,12 +878,19 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   uint16_t *q = reinterpret_cast<uint16_t *>(ws + L.q);
   uint16_t *qbuf = reinterpret_cast<uint16_t *>(ws + L.qbuf);
 
-  // 1. [input RMSNorm, fused into the staging of x] q_a | kv_a  (kv_a written
-  //    raw into the caches, inference/ops.py:136-141)
+  // 1. [input RMSNorm, layer mode] q_a | kv_a  (kv_a written raw into the
+  //    caches, inference/ops.py:136-141; forward.py:92)
   mark(ev, 0, st);
+  const uint16_t *xin = x;
+  if (a->input_gamma) {
+    uint16_t *xn = reinterpret_cast<uint16_t *>(ws + L.xn);
+    if ((rc = launch_rms_norm(x, B, a->hidden, a->hidden, reinterpret_cast<const uint16_t *>(a->input_gamma), a->eps,
+                              xn, a->hidden, st)))
+      return rc;
+    xin = xn;
+  }
   GemvParams pa = {};
-  pa.x = x; pa.M = B; pa.ldx = a->hidden;
-  pa.xgamma = reinterpret_cast<const uint16_t *>(a->input_gamma); pa.xeps = a->eps;
+  pa.x = xin; pa.M = B; pa.ldx = a->hidden;
   pa.w0 = reinterpret_cast<const uint8_t *>(a->w_q_a); pa.s0 = a->s_q_a;
   pa.w1 = reinterpret_cast<const uint8_t *>(a->w_kv_a); pa.s1 = a->s_kv_a;
   pa.N = a->q_lora + LORA + ROPE; pa.K = a->hidden; pa.n_split = a->q_lora;
@@ -893,15 +900,22 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pa.ckv_bstride = (int64_t)a->max_seq * LORA; pa.kpe_bstride = (int64_t)a->max_seq * ROPE;
   pa.kv_lora = LORA; pa.rope = ROPE; pa.pos = a->positions; pa.seq_len = 1;
   pa.part = reinterpret_cast<float *>(ws + L.lin);
-  if ((rc = launch_gemv(pa, GEMV_QKVA, L.pa, st))) return rc;
-
-  // 2.-3. q = q_a_layernorm(q_a) W_qb^T (the norm fused into the staging of
-  //    q_a), RoPE on q_pe at pos[b] (inference/ops.py:130-133, :156)
+  // 2. q_a_layernorm (inference/ops.py:130): fused into the K-part finish, or
+  //    a row norm in place when the GEMV needs no finishing pass
   mark(ev, 1, st);
+  const uint16_t *gq = reinterpret_cast<const uint16_t *>(a->gamma_q);
+  if (L.pa.kparts > 1) {
+    if ((rc = launch_gemv(pa, GEMV_QKVA, L.pa, st, false))) return rc;
+    if ((rc = launch_qkva_finish_norm(pa, L.pa.kparts, gq, a->eps, st))) return rc;
+  } else {
+    if ((rc = launch_gemv(pa, GEMV_QKVA, L.pa, st))) return rc;
+    if ((rc = launch_rms_norm(qa, B, a->q_lora, a->q_lora, gq, a->eps, qa, a->q_lora, st))) return rc;
+  }
+
+  // 3. q = q_a_norm W_qb^T, RoPE on q_pe at pos[b] (inference/ops.py:131-133, :156)
   mark(ev, 2, st);
   GemvParams pb = {};
   pb.x = qa; pb.M = B; pb.ldx = a->q_lora;
-  pb.xgamma = reinterpret_cast<const uint16_t *>(a->gamma_q); pb.xeps = a->eps;
   pb.w0 = reinterpret_cast<const uint8_t *>(a->w_q_b); pb.s0 = a->s_q_b;
   pb.N = a->heads * HD; pb.K = a->q_lora; pb.n_split = pb.N;
   pb.y = q; pb.ldy = pb.N;
