@@ -362,7 +362,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       // the compiler does not track their hazards, so the VALU touches of sc
       // below are preceded by explicit wait states.
       constexpr int NSTEP = QKD / 32;
-      constexpr int SD = 4;
+      constexpr int SD = 6;
       const uint32_t kaddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
           (__attribute__((address_space(3))) const uint16_t *)(K + li * KROW + 8 * lg)));
 #define AMLA_RDA(dst, S, MT) \
@@ -382,7 +382,9 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       for (int ks = 0; ks < NSTEP; ++ks) {
         const int c = ks % SD;
         const int later = (NSTEP - 1 - ks) < (SD - 1) ? (NSTEP - 1 - ks) : (SD - 1);  // steps issued after ks
-        if (later == 3) asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
+        if (later == 5) asm volatile("s_waitcnt lgkmcnt(10)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
+        else if (later == 4) asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
+        else if (later == 3) asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
         else if (later == 2) asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
         else if (later == 1) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
         else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
@@ -418,29 +420,33 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
 
       // ---- probabilities relative to the head's fixed reference max; r_t of
       // the lane's rows 4*lg + r (mt 0) and 16 + 4*lg + r (mt 1)
+      // (the scale is positive: the max is taken on the raw scores, and
+      // 2^(scale*s - m_ref) is one fma and one exp per score; rows past the
+      // context exist only in the last tile of a sequence)
       const int tbase = tile * TT;
+      const bool partial = tbase + TT > T;
       u32x4 pk[2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         float sv[8];
-        float mx = -INFINITY;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int tl = mt * 16 + 4 * lg + r;
-            const float v = (tbase + tl < T) ? p.scale_log2 * sc[mt][nt][r] : -INFINITY;
-            sv[mt * 4 + r] = v;
-            mx = fmaxf(mx, v);
-          }
-        mx = max_lane_groups(mx);
+          for (int r = 0; r < 4; ++r) sv[mt * 4 + r] = sc[mt][nt][r];
+        if (partial) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (tbase + (e >> 2) * 16 + 4 * lg + (e & 3) >= T) sv[e] = -INFINITY;
+        }
+        float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+        mx = p.scale_log2 * max_lane_groups(mx);
         if (!have_ref) m_ref[nt] = mx;
         bad[nt] = bad[nt] || (mx > m_ref[nt] + REF_HEADROOM);
         float pv[8];
         float lsum = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float pe = __builtin_amdgcn_exp2f(sv[e] - m_ref[nt]);  // v_exp_f32: 2^-inf = 0
+          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(p.scale_log2, sv[e], -m_ref[nt]));  // 2^-inf = 0
           lsum += pe;
           pv[e] = pe * rc[e >> 2][e & 3];
         }
