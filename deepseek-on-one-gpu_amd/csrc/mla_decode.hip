@@ -361,37 +361,60 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       // inline asm with VGPR accumulators (the O accumulators own the AGPRs);
       // the compiler does not track their hazards, so the VALU touches of sc
       // below are preceded by explicit wait states.
+      // The next tile's own-row preparation (r_t and the rope rotation, as
+      // prepare_own_rows) runs inside this loop between the MFMAs: its 11 LDS
+      // reads go out in three batches (iterations 0, 5, 10), are consumed five
+      // iterations later, and its two LDS writes follow at iteration 15; the
+      // current tile's r_t is read at iteration 12 for step 16.  Every
+      // LDS operation here is inline asm issued in a fixed order, so the wait
+      // for step k's A fragments is a fixed count (LDS operations complete in
+      // order): kLgkm[k] = operations issued after step k's two reads.  The
+      // preparation always runs (past the last tile it reads and writes a stage
+      // nothing reads any more) so that the counts hold.
       constexpr int NSTEP = QKD / 32;
-      constexpr int SD = 6;
+      constexpr int SD = 3;
+      constexpr int kLgkm[NSTEP] = {4, 8, 8, 8, 4, 4, 8, 8, 8, 4, 4, 7, 7, 9, 6, 6, 4, 2};
       const uint32_t kaddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
           (__attribute__((address_space(3))) const uint16_t *)(K + li * KROW + 8 * lg)));
 #define AMLA_RDA(dst, S, MT) \
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(kaddr), "i"(((MT) * 16 * KROW + (S) * 32) * 2))
+#define AMLA_RD(dst, addr, off) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(off))
       f32x4 sc[2][2];
       // r_t of the lane's C-layout rows 4*lg + r (mt 0) and 16 + 4*lg + r (mt 1)
+      // (read at iteration 12, needed from step 16 on)
       f32x4 rc[2];
-      rc[0] = *reinterpret_cast<const f32x4 *>(cur + RT_OFF + (4 * lg) * 4);
-      rc[1] = *reinterpret_cast<const f32x4 *>(cur + RT_OFF + (16 + 4 * lg) * 4);
       u32x4 ab[SD][2];
 #pragma unroll
       for (int d = 0; d < SD; ++d) {
         AMLA_RDA(ab[d][0], d, 0);
         AMLA_RDA(ab[d][1], d, 1);
       }
+      // next tile's rows: this wave's 8 rows, 8 lanes per row (lane q of a row
+      // owns 16-byte chunks q, q+8, .. of the latent row)
+      uint8_t *const nxt = smem + ((it + 1) % NST) * STAGE_BYTES;
+      const uint8_t *const tabn = smem + TAB_OFF + ((tile + 1) & 1) * TAB_BYTES;
+      int pln;
+      asm volatile("v_mov_b32 %0, %1" : "=v"(pln) : "v"(lane));  // recomputed per tile, not held
+      const int prow = wave * 8 + (pln >> 3), pq = pln & 7;
+      const uint32_t rpa = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+          (__attribute__((address_space(3))) const uint8_t *)(nxt + prow * (KROW * 2) + pq * 16)));
+      u32x4 pv4[4], praw, pc0, pc1;
+      float pss = 0.f;
 #pragma unroll
       for (int ks = 0; ks < NSTEP; ++ks) {
         const int c = ks % SD;
-        const int later = (NSTEP - 1 - ks) < (SD - 1) ? (NSTEP - 1 - ks) : (SD - 1);  // steps issued after ks
-        if (later == 5) asm volatile("s_waitcnt lgkmcnt(10)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
-        else if (later == 4) asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
-        else if (later == 3) asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
-        else if (later == 2) asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
-        else if (later == 1) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
-        else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory");
+        switch (kLgkm[ks]) {
+          case 9: asm volatile("s_waitcnt lgkmcnt(9)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
+          case 8: asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
+          case 7: asm volatile("s_waitcnt lgkmcnt(7)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
+          case 6: asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
+          case 4: asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
+          default: asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
+        }
         if (ks == LORA / 32) {
           // latent part complete: apply r_t before the rope K steps (MFMA
           // write -> VALU read, then VALU write -> MFMA read wait states)
-          asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory");
+          asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(rc[0]), "+v"(rc[1])::"memory");
 #pragma unroll
           for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -407,14 +430,73 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
             else
               asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(sc[mt][nt]) : "v"(ab[c][mt]), "v"(qf[nt][ks]));
           }
+        // consume a batch of the next tile's rows (landed: this step's wait
+        // covers every operation issued before step ks's reads)
+        if (ks == 5 || ks == 10) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            pss = dot2_bf16(pv4[i].x, pss);
+            pss = dot2_bf16(pv4[i].y, pss);
+            pss = dot2_bf16(pv4[i].z, pss);
+            pss = dot2_bf16(pv4[i].w, pss);
+          }
+        }
+        if (ks == 15) {
+          // r_t = rsqrt(mean(c_t^2) + eps): sum over the row's 8 lanes (every
+          // lane of the row ends with the total); rope key rotated in fp32,
+          // rounded to bf16 (inference/ops.py:10-12, :93-97)
+          pss += dpp_f32<0xB1>(pss);   // quad_perm [1,0,3,2]
+          pss += dpp_f32<0x4E>(pss);   // quad_perm [2,3,0,1]
+          pss += dpp_f32<0x141>(pss);  // row_half_mirror
+          const float rt = __builtin_amdgcn_rsqf(pss * (1.f / LORA) + p.eps);
+          const f32x4 c0 = __builtin_bit_cast(f32x4, pc0), c1 = __builtin_bit_cast(f32x4, pc1);
+          u32x4 kr;
+          kr.x = rot_pair(praw.x, c0.x, c0.y);
+          kr.y = rot_pair(praw.y, c0.z, c0.w);
+          kr.z = rot_pair(praw.z, c1.x, c1.y);
+          kr.w = rot_pair(praw.w, c1.z, c1.w);
+          const uint32_t rta = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+              (__attribute__((address_space(3))) const uint8_t *)(nxt + RT_OFF + prow * 4)));
+          asm volatile("ds_write_b32 %0, %1\n\tds_write_b128 %2, %3 offset:%4"
+                       :
+                       : "v"(rta), "v"(rt), "v"(rpa), "v"(kr), "i"(LORA * 2 - 0)
+                       : "memory");
+        }
         if (ks + SD < NSTEP) {
           AMLA_RDA(ab[c][0], ks + SD, 0);
           AMLA_RDA(ab[c][1], ks + SD, 1);
+        }
+        if (ks == 0) {
+          // the next tile's copies landed (issued during the previous tile;
+          // this tile's own copies start below)
+          wait_vmcnt<0>();
+          AMLA_RD(pv4[0], rpa, 0);
+          AMLA_RD(pv4[1], rpa, 128);
+          AMLA_RD(pv4[2], rpa, 256);
+          AMLA_RD(pv4[3], rpa, 384);
+        } else if (ks == 5) {
+          AMLA_RD(pv4[0], rpa, 512);
+          AMLA_RD(pv4[1], rpa, 640);
+          AMLA_RD(pv4[2], rpa, 768);
+          AMLA_RD(pv4[3], rpa, 896);
+        } else if (ks == 10) {
+          const uint32_t rawa = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+              (__attribute__((address_space(3))) const uint8_t *)(nxt + K_BYTES + prow * (ROPE * 2) + pq * 16)));
+          const uint32_t taba = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+              (__attribute__((address_space(3))) const uint8_t *)(tabn + prow * (ROPE * 4) + pq * 32)));
+          AMLA_RD(praw, rawa, 0);
+          AMLA_RD(pc0, taba, 0);
+          AMLA_RD(pc1, taba, 16);
+        } else if (ks == 12) {
+          const uint32_t ra = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+              (__attribute__((address_space(3))) const uint8_t *)(cur + RT_OFF + (4 * lg) * 4)));
+          asm volatile("ds_read_b128 %0, %2 offset:0\n\tds_read_b128 %1, %2 offset:64" : "=v"(rc[0]), "=v"(rc[1]) : "v"(ra));
         }
         if (ks < TILE_DMA && dma_next) dma_piece(p, b, tile + 2, T, smem, nst, wave, lane, ks);
       }
       // the softmax reads sc: MFMA write -> VALU read wait states
       asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sc[0][0]), "+v"(sc[0][1]), "+v"(sc[1][0]), "+v"(sc[1][1])::"memory");
+#undef AMLA_RD
 #undef AMLA_RDA
       __builtin_amdgcn_sched_barrier(0);
 
@@ -514,13 +596,6 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
 #undef AMLA_TR
       __builtin_amdgcn_sched_barrier(0);
 
-      // ---- next tile: own rows and table landed -> rotate their rope keys
-      if (tile + 1 < te) {
-        if (tile + 2 < te) wait_vmcnt<TILE_DMA>();
-        else wait_vmcnt<0>();
-        prepare_own_rows(smem + ((it + 1) % NST) * STAGE_BYTES, smem + TAB_OFF + ((tile + 1) & 1) * TAB_BYTES, wave,
-                         lane, p.eps);
-      }
       // barrier without a memory fence: a fence would also wait for the copy
       // of the tile after next; LDS writes (rotated keys) are drained by hand
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
