@@ -109,6 +109,17 @@ def test_decode_ragged_positions():
     _check_cache(gc, rc, [(p, p + 1) for p in pos])
 
 
+def test_decode_batch32_ragged():
+    """Batched decode at batch 32 with ragged positions (the reference's batched-decode
+    workload, at contexts the oracle finishes in seconds): 17..32-row skinny GEMMs and
+    eight splits per sequence."""
+    g = torch.Generator().manual_seed(32)
+    pos = torch.randint(0, 300, (32,), generator=g).tolist()
+    got, want, gc, rc = _run_case("ragged32", 32, 1, pos, 320)
+    assert_parity(got, want, "batch-32 ragged decode")
+    _check_cache(gc, rc, [(p, p + 1) for p in pos])
+
+
 def test_decode_split_count_does_not_matter():
     a, want, _, _ = _run_case("splits", 2, 1, 3000, 8192, max_context=3001)
     b, _, _, _ = _run_case("splits", 2, 1, 3000, 8192, max_context=8192)
