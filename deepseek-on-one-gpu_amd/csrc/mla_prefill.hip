@@ -65,6 +65,46 @@ AMLA_DEV void pstore4(const GemvParams &p, int m, int n, f32x4 v) {
 
 // ---------------------------------------------------------------- K3 GEMM
 
+
+// Eight consecutive outputs n .. n+7 (n % 8 == 0) already rounded to bf16.
+template <int MODE>
+AMLA_DEV void pstore8(const GemvParams &p, int m, int n, u32x4 v) {
+  if (MODE == GEMV_PLAIN) {
+    *reinterpret_cast<u32x4 *>(p.y + (size_t)m * p.ldy + n) = v;
+  } else if (MODE == GEMV_RESID) {
+    const u32x4 r = *reinterpret_cast<const u32x4 *>(p.res + (size_t)m * p.ldr + n);
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = pack_bf16(lo_bf(r[i]) + lo_bf(v[i]), hi_bf(r[i]) + hi_bf(v[i]));
+    *reinterpret_cast<u32x4 *>(p.y + (size_t)m * p.ldy + n) = o;
+  } else if (MODE == GEMV_QKVA) {
+    if (n < p.n_split) {
+      *reinterpret_cast<u32x4 *>(p.y + (size_t)m * p.ldy + n) = v;
+    } else {
+      const int b = m / p.seq_len;
+      const int64_t row = prow_position(p, m);
+      const int nn = n - p.n_split;
+      uint16_t *dst = nn < p.kv_lora ? p.ckv + b * p.ckv_bstride + row * p.kv_lora + nn
+                                     : p.kpe + b * p.kpe_bstride + row * p.rope + (nn - p.kv_lora);
+      *reinterpret_cast<u32x4 *>(dst) = v;
+    }
+  } else {
+    const int d = n % p.head_dim;
+    u32x4 o = v;
+    if (d >= p.nope) {
+      const int64_t row = prow_position(p, m);
+      const float *tab = p.rope_table + (row * (p.rope >> 1) + ((d - p.nope) >> 1)) * 2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a0 = lo_bf(v[i]), a1 = hi_bf(v[i]);
+        const float c = tab[2 * i], s = tab[2 * i + 1];
+        o[i] = pack_bf16(__fsub_rn(__fmul_rn(a0, c), __fmul_rn(a1, s)), __fadd_rn(__fmul_rn(a0, s), __fmul_rn(a1, c)));
+      }
+    }
+    *reinterpret_cast<u32x4 *>(p.y + (size_t)m * p.ldy + n) = o;
+  }
+}
+
 AMLA_DEV f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -73,8 +113,9 @@ AMLA_DEV f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 // Workgroup tile 256 weight rows (n) x 256 activation rows (m), K stage 64,
 // three LDS stages filled by direct global-to-LDS copies: fp8 weight rows
 // (64 B) and bf16 activation rows (128 B), 16-byte chunks swizzled per row
-// (chunk c of weight row r at c ^ ((r >> 1) & 3), of activation row r at
-// c ^ (r & 7)) so the fragment reads hit distinct banks.  Eight waves (two
+// (chunk c of weight row r at c ^ ((r >> 2) & 3), of activation row r at
+// c ^ ((r >> 1) & 7)) so that the 16 lanes of each fragment-read group hit
+// distinct banks.  Eight waves (two
 // per SIMD), each 128 (n) x 64 (m) with 32x32x16 MFMAs; weight fragments are
 // converted exactly from fp8 to bf16 in registers.
 //
@@ -90,9 +131,11 @@ constexpr int G_WOFF = 0, G_XOFF = G_BN * G_BK;  // fp8 weight rows, then bf16 a
 constexpr int G_STAGE = G_BN * G_BK + G_BM * G_BK * 2;
 constexpr int G_LDS = G_NST * G_STAGE;           // 144 KB
 constexpr int G_DMA = G_STAGE / 1024 / G_NW;     // copies per wave per stage
+constexpr int G_EPITCH = 128 * 2 + 8;           // LDS row pitch of the staged output block
+static_assert(G_NW * 64 * G_EPITCH <= G_LDS, "staged output block exceeds LDS");
 
 template <int MODE>
-__global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p) {
+__global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p, bool staged_out) {
   extern __shared__ __align__(16) uint8_t gsm[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -112,8 +155,7 @@ __global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p) {
   // copies: wave w fills weight rows 32w .. +31 (two copies of 16 rows) and
   // activation rows 32w .. +31 (four copies of 8 rows) of each stage
   const bool wfull = nvalid >= G_BN, xfull = m0 + G_BM <= p.M;
-  const uint32_t wlane = (uint32_t)(lane >> 2) * p.K + 16 * ((lane & 3) ^ ((lane >> 3) & 3));
-  const uint32_t xlane = (uint32_t)(lane >> 3) * p.ldx * 2 + 16 * ((lane & 7) ^ (lane >> 3));
+  const uint32_t wrow = (uint32_t)(lane >> 2) * p.K, xrow = (uint32_t)(lane >> 3) * p.ldx * 2;
   auto dma = [&](int it, uint8_t *st) {
     const int k0 = it * G_BK;
 #pragma unroll
@@ -121,10 +163,10 @@ __global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p) {
       const int r0 = 32 * wave + 16 * j;
       const uint8_t *src;
       if (wfull) {
-        src = W + (size_t)(nl0 + r0) * p.K + k0 + wlane;
+        src = W + (size_t)(nl0 + r0) * p.K + k0 + wrow + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
       } else {
         const int r = min(r0 + (lane >> 2), nvalid - 1);
-        src = W + (size_t)(nl0 + r) * p.K + k0 + 16 * ((lane & 3) ^ ((lane >> 3) & 3));
+        src = W + (size_t)(nl0 + r) * p.K + k0 + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
       }
       __builtin_amdgcn_global_load_lds(src, LDS_PTR(st + G_WOFF + r0 * G_BK), 16, 0, 0);
     }
@@ -133,10 +175,12 @@ __global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p) {
       const int r0 = 32 * wave + 8 * j;
       const uint8_t *src;
       if (xfull) {
-        src = reinterpret_cast<const uint8_t *>(p.x + (size_t)(m0 + r0) * p.ldx + k0) + xlane;
+        src = reinterpret_cast<const uint8_t *>(p.x + (size_t)(m0 + r0) * p.ldx + k0) + xrow +
+              16 * ((lane & 7) ^ ((4 * j + (lane >> 4)) & 7));
       } else {
         const int r = min(m0 + r0 + (lane >> 3), p.M - 1);
-        src = reinterpret_cast<const uint8_t *>(p.x + (size_t)r * p.ldx + k0) + 16 * ((lane & 7) ^ (lane >> 3));
+        src = reinterpret_cast<const uint8_t *>(p.x + (size_t)r * p.ldx + k0) +
+              16 * ((lane & 7) ^ ((4 * j + (lane >> 4)) & 7));
       }
       __builtin_amdgcn_global_load_lds(src, LDS_PTR(st + G_XOFF + r0 * (G_BK * 2)), 16, 0, 0);
     }
@@ -148,10 +192,10 @@ __global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p) {
   uint32_t aoff[2], boff[2][2];
 #pragma unroll
   for (int pr = 0; pr < 2; ++pr) {
-    aoff[pr] = G_WOFF + (wn * 128 + j32) * G_BK + 16 * ((2 * pr + hh) ^ ((j32 >> 1) & 3));
+    aoff[pr] = G_WOFF + (wn * 128 + j32) * G_BK + 16 * ((2 * pr + hh) ^ ((j32 >> 2) & 3));
 #pragma unroll
     for (int st = 0; st < 2; ++st)
-      boff[pr][st] = G_XOFF + (wm * 64 + j32) * (G_BK * 2) + 16 * ((4 * pr + 2 * hh + st) ^ (j32 & 7));
+      boff[pr][st] = G_XOFF + (wm * 64 + j32) * (G_BK * 2) + 16 * ((4 * pr + 2 * hh + st) ^ ((j32 >> 1) & 7));
   }
 
   f32x16 acc[4][2];
@@ -219,22 +263,52 @@ __global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p) {
     stg = stg == G_NST - 1 ? 0 : stg + 1;
   }
 
-  // C[n][m]: lane holds m = 32 j + j32 of its rows, n = 32 g + 8 q + 4 hh .. +3
+  // C[n][m]: lane holds m = 32 j + j32 of its rows, n = 32 g + 8 q + 4 hh .. +3.
+  if (!staged_out) {
+    // outputs without 16-byte aligned rows: 8-byte stores straight from the accumulators
+    if (wave_rows) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int m = m0 + wm * 64 + 32 * j + j32;
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int n = n0 + wn * 128 + 32 * g + 8 * q + 4 * hh;
+            if (n < p.N)
+              pstore4<MODE>(p, m, n,
+                            f32x4{acc[g][j][4 * q], acc[g][j][4 * q + 1], acc[g][j][4 * q + 2], acc[g][j][4 * q + 3]} *
+                                s_run);
+          }
+      }
+    }
+    return;
+  }
+  // bf16(C * s) goes through LDS (this wave's 64 x 128 block, rows of m) so
+  // that every global store is 16 bytes of one output row.
+  __builtin_amdgcn_s_barrier();  // every wave is past its last fragment read
+  asm volatile("" ::: "memory");
+  uint8_t *cst = gsm + wave * (64 * G_EPITCH);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 v =
+            f32x4{acc[g][j][4 * q], acc[g][j][4 * q + 1], acc[g][j][4 * q + 2], acc[g][j][4 * q + 3]} * s_run;
+        *reinterpret_cast<u32x2 *>(cst + (32 * j + j32) * G_EPITCH + (32 * g + 8 * q + 4 * hh) * 2) =
+            u32x2{pack_bf16(v.x, v.y), pack_bf16(v.z, v.w)};
+      }
   if (wave_rows) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int m = m0 + wm * 64 + 32 * j + j32;
-      if (m >= p.M) continue;
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int n = n0 + wn * 128 + 32 * g + 8 * q + 4 * hh;
-          if (n < p.N)
-            pstore4<MODE>(p, m, n,
-                          f32x4{acc[g][j][4 * q], acc[g][j][4 * q + 1], acc[g][j][4 * q + 2], acc[g][j][4 * q + 3]} *
-                              s_run);
-        }
+    const int c16 = lane & 15;
+#pragma unroll 4
+    for (int r4 = 0; r4 < 16; ++r4) {
+      const int ml = 4 * r4 + (lane >> 4);
+      const int m = m0 + wm * 64 + ml, n = n0 + wn * 128 + 8 * c16;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(cst + ml * G_EPITCH + c16 * 16);
+      if (m < p.M && n < p.N) pstore8<MODE>(p, m, n, v);
     }
   }
 }
@@ -255,12 +329,20 @@ int launch_gemm(const GemvParams &p, int mode, hipStream_t st) {
     (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS);
     attr_set[mode & 3] = true;
   }
+  // 16-byte output stores need N, the row strides and the bases of every
+  // output (and of the residual) on 8-element boundaries
+  bool staged = p.N % 8 == 0 && p.ldy % 8 == 0 && aligned16(p.y);
+  if (mode == GEMV_RESID) staged = staged && p.ldr % 8 == 0 && aligned16(p.res);
+  if (mode == GEMV_QKVA)
+    staged = staged && aligned16(p.ckv) && aligned16(p.kpe) && p.kv_lora % 8 == 0 && p.rope % 8 == 0 &&
+             p.ckv_bstride % 8 == 0 && p.kpe_bstride % 8 == 0;
+  if (mode == GEMV_QROPE) staged = staged && p.head_dim % 8 == 0 && p.nope % 8 == 0;
   dim3 grid((p.N + G_BN - 1) / G_BN, (p.M + G_BM - 1) / G_BM);
   switch (mode) {
-    case GEMV_PLAIN: gemm_kernel<GEMV_PLAIN><<<grid, G_NW * 64, G_LDS, st>>>(p); break;
-    case GEMV_RESID: gemm_kernel<GEMV_RESID><<<grid, G_NW * 64, G_LDS, st>>>(p); break;
-    case GEMV_QKVA: gemm_kernel<GEMV_QKVA><<<grid, G_NW * 64, G_LDS, st>>>(p); break;
-    default: gemm_kernel<GEMV_QROPE><<<grid, G_NW * 64, G_LDS, st>>>(p); break;
+    case GEMV_PLAIN: gemm_kernel<GEMV_PLAIN><<<grid, G_NW * 64, G_LDS, st>>>(p, staged); break;
+    case GEMV_RESID: gemm_kernel<GEMV_RESID><<<grid, G_NW * 64, G_LDS, st>>>(p, staged); break;
+    case GEMV_QKVA: gemm_kernel<GEMV_QKVA><<<grid, G_NW * 64, G_LDS, st>>>(p, staged); break;
+    default: gemm_kernel<GEMV_QROPE><<<grid, G_NW * 64, G_LDS, st>>>(p, staged); break;
   }
   return check_launch("fp8 GEMM");
 }
