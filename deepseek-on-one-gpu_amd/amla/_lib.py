@@ -53,6 +53,15 @@ SIGNATURES = [
     ("amla_mla_decode_profiled", c_int, [ctypes.POINTER(MlaArgs), c_void_p, ctypes.POINTER(c_void_p)]),
     ("amla_mla_decode_workspace_bytes", c_size_t, [ctypes.POINTER(MlaArgs)]),
     ("amla_mla_prefill_workspace_bytes", c_size_t, [ctypes.POINTER(MlaArgs)]),
+    ("amla_silu_mul", c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    ("amla_swiglu", c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+                            c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    ("amla_swiglu_workspace_bytes", c_size_t, [c_int64, c_int64, c_int64]),
+    ("amla_moe_route", c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int, c_int, c_int, c_int,
+                               c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    ("amla_moe_route_workspace_bytes", c_size_t, [c_int64, c_int64]),
+    ("amla_moe_combine", c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int64, c_float, c_void_p,
+                                 c_void_p]),
 ]
 
 _lib = None

@@ -4,7 +4,10 @@ Drop-in for the MLA half of inference/ops.py: ``rms_norm`` (:10-12),
 ``fp8_linear`` (:15-44), ``yarn_get_mscale`` (:47-50), ``precompute_rope_freqs``
 (:53-83), ``apply_rope`` (:86-97) and ``mla_attention`` (:100-183), plus the
 attention half of ``transformer_layer`` (inference/forward.py:92-94) as
-``mla_layer``.  Same argument names, tensor layouts and dtypes; tensors must be
+``mla_layer``; and the FFN / MoE functions on the same fp8 kernels: ``swiglu``
+(:186-192), ``dense_ffn`` / ``expert_ffn`` (:195-206), ``route`` (:209-257) and
+``moe_block`` (inference/forward.py:112-153, experts handed in).  Same argument
+names, tensor layouts and dtypes; tensors must be
 on a ROCm device.  Every compute call goes to libamla.so; there is no CPU or
 PyTorch fallback (a missing library raises).
 
@@ -307,4 +310,126 @@ def mla_layer(hidden: torch.Tensor, input_layernorm: torch.Tensor, attn_weights:
     a, pos_t = _fill_args(hidden, attn_weights, kv_cache, position, rope_freqs, config, out=out,
                           input_gamma=input_layernorm, residual=hidden, max_context=max_context)
     _run_mla(a, hidden.device, _stream_ptr(hidden), pos_t)
+    return out
+
+
+# ------------------------------------------------------------------ FFN / MoE
+
+def _fp8_pair(w: torch.Tensor, s: torch.Tensor, name: str, shape: tuple, dev) -> None:
+    _need(w, name, FP8, dev)
+    _need(s, name + " scale", torch.float32, dev)
+    if tuple(w.shape) != shape:
+        raise ValueError(f"{name}: shape {tuple(w.shape)}, expected {shape}")
+    if tuple(s.shape) != (math.ceil(shape[0] / 128), math.ceil(shape[1] / 128)):
+        raise ValueError(f"{name} scale: shape {tuple(s.shape)} does not match {shape}")
+
+
+def swiglu(x: torch.Tensor, gate_proj: torch.Tensor, gate_scale: torch.Tensor, up_proj: torch.Tensor,
+           up_scale: torch.Tensor, down_proj: torch.Tensor, down_scale: torch.Tensor) -> torch.Tensor:
+    """inference/ops.py:186-192: down_proj(silu(gate_proj(x)) * up_proj(x)), every fp8 linear,
+    the silu and the product rounded to bf16 as in the reference."""
+    _need_cuda(x, "x")
+    if x.dtype != BF16:
+        raise TypeError(f"swiglu: x must be bfloat16 (got {x.dtype})")
+    if gate_proj.dim() != 2:
+        raise ValueError("swiglu: gate_proj must be (intermediate, hidden)")
+    n, k = gate_proj.shape
+    if x.shape[-1] != k:
+        raise ValueError(f"swiglu: x has {x.shape[-1]} features, gate_proj expects {k}")
+    _fp8_pair(gate_proj, gate_scale, "gate_proj", (n, k), x.device)
+    _fp8_pair(up_proj, up_scale, "up_proj", (n, k), x.device)
+    _fp8_pair(down_proj, down_scale, "down_proj", (k, n), x.device)
+    x2 = x.reshape(-1, k)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    y = torch.empty(m, k, dtype=BF16, device=x.device)
+    if m:
+        need = lib().amla_swiglu_workspace_bytes(m, k, n)
+        ws = workspace(x.device, need)
+        check(lib().amla_swiglu(x2.data_ptr(), m, k, gate_proj.data_ptr(), gate_scale.data_ptr(),
+                                up_proj.data_ptr(), up_scale.data_ptr(), n, down_proj.data_ptr(),
+                                down_scale.data_ptr(), y.data_ptr(), ws.data_ptr(), ws.numel(), _stream_ptr(x)),
+              "swiglu")
+    return y.view(*x.shape[:-1], k)
+
+
+def dense_ffn(hidden: torch.Tensor, mlp_weights: dict) -> torch.Tensor:
+    """inference/ops.py:195-199."""
+    return swiglu(hidden, *mlp_weights["gate_proj"], *mlp_weights["up_proj"], *mlp_weights["down_proj"])
+
+
+def expert_ffn(hidden: torch.Tensor, expert_weights: dict) -> torch.Tensor:
+    """inference/ops.py:202-206."""
+    return swiglu(hidden, *expert_weights["gate_proj"], *expert_weights["up_proj"], *expert_weights["down_proj"])
+
+
+def route(hidden: torch.Tensor, gate_weight: torch.Tensor, config) -> tuple[torch.Tensor, torch.Tensor]:
+    """inference/ops.py:209-257: sigmoid scores, group-limited top-k, optional normalisation.
+
+    Returns (indices int64, weights fp32), each (*hidden.shape[:-1], num_experts_per_tok).
+    """
+    _need_cuda(hidden, "hidden")
+    if hidden.dtype != BF16:
+        raise TypeError(f"route: hidden must be bfloat16 (got {hidden.dtype})")
+    _need(gate_weight, "gate_weight", BF16, hidden.device)
+    E, d = gate_weight.shape
+    if hidden.shape[-1] != d:
+        raise ValueError(f"route: hidden has {hidden.shape[-1]} features, gate_weight expects {d}")
+    if E != config.n_routed_experts:
+        raise ValueError(f"route: gate_weight has {E} experts, config says {config.n_routed_experts}")
+    top_k = config.num_experts_per_tok
+    h2 = hidden.reshape(-1, d)
+    if not h2.is_contiguous() or h2.data_ptr() % 16:
+        h2 = h2.contiguous()
+    m = h2.shape[0]
+    idx = torch.empty(m, top_k, dtype=torch.int64, device=hidden.device)
+    w = torch.empty(m, top_k, dtype=torch.float32, device=hidden.device)
+    if m:
+        ws = workspace(hidden.device, lib().amla_moe_route_workspace_bytes(m, E))
+        check(lib().amla_moe_route(h2.data_ptr(), m, d, gate_weight.data_ptr(), E, config.n_group,
+                                   config.topk_group, top_k, int(bool(config.norm_topk_prob)), idx.data_ptr(),
+                                   w.data_ptr(), ws.data_ptr(), ws.numel(), _stream_ptr(hidden)), "route")
+    shape = (*hidden.shape[:-1], top_k)
+    return idx.view(shape), w.view(shape)
+
+
+def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: dict, experts, config) -> torch.Tensor:
+    """inference/forward.py:112-153 with the routed experts handed in.
+
+    ``experts`` maps an expert index to its weight dict (a Mapping, or a
+    callable taking the index) on the same device; the reference's
+    weight_store / gpu_transfer streaming is out of scope here.  As in the
+    reference, the chosen indices come to the host once (one synchronisation).
+    Each chosen expert then runs once over all tokens that chose it (the
+    reference loops over (token, k) pairs), and the combine keeps the
+    reference's order and bf16 roundings: per token, k = 0.. accumulates
+    bf16(bf16(w_k) * expert_k(x)) into a bf16 sum, then shared + sum * 2.5.
+    """
+    get = experts if callable(experts) else experts.__getitem__
+    idx, w = route(hidden, gate_weight, config)
+    shared_out = expert_ffn(hidden, shared_weights)
+    d = hidden.shape[-1]
+    top_k = config.num_experts_per_tok
+    h2 = hidden.reshape(-1, d)
+    m = h2.shape[0]
+    out = torch.empty_like(hidden)
+    if m == 0:
+        return out
+    flat = idx.reshape(-1).cpu()
+    eout = torch.empty(m * top_k, d, dtype=BF16, device=hidden.device)
+    order = torch.argsort(flat, stable=True)
+    experts_sorted = flat[order]
+    uniq, counts = torch.unique_consecutive(experts_sorted, return_counts=True)
+    start = 0
+    for e, c in zip(uniq.tolist(), counts.tolist()):
+        slots = order[start:start + c].to(hidden.device, non_blocking=True)
+        start += c
+        ye = expert_ffn(h2.index_select(0, torch.div(slots, top_k, rounding_mode="floor")), get(int(e)))
+        eout.index_copy_(0, slots, ye)
+    sh = shared_out.reshape(m, d).contiguous()
+    wc = w.reshape(m, top_k).contiguous()
+    check(lib().amla_moe_combine(sh.data_ptr(), eout.data_ptr(), wc.data_ptr(), m, top_k, d,
+                                 float(config.routed_scaling_factor), out.data_ptr(), _stream_ptr(hidden)),
+          "moe_combine")
     return out

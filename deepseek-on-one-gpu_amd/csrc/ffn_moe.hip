@@ -1,0 +1,327 @@
+// FFN / MoE entry points for gfx950, built on the block-FP8 linear kernels:
+//
+//   amla_silu_mul     <- F.silu(gate) * up inside swiglu, inference/ops.py:189-191
+//   amla_swiglu       <- swiglu / dense_ffn / expert_ffn, inference/ops.py:186-206
+//   amla_moe_route    <- route, inference/ops.py:209-257
+//   amla_moe_combine  <- the combine of moe_block, inference/forward.py:138-153
+//
+// swiglu runs the gate and up projections with the skinny (M <= 64) or large
+// fp8 GEMM, one elementwise pass for silu * up, and the down projection; the
+// rounding points are the reference's (bf16 after every linear, after silu and
+// after the product).  Routing computes the fp32 logits with bf16 MFMAs (exact
+// products, fp32 sums), then one wave per token does the sigmoid, the group
+// ranking and the top-k in fp32.
+#include <math.h>
+
+#include <algorithm>
+
+#include "amla_common.h"
+#include "amla_internal.h"
+
+namespace amla {
+
+// ---------------------------------------------------------------- silu * up
+
+AMLA_DEV float silu_bf16(float g) { return round_bf16(g / (1.f + expf(-g))); }
+
+// h[i] = bf16( bf16(silu(g[i])) * u[i] ); eight elements per thread step.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restrict__ g, const uint16_t *__restrict__ u,
+                                                       int64_t n8, int64_t n, uint16_t *__restrict__ h) {
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < n8; c += (int64_t)gridDim.x * blockDim.x) {
+    const u32x4 gv = *reinterpret_cast<const u32x4 *>(g + c * 8);
+    const u32x4 uv = *reinterpret_cast<const u32x4 *>(u + c * 8);
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = pack_bf16(silu_bf16(lo_bf(gv[i])) * lo_bf(uv[i]), silu_bf16(hi_bf(gv[i])) * hi_bf(uv[i]));
+    *reinterpret_cast<u32x4 *>(h + c * 8) = o;
+  }
+  // elements past the last full group of 8 (all of them when a pointer is not 16-byte aligned)
+  for (int64_t t = n8 * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n;
+       t += (int64_t)gridDim.x * blockDim.x)
+    h[t] = f2bf(silu_bf16(bf2f(g[t])) * bf2f(u[t]));
+}
+
+static int launch_silu_mul(const uint16_t *g, const uint16_t *u, int64_t n, uint16_t *h, hipStream_t st) {
+  const int64_t n8 = (aligned16(g) && aligned16(u) && aligned16(h)) ? n / 8 : 0;
+  const int64_t work = std::max<int64_t>(n8, n - n8 * 8);
+  const int blocks = (int)std::min<int64_t>((work + 255) / 256, 4096);
+  silu_mul_kernel<<<std::max(blocks, 1), 256, 0, st>>>(g, u, n8, n, h);
+  return check_launch("silu_mul");
+}
+
+// ---------------------------------------------------------------- swiglu
+
+// One fp8 linear (y = bf16(x W^T)), skinny or large-M path.
+static int fp8_linear_into(const uint16_t *x, int m, int k, const uint8_t *w, const float *s, int n, uint16_t *y,
+                           float *part, hipStream_t st) {
+  GemvParams p = {};
+  p.x = x;
+  p.M = m;
+  p.ldx = k;
+  p.w0 = w;
+  p.s0 = s;
+  p.N = n;
+  p.K = k;
+  p.n_split = n;
+  p.y = y;
+  p.ldy = n;
+  p.seq_len = 1;
+  if (m > 64) return launch_gemm(p, GEMV_PLAIN, st);
+  const GemvPlan pl = plan_gemv(m, n, k);
+  p.part = part;
+  return launch_gemv(p, GEMV_PLAIN, pl, st);
+}
+
+struct SwigluLayout {
+  size_t g, u, part, total;
+};
+
+static SwigluLayout swiglu_layout(int64_t m, int64_t k, int64_t n) {
+  SwigluLayout L;
+  size_t off = 0;
+  L.g = off;
+  off = align_up(off + (size_t)m * n * 2, 256);
+  L.u = off;
+  off = align_up(off + (size_t)m * n * 2, 256);
+  size_t part = 0;
+  if (m <= 64 && m > 0)
+    part = std::max(plan_gemv((int)m, (int)n, (int)k).part_bytes, plan_gemv((int)m, (int)k, (int)n).part_bytes);
+  L.part = off;
+  off = align_up(off + part, 256);
+  L.total = off;
+  return L;
+}
+
+}  // namespace amla
+
+using namespace amla;
+
+extern "C" {
+
+int amla_silu_mul(const void *gate, const void *up, int64_t numel, void *out, void *stream) {
+  if (!gate || !up || !out) return fail(AMLA_EINVAL, "silu_mul: null pointer");
+  if (numel < 0) return fail(AMLA_EINVAL, "silu_mul: numel < 0");
+  if (numel == 0) return AMLA_OK;
+  return launch_silu_mul(static_cast<const uint16_t *>(gate), static_cast<const uint16_t *>(up), numel,
+                         static_cast<uint16_t *>(out), reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t amla_swiglu_workspace_bytes(int64_t m, int64_t k, int64_t n) {
+  if (m <= 0 || k <= 0 || n <= 0) return 0;
+  return swiglu_layout(m, k, n).total;
+}
+
+int amla_swiglu(const void *x, int64_t m, int64_t k, const void *gate_w, const float *gate_s, const void *up_w,
+                const float *up_s, int64_t n, const void *down_w, const float *down_s, void *y, void *workspace,
+                size_t workspace_bytes, void *stream) {
+  if (!x || !gate_w || !gate_s || !up_w || !up_s || !down_w || !down_s || !y)
+    return fail(AMLA_EINVAL, "swiglu: null pointer");
+  if (m < 0 || k <= 0 || n <= 0) return fail(AMLA_EINVAL, "swiglu: bad shape m=%lld k=%lld n=%lld", (long long)m,
+                                             (long long)k, (long long)n);
+  if (m == 0) return AMLA_OK;
+  if (k % 128 || n % 128 || !aligned16(x) || !aligned16(y) || !aligned16(gate_w) || !aligned16(up_w) ||
+      !aligned16(down_w))
+    return fail(AMLA_EUNSUPPORTED,
+                "swiglu: needs hidden and intermediate sizes that are multiples of 128 and 16-byte aligned "
+                "x, y and weights (k=%lld n=%lld)",
+                (long long)k, (long long)n);
+  if (m > INT32_MAX || k > INT32_MAX || n > INT32_MAX) return fail(AMLA_EUNSUPPORTED, "swiglu: sizes above 2^31");
+  const SwigluLayout L = swiglu_layout(m, k, n);
+  if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
+    return fail(AMLA_EWORKSPACE, "swiglu: needs %zu bytes of 16-byte aligned workspace (got %zu)", L.total,
+                workspace ? workspace_bytes : (size_t)0);
+  uint8_t *ws = static_cast<uint8_t *>(workspace);
+  uint16_t *g = reinterpret_cast<uint16_t *>(ws + L.g);
+  uint16_t *u = reinterpret_cast<uint16_t *>(ws + L.u);
+  float *part = reinterpret_cast<float *>(ws + L.part);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const uint16_t *xb = static_cast<const uint16_t *>(x);
+  int rc;
+  if ((rc = fp8_linear_into(xb, (int)m, (int)k, static_cast<const uint8_t *>(gate_w), gate_s, (int)n, g, part, st)))
+    return rc;
+  if ((rc = fp8_linear_into(xb, (int)m, (int)k, static_cast<const uint8_t *>(up_w), up_s, (int)n, u, part, st)))
+    return rc;
+  if ((rc = launch_silu_mul(g, u, m * n, g, st))) return rc;
+  return fp8_linear_into(g, (int)m, (int)n, static_cast<const uint8_t *>(down_w), down_s, (int)k,
+                         static_cast<uint16_t *>(y), part, st);
+}
+
+}  // extern "C"
+
+namespace amla {
+
+// ---------------------------------------------------------------- routing
+
+// logits[m, e] = sum_k f32(hidden[m, k]) * f32(gate_w[e, k]) for a 16-token x
+// 16-expert tile per workgroup; the four waves take interleaved 32-wide K
+// steps and add their partial tiles in wave order through LDS.
+__global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t *__restrict__ hidden,
+                                                           const uint16_t *__restrict__ gw, int M, int D, int E,
+                                                           float *__restrict__ logits) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int e0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  const int r = lane & 15, kq = lane >> 4;
+  const uint16_t *hp = hidden + (size_t)min(m0 + r, M - 1) * D + 8 * kq;
+  const uint16_t *wp = gw + (size_t)min(e0 + r, E - 1) * D + 8 * kq;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int steps = D / 32;
+#pragma unroll 4
+  for (int ks = wave; ks < steps; ks += 4)
+    acc = mfma16(as_bf16x8(ldg16(hp + ks * 32)), as_bf16x8(ldg16(wp + ks * 32)), acc);
+  __shared__ f32x4 red[4][64];
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    f32x4 v = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) v += red[w][lane];
+    // C layout: lane holds rows (tokens) 4 (lane/16) .. +3 of column (expert) lane % 16
+    const int e = e0 + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + 4 * (lane >> 4) + i;
+      if (m < M && e < E) logits[(size_t)m * E + e] = v[i];
+    }
+  }
+}
+
+constexpr int ROUTE_MAX_E = 1024;  // experts per token handled by one wave (16 per lane)
+
+// One wave per token: scores = sigmoid(logits); rank the n_group groups by
+// their maximum score and keep topk_group of them; take the top_k experts of
+// the kept groups by score (ties to the lower index); weights are the scores,
+// divided by (sum + 1e-9) when norm is set.
+__global__ __launch_bounds__(64) void route_select_kernel(const float *__restrict__ logits, int E, int n_group,
+                                                          int topk_group, int top_k, int norm,
+                                                          int64_t *__restrict__ idx_out, float *__restrict__ w_out) {
+  __shared__ float sc[ROUTE_MAX_E];
+  __shared__ float gmax[64];
+  __shared__ int keep[64];
+  const int lane = threadIdx.x, m = blockIdx.x;
+  const float *lg = logits + (size_t)m * E;
+  for (int e = lane; e < E; e += 64) sc[e] = 1.f / (1.f + expf(-lg[e]));
+  __syncthreads();
+  const int gs = E / n_group;
+  if (lane < n_group) {
+    float v = sc[lane * gs];
+    for (int i = 1; i < gs; ++i) v = fmaxf(v, sc[lane * gs + i]);
+    gmax[lane] = v;
+    keep[lane] = 0;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    for (int t = 0; t < topk_group; ++t) {
+      int best = -1;
+      for (int g = 0; g < n_group; ++g)
+        if (!keep[g] && (best < 0 || gmax[g] > gmax[best])) best = g;
+      keep[best] = 1;
+    }
+  }
+  __syncthreads();
+  // candidate scores: experts of dropped groups take part as 0.0 (the
+  // reference's masked_scores), chosen ones are removed as -1
+  for (int e = lane; e < E; e += 64)
+    if (!keep[e / gs]) sc[e] = 0.f;
+  __syncthreads();
+  float sum = 0.f;
+  for (int t = 0; t < top_k; ++t) {
+    float bv = -2.f;
+    int bi = E;
+    for (int e = lane; e < E; e += 64) {
+      const float v = sc[e];
+      if (v > bv) { bv = v; bi = e; }  // ascending e per lane: ties keep the lower index
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) {
+      idx_out[(size_t)m * top_k + t] = bi;
+      w_out[(size_t)m * top_k + t] = bv;
+      sc[bi] = -1.f;
+    }
+    sum += bv;
+    __syncthreads();
+  }
+  if (norm && lane < top_k) {
+    const float d = sum + 1e-9f;
+    w_out[(size_t)m * top_k + lane] = w_out[(size_t)m * top_k + lane] / d;
+  }
+}
+
+// ---------------------------------------------------------------- combine
+
+// out[m] = bf16( shared[m] + bf16( acc * scale ) ),  acc = bf16 running sum
+// over k of bf16( bf16(w[m, k]) * expert_out[m, k] ), in k order.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__restrict__ shared,
+                                                          const uint16_t *__restrict__ eout,
+                                                          const float *__restrict__ w, int top_k, int64_t D,
+                                                          float scale, uint16_t *__restrict__ out) {
+  const int m = blockIdx.y;
+  for (int64_t d = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; d < D; d += (int64_t)gridDim.x * blockDim.x) {
+    float acc = 0.f;
+    for (int k = 0; k < top_k; ++k) {
+      const float wk = round_bf16(w[(size_t)m * top_k + k]);
+      acc = round_bf16(acc + round_bf16(wk * bf2f(eout[((size_t)m * top_k + k) * D + d])));
+    }
+    out[(size_t)m * D + d] = f2bf(bf2f(shared[(size_t)m * D + d]) + round_bf16(acc * scale));
+  }
+}
+
+}  // namespace amla
+
+extern "C" {
+
+size_t amla_moe_route_workspace_bytes(int64_t m, int64_t n_experts) {
+  if (m <= 0 || n_experts <= 0) return 0;
+  return align_up((size_t)m * n_experts * 4, 256);
+}
+
+int amla_moe_route(const void *hidden, int64_t m, int64_t d, const void *gate_weight, int64_t n_experts,
+                   int n_group, int topk_group, int top_k, int norm_topk_prob, int64_t *indices, float *weights,
+                   void *workspace, size_t workspace_bytes, void *stream) {
+  if (!hidden || !gate_weight || !indices || !weights) return fail(AMLA_EINVAL, "moe_route: null pointer");
+  if (m < 0 || d <= 0 || n_experts <= 0 || n_group <= 0 || topk_group <= 0 || top_k <= 0)
+    return fail(AMLA_EINVAL, "moe_route: bad sizes");
+  if (m == 0) return AMLA_OK;
+  if (n_experts % n_group || topk_group > n_group || n_group > 64 || n_experts > ROUTE_MAX_E ||
+      (int64_t)topk_group * (n_experts / n_group) < top_k)
+    return fail(AMLA_EINVAL,
+                "moe_route: needs n_experts %% n_group == 0, topk_group <= n_group <= 64, n_experts <= %d and "
+                "top_k <= topk_group * group size",
+                ROUTE_MAX_E);
+  if (top_k > 64) return fail(AMLA_EUNSUPPORTED, "moe_route: top_k > 64");
+  if (d % 32 || !aligned16(hidden) || !aligned16(gate_weight) || m > (int64_t)65535 * 16 || d > INT32_MAX)
+    return fail(AMLA_EUNSUPPORTED, "moe_route: needs hidden size %% 32 == 0 and 16-byte aligned inputs");
+  const size_t need = amla_moe_route_workspace_bytes(m, n_experts);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return fail(AMLA_EWORKSPACE, "moe_route: needs %zu bytes of 16-byte aligned workspace", need);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  float *logits = static_cast<float *>(workspace);
+  route_logits_kernel<<<dim3((unsigned)((n_experts + 15) / 16), (unsigned)((m + 15) / 16)), 256, 0, st>>>(
+      static_cast<const uint16_t *>(hidden), static_cast<const uint16_t *>(gate_weight), (int)m, (int)d,
+      (int)n_experts, logits);
+  int rc;
+  if ((rc = check_launch("moe_route logits"))) return rc;
+  route_select_kernel<<<dim3((unsigned)m), 64, 0, st>>>(logits, (int)n_experts, n_group, topk_group, top_k,
+                                                        norm_topk_prob, indices, weights);
+  return check_launch("moe_route select");
+}
+
+int amla_moe_combine(const void *shared_out, const void *expert_out, const float *weights, int64_t m, int top_k,
+                     int64_t d, float routed_scaling_factor, void *out, void *stream) {
+  if (!shared_out || !expert_out || !weights || !out) return fail(AMLA_EINVAL, "moe_combine: null pointer");
+  if (m < 0 || top_k <= 0 || d <= 0) return fail(AMLA_EINVAL, "moe_combine: bad sizes");
+  if (m == 0) return AMLA_OK;
+  if (m > 65535) return fail(AMLA_EUNSUPPORTED, "moe_combine: at most 65535 tokens per call");
+  const unsigned bx = (unsigned)std::min<int64_t>((d + 255) / 256, 64);
+  moe_combine_kernel<<<dim3(bx, (unsigned)m), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t *>(shared_out), static_cast<const uint16_t *>(expert_out), weights, top_k, d,
+      routed_scaling_factor, static_cast<uint16_t *>(out));
+  return check_launch("moe_combine");
+}
+
+}  // extern "C"

@@ -631,7 +631,7 @@ using namespace amla;
 
 extern "C" {
 
-int amla_abi_version(void) { return 100; }
+int amla_abi_version(void) { return 101; }
 
 const char *amla_last_error(void) { return g_last_error.c_str(); }
 

@@ -139,6 +139,46 @@ int amla_mla_prefill(const amla_mla_args *args, void *stream);
 size_t amla_mla_decode_workspace_bytes(const amla_mla_args *args);
 size_t amla_mla_prefill_workspace_bytes(const amla_mla_args *args);
 
+/* ---- FFN / MoE on the same fp8 kernels ---- */
+
+/* The elementwise half of swiglu, inference/ops.py:189-191 (F.silu(gate) * up):
+ *   out[i] = bf16( bf16( g / (1 + exp(-g)) ) * up[i] ),  g = f32(gate[i])
+ * gate, up, out: numel bf16 values (out may alias gate). */
+int amla_silu_mul(const void *gate, const void *up, int64_t numel, void *out, void *stream);
+
+/* Replaces swiglu(x, gate_proj, gate_scale, up_proj, up_scale, down_proj,
+ * down_scale), inference/ops.py:186-192, and so dense_ffn / expert_ffn
+ * (:195-206):  y = fp8_linear( bf16(silu(fp8_linear(x, gate))) * fp8_linear(x, up), down )
+ * x (m, k) bf16; gate_w, up_w (n, k) e4m3fn with (ceil(n/128), ceil(k/128))
+ * fp32 scales; down_w (k, n) with (ceil(k/128), ceil(n/128)) scales; y (m, k)
+ * bf16.  k and n multiples of 128.  Workspace (16-byte aligned) of
+ * amla_swiglu_workspace_bytes(m, k, n) bytes; scratch only. */
+int amla_swiglu(const void *x, int64_t m, int64_t k, const void *gate_w, const float *gate_s, const void *up_w,
+                const float *up_s, int64_t n, const void *down_w, const float *down_s, void *y, void *workspace,
+                size_t workspace_bytes, void *stream);
+size_t amla_swiglu_workspace_bytes(int64_t m, int64_t k, int64_t n);
+
+/* Replaces route(hidden, gate_weight, config), inference/ops.py:209-257:
+ *   scores = sigmoid(f32(hidden) @ f32(gate_weight)^T); keep the topk_group
+ *   groups (n_experts / n_group experts each) with the largest maximum score;
+ *   indices = the top_k experts by score with the other groups' scores at 0.0
+ *   (ties to the lower index); weights = their scores, / (sum + 1e-9) when
+ *   norm_topk_prob.
+ * hidden (m, d) bf16 (d % 32 == 0); gate_weight (n_experts, d) bf16;
+ * indices (m, top_k) int64, weights (m, top_k) fp32.  Workspace of
+ * amla_moe_route_workspace_bytes(m, n_experts) bytes (the fp32 logits). */
+int amla_moe_route(const void *hidden, int64_t m, int64_t d, const void *gate_weight, int64_t n_experts,
+                   int n_group, int topk_group, int top_k, int norm_topk_prob, int64_t *indices, float *weights,
+                   void *workspace, size_t workspace_bytes, void *stream);
+size_t amla_moe_route_workspace_bytes(int64_t m, int64_t n_experts);
+
+/* The combine of moe_block, inference/forward.py:138-153, for m tokens:
+ *   acc = 0;  for k in 0..top_k-1:  acc = bf16( acc + bf16( bf16(w[t, k]) * expert_out[t, k] ) )
+ *   out[t] = bf16( shared_out[t] + bf16( acc * routed_scaling_factor ) )
+ * shared_out, out (m, d) bf16; expert_out (m, top_k, d) bf16; weights (m, top_k) fp32. */
+int amla_moe_combine(const void *shared_out, const void *expert_out, const float *weights, int64_t m, int top_k,
+                     int64_t d, float routed_scaling_factor, void *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
