@@ -180,6 +180,57 @@ def cpu_baseline(T, B):
 
 # ------------------------------------------------------------------ main
 
+def _fp8_on_device(n, k, gen, dev):
+    """Random e4m3fn codes (no NaN codes) and scales in [0.5, 1.5) generated on the device."""
+    codes = torch.randint(0, 256, (n, k), generator=gen, device=dev, dtype=torch.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0
+    scale = torch.rand((n + 127) // 128, (k + 127) // 128, generator=gen, device=dev) + 0.5
+    return codes.view(torch.float8_e4m3fn), scale
+
+
+def _time_eager(fn, reps):
+    fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def ffn_extras(B, dev):
+    """Decode FFN figures: dense SwiGLU (layers 0-2 shape) and the full MoE block
+    (router + shared expert + 8 of 256 routed experts per token) for B tokens."""
+    out = {}
+    d, di, mi, E = CFG.hidden_size, CFG.intermediate_size, CFG.moe_intermediate_size, CFG.n_routed_experts
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(synth.seed_of("bench", "ffn") & 0x7FFFFFFF)
+    x = (torch.randn(B, 1, d, generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+    dense = {"gate_proj": _fp8_on_device(di, d, gen, dev), "up_proj": _fp8_on_device(di, d, gen, dev),
+             "down_proj": _fp8_on_device(d, di, gen, dev)}
+    ms = _time_eager(lambda: ops.dense_ffn(x, dense), 20)
+    out["dense_ffn_b8_us"] = round(ms * 1000, 2)
+    out["dense_ffn_b8_hbm_gbs"] = round(3 * di * d / (ms * 1e-3) / 1e9, 1)
+    del dense
+    experts = [{"gate_proj": _fp8_on_device(mi, d, gen, dev), "up_proj": _fp8_on_device(mi, d, gen, dev),
+                "down_proj": _fp8_on_device(d, mi, gen, dev)} for _ in range(E)]
+    shared = {"gate_proj": _fp8_on_device(mi, d, gen, dev), "up_proj": _fp8_on_device(mi, d, gen, dev),
+              "down_proj": _fp8_on_device(d, mi, gen, dev)}
+    gw = (torch.randn(E, d, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    idx, _ = ops.route(x, gw, CFG)
+    n_used = int(torch.unique(idx).numel())
+    ms = _time_eager(lambda: ops.moe_block(x, gw, shared, experts, CFG), 10)
+    out["moe_block_b8_us"] = round(ms * 1000, 2)
+    out["moe_block_b8_experts"] = n_used
+    moved = (n_used + 1) * 3 * mi * d + E * d * 2
+    out["moe_block_b8_hbm_gbs"] = round(moved / (ms * 1e-3) / 1e9, 1)
+    del experts, shared
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -263,6 +314,8 @@ def main():
         extras["prefill_4096_ms"] = round(pms, 3)
         extras["prefill_4096_tflops"] = round(prefill_flops(S) / (pms * 1e-3) / 1e12, 1)
         extras["prefill_frac_bf16_peak"] = round(extras["prefill_4096_tflops"] / BF16_PEAK_TFLOPS, 4)
+        del hp, cp
+        extras.update(ffn_extras(B, dev))
         log(f"[bench] extras: {extras}")
 
     result = {

@@ -17,6 +17,7 @@ reference's scalar position cannot express a ragged batch).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Sequence
 
@@ -401,9 +402,9 @@ def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: d
     callable taking the index) on the same device; the reference's
     weight_store / gpu_transfer streaming is out of scope here.  As in the
     reference, the chosen indices come to the host once (one synchronisation).
-    Each chosen expert then runs once over all tokens that chose it (the
-    reference loops over (token, k) pairs), and the combine keeps the
-    reference's order and bf16 roundings: per token, k = 0.. accumulates
+    amla_moe_experts then runs each chosen expert once over all tokens that
+    chose it (the reference loops over (token, k) pairs), and the combine keeps
+    the reference's order and bf16 roundings: per token, k = 0.. accumulates
     bf16(bf16(w_k) * expert_k(x)) into a bf16 sum, then shared + sum * 2.5.
     """
     get = experts if callable(experts) else experts.__getitem__
@@ -411,25 +412,44 @@ def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: d
     shared_out = expert_ffn(hidden, shared_weights)
     d = hidden.shape[-1]
     top_k = config.num_experts_per_tok
+    E = config.n_routed_experts
     h2 = hidden.reshape(-1, d)
+    if not h2.is_contiguous() or h2.data_ptr() % 16:
+        h2 = h2.contiguous()
     m = h2.shape[0]
     out = torch.empty_like(hidden)
     if m == 0:
         return out
-    flat = idx.reshape(-1).cpu()
-    eout = torch.empty(m * top_k, d, dtype=BF16, device=hidden.device)
-    order = torch.argsort(flat, stable=True)
-    experts_sorted = flat[order]
-    uniq, counts = torch.unique_consecutive(experts_sorted, return_counts=True)
-    start = 0
-    for e, c in zip(uniq.tolist(), counts.tolist()):
-        slots = order[start:start + c].to(hidden.device, non_blocking=True)
-        start += c
-        ye = expert_ffn(h2.index_select(0, torch.div(slots, top_k, rounding_mode="floor")), get(int(e)))
-        eout.index_copy_(0, slots, ye)
+    idx_host = idx.reshape(m, top_k).cpu().contiguous()
+    tables = [(ctypes.c_void_p * E)() for _ in range(6)]
+    n_inter = None
+    keep = []
+    for e in torch.unique(idx_host).tolist():
+        ew = get(int(e))
+        for j, key in enumerate(("gate_proj", "up_proj", "down_proj")):
+            wt, sc = ew[key]
+            _need(wt, f"expert {e} {key}", FP8, hidden.device)
+            _need(sc, f"expert {e} {key} scale", torch.float32, hidden.device)
+            tables[2 * j][e] = wt.data_ptr()
+            tables[2 * j + 1][e] = sc.data_ptr()
+            keep.append((wt, sc))
+        ni = ew["gate_proj"][0].shape[0]
+        if n_inter is None:
+            n_inter = ni
+        elif ni != n_inter:
+            raise ValueError("moe_block: experts of different intermediate sizes")
+        if tuple(ew["gate_proj"][0].shape) != (ni, d) or tuple(ew["up_proj"][0].shape) != (ni, d) or \
+                tuple(ew["down_proj"][0].shape) != (d, ni):
+            raise ValueError(f"moe_block: expert {e} weights do not match hidden size {d}")
+    eout = torch.empty(m, top_k, d, dtype=BF16, device=hidden.device)
+    ws = workspace(hidden.device, lib().amla_moe_experts_workspace_bytes(m, d, top_k, n_inter))
+    stream = _stream_ptr(hidden)
+    check(lib().amla_moe_experts(h2.data_ptr(), m, d, top_k, idx_host.data_ptr(), n_inter, E,
+                                 *[ctypes.cast(t, ctypes.c_void_p) for t in tables], eout.data_ptr(),
+                                 ws.data_ptr(), ws.numel(), stream), "moe_experts")
     sh = shared_out.reshape(m, d).contiguous()
     wc = w.reshape(m, top_k).contiguous()
     check(lib().amla_moe_combine(sh.data_ptr(), eout.data_ptr(), wc.data_ptr(), m, top_k, d,
-                                 float(config.routed_scaling_factor), out.data_ptr(), _stream_ptr(hidden)),
-          "moe_combine")
+                                 float(config.routed_scaling_factor), out.data_ptr(), stream), "moe_combine")
+    del keep
     return out

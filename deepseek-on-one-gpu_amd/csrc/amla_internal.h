@@ -31,7 +31,7 @@ struct GemvParams {
   int M, ldx;
   const uint8_t *w0;  // rows [0, n_split) (all rows unless QKVA)
   const float *s0;
-  const uint8_t *w1;  // rows [n_split, N) for QKVA
+  const uint8_t *w1;  // rows [n_split, N) for QKVA, or for any mode when set (two stacked weights)
   const float *s1;
   int N, K, n_split;
   uint16_t *y;

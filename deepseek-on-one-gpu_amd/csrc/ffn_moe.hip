@@ -3,6 +3,7 @@
 //   amla_silu_mul     <- F.silu(gate) * up inside swiglu, inference/ops.py:189-191
 //   amla_swiglu       <- swiglu / dense_ffn / expert_ffn, inference/ops.py:186-206
 //   amla_moe_route    <- route, inference/ops.py:209-257
+//   amla_moe_experts  <- the routed-expert loop of moe_block, inference/forward.py:139-151
 //   amla_moe_combine  <- the combine of moe_block, inference/forward.py:138-153
 //
 // swiglu runs the gate and up projections with the skinny (M <= 64) or large
@@ -14,6 +15,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <vector>
 
 #include "amla_common.h"
 #include "amla_internal.h"
@@ -322,6 +324,180 @@ int amla_moe_combine(const void *shared_out, const void *expert_out, const float
       static_cast<const uint16_t *>(shared_out), static_cast<const uint16_t *>(expert_out), weights, top_k, d,
       routed_scaling_factor, static_cast<uint16_t *>(out));
   return check_launch("moe_combine");
+}
+
+}  // extern "C"
+
+namespace amla {
+
+// ---------------------------------------------------------------- routed experts
+
+constexpr int MOE_MAX_SLOTS = 512;  // (token, k) slots per chunk; their row lists travel as kernel arguments
+
+struct RowList {
+  int32_t row[MOE_MAX_SLOTS];
+};
+
+// dst row i (of `rows`) = src row list.row[i]  (gather), or dst row list.row[i] = src row i (scatter)
+template <bool SCATTER>
+__global__ __launch_bounds__(256) void move_rows_kernel(const uint16_t *__restrict__ src, int64_t d, int rows,
+                                                        RowList list, uint16_t *__restrict__ dst) {
+  const int i = blockIdx.x;
+  if (i >= rows) return;
+  const uint16_t *s = src + (size_t)(SCATTER ? i : list.row[i]) * d;
+  uint16_t *t = dst + (size_t)(SCATTER ? list.row[i] : i) * d;
+  for (int64_t c = threadIdx.x; c < d / 8; c += blockDim.x)
+    *reinterpret_cast<u32x4 *>(t + c * 8) = *reinterpret_cast<const u32x4 *>(s + c * 8);
+}
+
+// h[r, j] = bf16( bf16(silu(gu[r, j])) * gu[r, n + j] ) for rows r of [gate | up]
+__global__ __launch_bounds__(256) void silu_mul_rows_kernel(const uint16_t *__restrict__ gu, int rows, int n,
+                                                            uint16_t *__restrict__ h) {
+  const int r = blockIdx.y;
+  if (r >= rows) return;
+  const uint16_t *g = gu + (size_t)r * 2 * n, *u = g + n;
+  for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < n / 8; c += gridDim.x * blockDim.x) {
+    const u32x4 gv = *reinterpret_cast<const u32x4 *>(g + c * 8);
+    const u32x4 uv = *reinterpret_cast<const u32x4 *>(u + c * 8);
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = pack_bf16(silu_bf16(lo_bf(gv[i])) * lo_bf(uv[i]), silu_bf16(hi_bf(gv[i])) * hi_bf(uv[i]));
+    *reinterpret_cast<u32x4 *>(h + (size_t)r * n + c * 8) = o;
+  }
+}
+
+struct MoeLayout {
+  int chunk_tokens;
+  size_t xs, ys, gu, h, part, total;
+};
+
+static MoeLayout moe_layout(int64_t m, int64_t d, int top_k, int64_t n) {
+  MoeLayout L;
+  L.chunk_tokens = (int)std::min<int64_t>(m, MOE_MAX_SLOTS / top_k);
+  const size_t slots = (size_t)L.chunk_tokens * top_k;
+  const int mg = std::min(L.chunk_tokens, 64);  // tokens of one expert on the skinny path
+  size_t off = 0;
+  L.xs = off;
+  off = align_up(off + slots * d * 2, 256);
+  L.ys = off;
+  off = align_up(off + slots * d * 2, 256);
+  L.gu = off;
+  off = align_up(off + (size_t)L.chunk_tokens * 2 * n * 2, 256);
+  L.h = off;
+  off = align_up(off + (size_t)L.chunk_tokens * n * 2, 256);
+  L.part = off;
+  off = align_up(off + std::max(plan_gemv(mg, (int)(2 * n), (int)d).part_bytes, plan_gemv(mg, (int)d, (int)n).part_bytes),
+                 256);
+  L.total = off;
+  return L;
+}
+
+}  // namespace amla
+
+extern "C" {
+
+size_t amla_moe_experts_workspace_bytes(int64_t m, int64_t d, int top_k, int64_t n_inter) {
+  if (m <= 0 || d <= 0 || top_k <= 0 || top_k > 64 || n_inter <= 0) return 0;
+  return moe_layout(m, d, top_k, n_inter).total;
+}
+
+int amla_moe_experts(const void *hidden, int64_t m, int64_t d, int top_k, const int64_t *indices, int64_t n_inter,
+                     int64_t n_experts, const void *const *gate_w, const float *const *gate_s,
+                     const void *const *up_w, const float *const *up_s, const void *const *down_w,
+                     const float *const *down_s, void *expert_out, void *workspace, size_t workspace_bytes,
+                     void *stream) {
+  if (!hidden || !indices || !gate_w || !gate_s || !up_w || !up_s || !down_w || !down_s || !expert_out)
+    return fail(AMLA_EINVAL, "moe_experts: null pointer");
+  if (m < 0 || d <= 0 || top_k <= 0 || n_inter <= 0 || n_experts <= 0) return fail(AMLA_EINVAL, "moe_experts: bad sizes");
+  if (m == 0) return AMLA_OK;
+  if (top_k > 64) return fail(AMLA_EUNSUPPORTED, "moe_experts: top_k > 64");
+  if (d % 128 || n_inter % 256 || d > INT32_MAX || n_inter > INT32_MAX / 2 || !aligned16(hidden) ||
+      !aligned16(expert_out))
+    return fail(AMLA_EUNSUPPORTED,
+                "moe_experts: needs hidden %% 128 == 0, intermediate %% 256 == 0 and 16-byte aligned rows");
+  for (int64_t i = 0; i < m * top_k; ++i) {
+    const int64_t e = indices[i];
+    if (e < 0 || e >= n_experts) return fail(AMLA_EINVAL, "moe_experts: expert index %lld out of range", (long long)e);
+    if (!gate_w[e] || !gate_s[e] || !up_w[e] || !up_s[e] || !down_w[e] || !down_s[e] || !aligned16(gate_w[e]) ||
+        !aligned16(up_w[e]) || !aligned16(down_w[e]))
+      return fail(AMLA_EINVAL, "moe_experts: expert %lld has a null or misaligned weight", (long long)e);
+  }
+  const MoeLayout L = moe_layout(m, d, top_k, n_inter);
+  if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
+    return fail(AMLA_EWORKSPACE, "moe_experts: needs %zu bytes of 16-byte aligned workspace (got %zu)", L.total,
+                workspace ? workspace_bytes : (size_t)0);
+  uint8_t *ws = static_cast<uint8_t *>(workspace);
+  uint16_t *xs = reinterpret_cast<uint16_t *>(ws + L.xs), *ys = reinterpret_cast<uint16_t *>(ws + L.ys);
+  uint16_t *gu = reinterpret_cast<uint16_t *>(ws + L.gu), *hb = reinterpret_cast<uint16_t *>(ws + L.h);
+  float *part = reinterpret_cast<float *>(ws + L.part);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const uint16_t *hid = static_cast<const uint16_t *>(hidden);
+  uint16_t *eout = static_cast<uint16_t *>(expert_out);
+  const int n = (int)n_inter, D = (int)d;
+  int rc;
+  std::vector<int32_t> order;
+  for (int64_t t0 = 0; t0 < m; t0 += L.chunk_tokens) {
+    const int nt = (int)std::min<int64_t>(L.chunk_tokens, m - t0);
+    const int ns = nt * top_k;
+    // slots of this chunk sorted by expert (stable: token-major within an expert)
+    order.resize(ns);
+    for (int i = 0; i < ns; ++i) order[i] = i;
+    const int64_t *ix = indices + t0 * top_k;
+    std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return ix[a] < ix[b]; });
+    RowList gather, scatter;
+    for (int i = 0; i < ns; ++i) {
+      gather.row[i] = (int32_t)(t0 + order[i] / top_k);
+      scatter.row[i] = (int32_t)(t0 * top_k + order[i]);
+    }
+    move_rows_kernel<false><<<ns, 256, 0, st>>>(hid, d, ns, gather, xs);
+    if ((rc = check_launch("moe_experts gather"))) return rc;
+    for (int i0 = 0; i0 < ns;) {
+      const int64_t e = ix[order[i0]];
+      int i1 = i0 + 1;
+      while (i1 < ns && ix[order[i1]] == e) ++i1;
+      const int cnt = i1 - i0;
+      GemvParams p = {};
+      p.x = xs + (size_t)i0 * D;
+      p.M = cnt;
+      p.ldx = D;
+      p.w0 = static_cast<const uint8_t *>(gate_w[e]);
+      p.s0 = gate_s[e];
+      p.w1 = static_cast<const uint8_t *>(up_w[e]);
+      p.s1 = up_s[e];
+      p.N = 2 * n;
+      p.K = D;
+      p.n_split = n;
+      p.y = gu;
+      p.ldy = 2 * n;
+      p.seq_len = 1;
+      p.part = part;
+      rc = cnt > 64 ? launch_gemm(p, GEMV_PLAIN, st) : launch_gemv(p, GEMV_PLAIN, plan_gemv(cnt, 2 * n, D), st);
+      if (rc) return rc;
+      silu_mul_rows_kernel<<<dim3((unsigned)std::max(1, std::min(n / 8 / 256, 16)), (unsigned)cnt), 256, 0, st>>>(
+          gu, cnt, n, hb);
+      if ((rc = check_launch("moe_experts silu_mul"))) return rc;
+      GemvParams q = {};
+      q.x = hb;
+      q.M = cnt;
+      q.ldx = n;
+      q.w0 = static_cast<const uint8_t *>(down_w[e]);
+      q.s0 = down_s[e];
+      q.N = D;
+      q.K = n;
+      q.n_split = D;
+      q.y = ys + (size_t)i0 * D;
+      q.ldy = D;
+      q.seq_len = 1;
+      q.part = part;
+      rc = cnt > 64 ? launch_gemm(q, GEMV_PLAIN, st) : launch_gemv(q, GEMV_PLAIN, plan_gemv(cnt, D, n), st);
+      if (rc) return rc;
+      i0 = i1;
+    }
+    move_rows_kernel<true><<<ns, 256, 0, st>>>(ys, d, ns, scatter, eout);
+    if ((rc = check_launch("moe_experts scatter"))) return rc;
+  }
+  return AMLA_OK;
 }
 
 }  // extern "C"

@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
   // weight copies of one tile: row pairs i = 2*wave, 2*wave+1, every segment
   auto dma_tile = [&](int tile, int buf) {
     const int nt = min(tile, tile_end - 1) * 16;
-    const bool seg1 = (MODE == GEMV_QKVA) && nt >= p.n_split;
+    const bool seg1 = (MODE == GEMV_QKVA || p.w1) && nt >= p.n_split;
     const uint8_t *wb = (seg1 ? p.w1 : p.w0) + (size_t)(seg1 ? nt - p.n_split : nt) * p.K;
     uint8_t *tb = wbuf + buf * TILE_BYTES;
     for (int s = 0; s < nseg; ++s) {
@@ -257,7 +257,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
     // block scales of this wave's blocks through the scalar cache (constant
     // address space: the scales are never written here), so waiting for them
     // is not waiting for the weight copies in flight
-    const bool seg1 = (MODE == GEMV_QKVA) && nt >= p.n_split;
+    const bool seg1 = (MODE == GEMV_QKVA || p.w1) && nt >= p.n_split;
     const __attribute__((address_space(4))) float *srow =
         (const __attribute__((address_space(4))) float *)((seg1 ? p.s1 : p.s0) +
                                                           (size_t)((seg1 ? nt - p.n_split : nt) >> 7) * KB + kb_begin);
@@ -516,6 +516,8 @@ int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t 
     return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM: K=%d is too long for M=%d (more than %d K parts)", p0.K, p0.M,
                 GEMV_MAX_PARTS);
   if (pl.kparts > 1 && !p0.part) return fail(AMLA_EWORKSPACE, "skinny fp8 GEMM: missing partial-sum workspace");
+  if (p0.w1 && p0.n_split % 128)
+    return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM: the first weight segment must be a multiple of 128 rows");
   const int MT = p0.M <= 16 ? 1 : (p0.M <= 32 ? 2 : 4);
   if (MT == 1) launch_mt<1>(p0, mode, pl, st);
   else if (MT == 2) launch_mt<2>(p0, mode, pl, st);

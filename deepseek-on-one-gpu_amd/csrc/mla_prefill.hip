@@ -142,7 +142,7 @@ __global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p, bool s
   const int wn = wave & 1, wm = wave >> 1;
   const int j32 = lane & 31, hh = lane >> 5;
   const int n0 = blockIdx.x * G_BN, m0 = blockIdx.y * G_BM;
-  const bool seg1 = (MODE == GEMV_QKVA) && n0 >= p.n_split;
+  const bool seg1 = (MODE == GEMV_QKVA || p.w1) && n0 >= p.n_split;
   const uint8_t *W = seg1 ? p.w1 : p.w0;
   const float *S = seg1 ? p.s1 : p.s0;
   const int nl0 = seg1 ? n0 - p.n_split : n0;
@@ -318,8 +318,8 @@ size_t gemm_ws_bytes(int, int, int) { return 0; }
 int launch_gemm(const GemvParams &p, int mode, hipStream_t st) {
   if (p.K % 128 || p.N % 4) return fail(AMLA_EUNSUPPORTED, "fp8 GEMM needs K %% 128 == 0 and N %% 4 == 0");
   if (p.ldx % 8) return fail(AMLA_EUNSUPPORTED, "fp8 GEMM needs 16-byte aligned activation rows");
-  if (mode == GEMV_QKVA && p.n_split % G_BN)
-    return fail(AMLA_EUNSUPPORTED, "fp8 GEMM: q_lora must be a multiple of 256");
+  if ((mode == GEMV_QKVA || p.w1) && p.n_split % G_BN)
+    return fail(AMLA_EUNSUPPORTED, "fp8 GEMM: the first weight segment must be a multiple of 256 rows");
   static bool attr_set[4] = {false, false, false, false};  // dynamic LDS above 64 KB, once per mode
   const void *fn = mode == GEMV_PLAIN  ? (const void *)gemm_kernel<GEMV_PLAIN>
                    : mode == GEMV_RESID ? (const void *)gemm_kernel<GEMV_RESID>

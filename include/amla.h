@@ -172,6 +172,24 @@ int amla_moe_route(const void *hidden, int64_t m, int64_t d, const void *gate_we
                    void *workspace, size_t workspace_bytes, void *stream);
 size_t amla_moe_route_workspace_bytes(int64_t m, int64_t n_experts);
 
+/* Replaces the routed-expert loop of moe_block, inference/forward.py:139-151
+ * (expert_ffn of every (token, k) pair), with the experts already on the device:
+ *   expert_out[t, k] = swiglu(hidden[t], expert indices[t, k])
+ * indices (m, top_k) int64 in HOST memory (the reference also brings them to
+ * the host); gate_w .. down_s: HOST arrays of n_experts device pointers (only
+ * the chosen experts' entries are read; others may be NULL), the weights of
+ * expert e laid out as for amla_swiglu with intermediate size n_inter.  Each
+ * chosen expert runs once over all of its tokens (gather, [gate | up] in one
+ * skinny GEMM, silu * up, down, scatter).  hidden (m, d) bf16, expert_out
+ * (m, top_k, d) bf16; d % 128 == 0, n_inter % 256 == 0, top_k <= 64.
+ * Workspace of amla_moe_experts_workspace_bytes(m, d, top_k, n_inter) bytes. */
+int amla_moe_experts(const void *hidden, int64_t m, int64_t d, int top_k, const int64_t *indices, int64_t n_inter,
+                     int64_t n_experts, const void *const *gate_w, const float *const *gate_s,
+                     const void *const *up_w, const float *const *up_s, const void *const *down_w,
+                     const float *const *down_s, void *expert_out, void *workspace, size_t workspace_bytes,
+                     void *stream);
+size_t amla_moe_experts_workspace_bytes(int64_t m, int64_t d, int top_k, int64_t n_inter);
+
 /* The combine of moe_block, inference/forward.py:138-153, for m tokens:
  *   acc = 0;  for k in 0..top_k-1:  acc = bf16( acc + bf16( bf16(w[t, k]) * expert_out[t, k] ) )
  *   out[t] = bf16( shared_out[t] + bf16( acc * routed_scaling_factor ) )

@@ -1,5 +1,6 @@
 """GPU parity of the FFN / MoE entry points (swiglu, route, moe combine, moe_block)
 against the CPU oracle (oracle/ref_ffn.py)."""
+import ctypes
 from types import SimpleNamespace
 
 import pytest
@@ -154,7 +155,7 @@ def test_moe_combine_bit_exact():
 @pytest.mark.parametrize("E,G,TG,K,B,S", [(16, 4, 2, 4, 2, 3), (256, 8, 4, 8, 8, 1)])
 def test_moe_block(E, G, TG, K, B, S):
     print(f"[case] moe_block E={E} K={K} B={B} S={S}", flush=True)
-    d, i = 256, 128
+    d, i = 256, 256
     cfg = _cfg(E, G, TG, K)
     h = _x((B, S, d), f"moe{E}")
     gw = synth.randn((E, d), synth.seed_of("moe-router", E), 0.1).to(torch.bfloat16)
@@ -168,3 +169,37 @@ def test_moe_block(E, G, TG, K, B, S):
     assert torch.equal(idx.cpu(), ridx), "routing differs from the oracle on this seed"
     want = F.moe_block(h, gw, shared, lambda e: table[e], cfg)
     assert_parity(got, want, f"moe_block E={E}")
+
+
+@pytest.mark.parametrize("E,K,m", [(2, 1, 300), (6, 3, 150), (256, 8, 8)])
+def test_moe_experts_vs_expert_ffn(E, K, m):
+    """amla_moe_experts (chunks of 512 slots; large expert groups take the GEMM path) against
+    expert_ffn of every (token, k) pair."""
+    print(f"[case] moe_experts E={E} K={K} m={m}", flush=True)
+    d, i = 256, 256
+    h = _x((m, d), f"mx{E}{K}")
+    g = torch.Generator().manual_seed(E * 1000 + K)
+    idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(m)])   # distinct experts per token
+    table = {e: _mlp(d, i, f"mx-expert{e}") for e in range(E)}
+    dev_table = {e: _dev(v) for e, v in table.items()}
+    ptrs = [(ctypes.c_void_p * E)() for _ in range(6)]
+    for e in range(E):
+        for j, key in enumerate(("gate_proj", "up_proj", "down_proj")):
+            ptrs[2 * j][e] = dev_table[e][key][0].data_ptr()
+            ptrs[2 * j + 1][e] = dev_table[e][key][1].data_ptr()
+    hd = h.to(DEV)
+    eout = torch.empty(m, K, d, dtype=torch.bfloat16, device=DEV)
+    need = ops.lib().amla_moe_experts_workspace_bytes(m, d, K, i)
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    idx64 = idx.to(torch.int64).contiguous()
+    ops.check(ops.lib().amla_moe_experts(hd.data_ptr(), m, d, K, idx64.data_ptr(), i, E,
+                                         *[ctypes.cast(t, ctypes.c_void_p) for t in ptrs], eout.data_ptr(),
+                                         ws.data_ptr(), need, ops._stream_ptr(hd)), "moe_experts")
+    torch.cuda.synchronize()
+    want = torch.empty(m, K, d, dtype=torch.bfloat16)
+    for e in range(E):
+        sel = (idx == e).nonzero()
+        if len(sel):
+            y = F.expert_ffn(h[sel[:, 0]], table[e])
+            want[sel[:, 0], sel[:, 1]] = y
+    assert_parity(eout, want, f"moe_experts E={E} K={K} m={m}")
