@@ -422,14 +422,17 @@ def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: d
         return out
     idx_host = idx.reshape(m, top_k).cpu().contiguous()
     tables = [(ctypes.c_void_p * E)() for _ in range(6)]
+    dev = hidden.device
     n_inter = None
     keep = []
     for e in torch.unique(idx_host).tolist():
         ew = get(int(e))
         for j, key in enumerate(("gate_proj", "up_proj", "down_proj")):
             wt, sc = ew[key]
-            _need(wt, f"expert {e} {key}", FP8, hidden.device)
-            _need(sc, f"expert {e} {key} scale", torch.float32, hidden.device)
+            if wt.dtype != FP8 or sc.dtype != torch.float32 or wt.device != dev or sc.device != dev or \
+                    not (wt.is_contiguous() and sc.is_contiguous()):
+                raise ValueError(f"moe_block: expert {e} {key} must be contiguous e4m3fn weights with fp32 "
+                                 f"scales on {dev}")
             tables[2 * j][e] = wt.data_ptr()
             tables[2 * j + 1][e] = sc.data_ptr()
             keep.append((wt, sc))

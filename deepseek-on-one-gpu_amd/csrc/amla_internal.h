@@ -69,6 +69,27 @@ int launch_gemv(const GemvParams &p, int mode, const GemvPlan &plan, hipStream_t
 // inference/ops.py:12) into p.y; one workgroup per row.
 int launch_qkva_finish_norm(const GemvParams &p, int kparts, const uint16_t *gamma, float eps, hipStream_t stream);
 
+// Independent skinny GEMMs of one shape in one launch (GEMV_PLAIN): the
+// fields below replace those of the shared GemvParams for group g.
+constexpr int GEMV_MAX_GROUPS = 32;
+struct GemvGroup {
+  const uint16_t *x;
+  const uint8_t *w0;
+  const float *s0;
+  const uint8_t *w1;
+  const float *s1;
+  uint16_t *y;
+  float *part;  // plan.kparts * M * N fp32 of this group when plan.kparts > 1
+  int M, pad;
+};
+struct GemvGroups {
+  int n;      // groups in use
+  int units;  // workgroups per group (set by launch_gemv_grouped)
+  GemvGroup g[GEMV_MAX_GROUPS];
+};
+// plan: plan_gemv_grouped(max M of the groups, N, K) (or plan_gemv).
+GemvPlan plan_gemv_grouped(int M, int N, int K);
+int launch_gemv_grouped(const GemvParams &p, GemvGroups groups, const GemvPlan &plan, hipStream_t stream);
 // Large-M fp8 GEMM with the same modes (M > 64).
 size_t gemm_ws_bytes(int M, int N, int K);
 int launch_gemm(const GemvParams &p, int mode, hipStream_t stream);

@@ -155,21 +155,24 @@ namespace amla {
 
 // ---------------------------------------------------------------- routing
 
-// logits[m, e] = sum_k f32(hidden[m, k]) * f32(gate_w[e, k]) for a 16-token x
-// 16-expert tile per workgroup; the four waves take interleaved 32-wide K
-// steps and add their partial tiles in wave order through LDS.
+// Partial logits part[z][m, e] = sum over the K steps of split z of
+// f32(hidden[m, k]) * f32(gate_w[e, k]) for a 16-token x 16-expert tile per
+// workgroup; the four waves take interleaved 32-wide K steps and add their
+// partial tiles in wave order through LDS.  route_select adds the splits in
+// order.
 __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t *__restrict__ hidden,
                                                            const uint16_t *__restrict__ gw, int M, int D, int E,
-                                                           float *__restrict__ logits) {
+                                                           float *__restrict__ part) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int e0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  const int e0 = blockIdx.x * 16, m0 = blockIdx.y * 16, z = blockIdx.z, nz = gridDim.z;
+  float *logits = part + (size_t)z * M * E;
   const int r = lane & 15, kq = lane >> 4;
   const uint16_t *hp = hidden + (size_t)min(m0 + r, M - 1) * D + 8 * kq;
   const uint16_t *wp = gw + (size_t)min(e0 + r, E - 1) * D + 8 * kq;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int steps = D / 32;
 #pragma unroll 4
-  for (int ks = wave; ks < steps; ks += 4)
+  for (int ks = wave + 4 * z; ks < steps; ks += 4 * nz)
     acc = mfma16(as_bf16x8(ldg16(hp + ks * 32)), as_bf16x8(ldg16(wp + ks * 32)), acc);
   __shared__ f32x4 red[4][64];
   red[wave][lane] = acc;
@@ -194,15 +197,18 @@ constexpr int ROUTE_MAX_E = 1024;  // experts per token handled by one wave (16 
 // their maximum score and keep topk_group of them; take the top_k experts of
 // the kept groups by score (ties to the lower index); weights are the scores,
 // divided by (sum + 1e-9) when norm is set.
-__global__ __launch_bounds__(64) void route_select_kernel(const float *__restrict__ logits, int E, int n_group,
-                                                          int topk_group, int top_k, int norm,
+__global__ __launch_bounds__(64) void route_select_kernel(const float *__restrict__ part, int M, int ksplit, int E,
+                                                          int n_group, int topk_group, int top_k, int norm,
                                                           int64_t *__restrict__ idx_out, float *__restrict__ w_out) {
   __shared__ float sc[ROUTE_MAX_E];
   __shared__ float gmax[64];
   __shared__ int keep[64];
   const int lane = threadIdx.x, m = blockIdx.x;
-  const float *lg = logits + (size_t)m * E;
-  for (int e = lane; e < E; e += 64) sc[e] = 1.f / (1.f + expf(-lg[e]));
+  for (int e = lane; e < E; e += 64) {
+    float l = part[(size_t)m * E + e];
+    for (int z = 1; z < ksplit; ++z) l += part[((size_t)z * M + m) * E + e];
+    sc[e] = 1.f / (1.f + expf(-l));
+  }
   __syncthreads();
   const int gs = E / n_group;
   if (lane < n_group) {
@@ -277,9 +283,15 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__rest
 
 extern "C" {
 
+// K splits of the router logits: about 128 workgroups for decode-sized batches
+static int route_ksplit(int64_t m, int64_t n_experts) {
+  const int64_t tiles = ((n_experts + 15) / 16) * ((m + 15) / 16);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(8, 128 / std::max<int64_t>(tiles, 1)));
+}
+
 size_t amla_moe_route_workspace_bytes(int64_t m, int64_t n_experts) {
   if (m <= 0 || n_experts <= 0) return 0;
-  return align_up((size_t)m * n_experts * 4, 256);
+  return align_up((size_t)route_ksplit(m, n_experts) * m * n_experts * 4, 256);
 }
 
 int amla_moe_route(const void *hidden, int64_t m, int64_t d, const void *gate_weight, int64_t n_experts,
@@ -302,13 +314,14 @@ int amla_moe_route(const void *hidden, int64_t m, int64_t d, const void *gate_we
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
     return fail(AMLA_EWORKSPACE, "moe_route: needs %zu bytes of 16-byte aligned workspace", need);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  float *logits = static_cast<float *>(workspace);
-  route_logits_kernel<<<dim3((unsigned)((n_experts + 15) / 16), (unsigned)((m + 15) / 16)), 256, 0, st>>>(
-      static_cast<const uint16_t *>(hidden), static_cast<const uint16_t *>(gate_weight), (int)m, (int)d,
-      (int)n_experts, logits);
+  float *part = static_cast<float *>(workspace);
+  const int ks = route_ksplit(m, n_experts);
+  route_logits_kernel<<<dim3((unsigned)((n_experts + 15) / 16), (unsigned)((m + 15) / 16), (unsigned)ks), 256, 0,
+                        st>>>(static_cast<const uint16_t *>(hidden), static_cast<const uint16_t *>(gate_weight),
+                              (int)m, (int)d, (int)n_experts, part);
   int rc;
   if ((rc = check_launch("moe_route logits"))) return rc;
-  route_select_kernel<<<dim3((unsigned)m), 64, 0, st>>>(logits, (int)n_experts, n_group, topk_group, top_k,
+  route_select_kernel<<<dim3((unsigned)m), 64, 0, st>>>(part, (int)m, ks, (int)n_experts, n_group, topk_group, top_k,
                                                         norm_topk_prob, indices, weights);
   return check_launch("moe_route select");
 }
@@ -376,19 +389,22 @@ static MoeLayout moe_layout(int64_t m, int64_t d, int top_k, int64_t n) {
   MoeLayout L;
   L.chunk_tokens = (int)std::min<int64_t>(m, MOE_MAX_SLOTS / top_k);
   const size_t slots = (size_t)L.chunk_tokens * top_k;
-  const int mg = std::min(L.chunk_tokens, 64);  // tokens of one expert on the skinny path
+  const int mg = std::min(L.chunk_tokens, 64);  // largest expert group on the skinny path
   size_t off = 0;
   L.xs = off;
   off = align_up(off + slots * d * 2, 256);
   L.ys = off;
   off = align_up(off + slots * d * 2, 256);
   L.gu = off;
-  off = align_up(off + (size_t)L.chunk_tokens * 2 * n * 2, 256);
+  off = align_up(off + slots * 2 * n * 2, 256);
   L.h = off;
-  off = align_up(off + (size_t)L.chunk_tokens * n * 2, 256);
+  off = align_up(off + slots * n * 2, 256);
   L.part = off;
-  off = align_up(off + std::max(plan_gemv(mg, (int)(2 * n), (int)d).part_bytes, plan_gemv(mg, (int)d, (int)n).part_bytes),
-                 256);
+  // partial sums of every group of one grouped launch, each sized for its own rows
+  const GemvPlan a = plan_gemv(mg, (int)(2 * n), (int)d), b = plan_gemv(mg, (int)d, (int)n);
+  const size_t pa = a.kparts > 1 ? (size_t)a.kparts * slots * 2 * n * 4 : 0;
+  const size_t pb = b.kparts > 1 ? (size_t)b.kparts * slots * d * 4 : 0;
+  off = align_up(off + std::max(pa, pb), 256);
   L.total = off;
   return L;
 }
@@ -452,47 +468,102 @@ int amla_moe_experts(const void *hidden, int64_t m, int64_t d, int top_k, const 
     }
     move_rows_kernel<false><<<ns, 256, 0, st>>>(hid, d, ns, gather, xs);
     if ((rc = check_launch("moe_experts gather"))) return rc;
-    for (int i0 = 0; i0 < ns;) {
+    // runs of one expert: [run_begin[r], run_begin[r + 1])
+    std::vector<int> run_begin;
+    for (int i = 0; i < ns; ++i)
+      if (i == 0 || ix[order[i]] != ix[order[i - 1]]) run_begin.push_back(i);
+    run_begin.push_back(ns);
+    const int nruns = (int)run_begin.size() - 1;
+    int max_small = 0;
+    for (int r = 0; r < nruns; ++r)
+      if (run_begin[r + 1] - run_begin[r] <= 64) max_small = std::max(max_small, run_begin[r + 1] - run_begin[r]);
+    GemvParams pg = {};  // [gate | up] x (cnt, D) -> gu (cnt, 2n)
+    pg.ldx = D;
+    pg.N = 2 * n;
+    pg.K = D;
+    pg.n_split = n;
+    pg.ldy = 2 * n;
+    pg.seq_len = 1;
+    GemvParams pd = {};  // down h (cnt, n) -> ys (cnt, D)
+    pd.ldx = n;
+    pd.N = D;
+    pd.K = n;
+    pd.n_split = D;
+    pd.ldy = D;
+    pd.seq_len = 1;
+    const GemvPlan plan_g = plan_gemv_grouped(std::max(max_small, 1), 2 * n, D);
+    const GemvPlan plan_d = plan_gemv_grouped(std::max(max_small, 1), D, n);
+    // experts with more than 64 of these tokens: one large-M GEMM each
+    for (int r = 0; r < nruns; ++r) {
+      const int i0 = run_begin[r], cnt = run_begin[r + 1] - i0;
+      if (cnt <= 64) continue;
       const int64_t e = ix[order[i0]];
-      int i1 = i0 + 1;
-      while (i1 < ns && ix[order[i1]] == e) ++i1;
-      const int cnt = i1 - i0;
-      GemvParams p = {};
+      GemvParams p = pg;
       p.x = xs + (size_t)i0 * D;
       p.M = cnt;
-      p.ldx = D;
       p.w0 = static_cast<const uint8_t *>(gate_w[e]);
       p.s0 = gate_s[e];
       p.w1 = static_cast<const uint8_t *>(up_w[e]);
       p.s1 = up_s[e];
-      p.N = 2 * n;
-      p.K = D;
-      p.n_split = n;
-      p.y = gu;
-      p.ldy = 2 * n;
-      p.seq_len = 1;
-      p.part = part;
-      rc = cnt > 64 ? launch_gemm(p, GEMV_PLAIN, st) : launch_gemv(p, GEMV_PLAIN, plan_gemv(cnt, 2 * n, D), st);
-      if (rc) return rc;
-      silu_mul_rows_kernel<<<dim3((unsigned)std::max(1, std::min(n / 8 / 256, 16)), (unsigned)cnt), 256, 0, st>>>(
-          gu, cnt, n, hb);
-      if ((rc = check_launch("moe_experts silu_mul"))) return rc;
-      GemvParams q = {};
-      q.x = hb;
+      p.y = gu + (size_t)i0 * 2 * n;
+      if ((rc = launch_gemm(p, GEMV_PLAIN, st))) return rc;
+    }
+    // the others: grouped skinny GEMMs, GEMV_MAX_GROUPS experts per launch
+    for (int pass = 0; pass < 2; ++pass) {
+      if (pass == 1) {
+        // silu * up over every row of [gate | up]
+        silu_mul_rows_kernel<<<dim3((unsigned)std::max(1, std::min(n / 8 / 256, 16)), (unsigned)ns), 256, 0, st>>>(
+            gu, ns, n, hb);
+        if ((rc = check_launch("moe_experts silu_mul"))) return rc;
+      }
+      const GemvPlan &pl = pass == 0 ? plan_g : plan_d;
+      const GemvParams &base = pass == 0 ? pg : pd;
+      GemvGroups gr;
+      gr.n = 0;
+      gr.units = 0;
+      for (int r = 0; r <= nruns; ++r) {
+        const bool flush = r == nruns || gr.n == GEMV_MAX_GROUPS;
+        if (flush && gr.n) {
+          if ((rc = launch_gemv_grouped(base, gr, pl, st))) return rc;
+          gr.n = 0;
+        }
+        if (r == nruns) break;
+        const int i0 = run_begin[r], cnt = run_begin[r + 1] - i0;
+        if (cnt > 64) continue;
+        const int64_t e = ix[order[i0]];
+        GemvGroup &g = gr.g[gr.n++];
+        g.M = cnt;
+        g.pad = 0;
+        if (pass == 0) {
+          g.x = xs + (size_t)i0 * D;
+          g.w0 = static_cast<const uint8_t *>(gate_w[e]);
+          g.s0 = gate_s[e];
+          g.w1 = static_cast<const uint8_t *>(up_w[e]);
+          g.s1 = up_s[e];
+          g.y = gu + (size_t)i0 * 2 * n;
+          g.part = pl.kparts > 1 ? part + (size_t)pl.kparts * i0 * 2 * n : nullptr;
+        } else {
+          g.x = hb + (size_t)i0 * n;
+          g.w0 = static_cast<const uint8_t *>(down_w[e]);
+          g.s0 = down_s[e];
+          g.w1 = nullptr;
+          g.s1 = nullptr;
+          g.y = ys + (size_t)i0 * D;
+          g.part = pl.kparts > 1 ? part + (size_t)pl.kparts * i0 * D : nullptr;
+        }
+      }
+    }
+    for (int r = 0; r < nruns; ++r) {
+      const int i0 = run_begin[r], cnt = run_begin[r + 1] - i0;
+      if (cnt <= 64) continue;
+      const int64_t e = ix[order[i0]];
+      GemvParams q = pd;
+      q.x = hb + (size_t)i0 * n;
       q.M = cnt;
-      q.ldx = n;
       q.w0 = static_cast<const uint8_t *>(down_w[e]);
       q.s0 = down_s[e];
-      q.N = D;
-      q.K = n;
-      q.n_split = D;
       q.y = ys + (size_t)i0 * D;
-      q.ldy = D;
-      q.seq_len = 1;
-      q.part = part;
-      rc = cnt > 64 ? launch_gemm(q, GEMV_PLAIN, st) : launch_gemv(q, GEMV_PLAIN, plan_gemv(cnt, D, n), st);
-      if (rc) return rc;
-      i0 = i1;
+      if ((rc = launch_gemm(q, GEMV_PLAIN, st))) return rc;
     }
     move_rows_kernel<true><<<ns, 256, 0, st>>>(ys, d, ns, scatter, eout);
     if ((rc = check_launch("moe_experts scatter"))) return rc;

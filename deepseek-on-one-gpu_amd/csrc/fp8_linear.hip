@@ -20,6 +20,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
+
 #include <string>
 
 #include "amla_common.h"
@@ -172,7 +174,7 @@ __host__ __device__ inline int gemv_kpb4(int kpb) { return (kpb + 3) & ~3; }
 __host__ __device__ inline int gemv_xrow(int kpb) { return kpb * 256 + 16; }
 
 template <int MT, int MODE>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kparts, int kpb) {
+AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int kpb) {
   constexpr bool XREG = MT == 1;
   constexpr int NBUF = gemv_nbuf(MT);
   const int tid = threadIdx.x;
@@ -180,8 +182,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
   const int li = lane & 15, lg = lane >> 4;
   const int KB = p.K >> 7;
   const int ntiles = p.N >> 4;
-  const int part = blockIdx.x % kparts;
-  const int tile_begin = (blockIdx.x / kparts) * rg;
+  const int part = unit % kparts;
+  const int tile_begin = (unit / kparts) * rg;
   const int tile_end = min(tile_begin + rg, ntiles);
   const int kb_begin = part * kpb;
   const int nbp = min(kpb, KB - kb_begin);  // blocks of this part
@@ -351,6 +353,29 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last trips' (unused) copies land before exit
 }
 
+template <int MT, int MODE>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kparts, int kpb) {
+  gemv_body<MT, MODE>(p, blockIdx.x, rg, kparts, kpb);
+}
+
+// Several independent skinny GEMMs of one shape (N, K) in one launch: group g
+// takes workgroups [g * units, (g + 1) * units) with its own x, weights, M,
+// output and partial-sum buffer (routed experts of a MoE layer).
+template <int MT>
+__global__ __launch_bounds__(256) void gemv_grouped_kernel(GemvParams p, GemvGroups gr, int rg, int kparts, int kpb) {
+  const int g = blockIdx.x / gr.units;
+  GemvParams q = p;
+  q.x = gr.g[g].x;
+  q.w0 = gr.g[g].w0;
+  q.s0 = gr.g[g].s0;
+  q.w1 = gr.g[g].w1;
+  q.s1 = gr.g[g].s1;
+  q.y = gr.g[g].y;
+  q.part = gr.g[g].part;
+  q.M = gr.g[g].M;
+  gemv_body<MT, GEMV_PLAIN>(q, blockIdx.x % gr.units, rg, kparts, kpb);
+}
+
 size_t gemv_lds_bytes(int M, int MT, int kpb, int rg) {
   return (size_t)gemv_nbuf(MT) * 16 * gemv_kpb4(kpb) * 128 + (MT == 1 ? 0 : (size_t)M * gemv_xrow(kpb)) +
          2 * 4 * MT * 64 * 16 + (size_t)rg * MT * 64 * 16;
@@ -359,9 +384,8 @@ size_t gemv_lds_bytes(int M, int MT, int kpb, int rg) {
 // Sums the K parts of gemv_kernel in part order and applies the epilogue.
 // All parts are loaded before the first add (independent loads in flight).
 template <int MODE>
-__global__ __launch_bounds__(64) void gemv_finish(GemvParams p, int kparts) {
+AMLA_DEV void gemv_finish_body(const GemvParams &p, int64_t i, int kparts) {
   const int64_t total = (int64_t)p.M * (p.N >> 2);
-  const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
   if (i >= total) return;
   const int m = (int)(i / (p.N >> 2));
   const int n = (int)(i % (p.N >> 2)) * 4;
@@ -374,6 +398,21 @@ __global__ __launch_bounds__(64) void gemv_finish(GemvParams p, int kparts) {
   for (int q = 1; q < GEMV_MAX_PARTS; ++q)
     if (q < kparts) s += v[q];
   store4<MODE>(p, m, n, s);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(64) void gemv_finish(GemvParams p, int kparts) {
+  gemv_finish_body<MODE>(p, (int64_t)blockIdx.x * 64 + threadIdx.x, kparts);
+}
+
+// gemv_finish for the groups of gemv_grouped_kernel: gr.units blocks per group.
+__global__ __launch_bounds__(64) void gemv_finish_grouped(GemvParams p, GemvGroups gr, int kparts) {
+  const int g = blockIdx.x / gr.units;
+  GemvParams q = p;
+  q.y = gr.g[g].y;
+  q.part = gr.g[g].part;
+  q.M = gr.g[g].M;
+  gemv_finish_body<GEMV_PLAIN>(q, (int64_t)(blockIdx.x % gr.units) * 64 + threadIdx.x, kparts);
 }
 
 // One workgroup per row m: sums the K parts of every output of the row in
@@ -486,6 +525,22 @@ GemvPlan plan_gemv(int M, int N, int K) {
   return pl;
 }
 
+GemvPlan plan_gemv_grouped(int M, int N, int K) {
+  // many groups fill the machine by themselves: take the longest row run per
+  // workgroup the LDS allows (fewer, longer weight streams)
+  GemvPlan pl = plan_gemv(M, N, K);
+  const int MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  const int tiles = N / 16;
+  int rg = std::min(GEMV_MAX_RG, tiles);
+  while (rg > pl.rg && gemv_lds_bytes(M, MT, pl.kpb, rg) > 160 * 1024) --rg;
+  if (rg > pl.rg) {
+    pl.rg = rg;
+    pl.groups = ((tiles + rg - 1) / rg) * pl.kparts;
+    pl.lds = gemv_lds_bytes(M, MT, pl.kpb, rg);
+  }
+  return pl;
+}
+
 template <int MT, int MODE>
 static int launch_cfg(const GemvParams &p, const GemvPlan &pl, hipStream_t st) {
   static bool attr_set = false;  // raise the dynamic LDS limit once per process
@@ -533,6 +588,42 @@ int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t 
     }
   }
   return check_launch("fp8 skinny GEMM");
+}
+
+template <int MT>
+static void launch_grouped_mt(const GemvParams &p, const GemvGroups &gr, const GemvPlan &pl, hipStream_t st) {
+  static bool attr_set = false;  // raise the dynamic LDS limit once per process
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void *)gemv_grouped_kernel<MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    attr_set = true;
+  }
+  gemv_grouped_kernel<MT><<<dim3((unsigned)(gr.n * gr.units)), 256, pl.lds, st>>>(p, gr, pl.rg, pl.kparts, pl.kpb);
+}
+
+int launch_gemv_grouped(const GemvParams &p, GemvGroups gr, const GemvPlan &pl, hipStream_t st) {
+  if (gr.n < 1 || gr.n > GEMV_MAX_GROUPS) return fail(AMLA_EINVAL, "grouped skinny GEMM: %d groups", gr.n);
+  int max_m = 0;
+  for (int g = 0; g < gr.n; ++g) {
+    if (gr.g[g].M < 1 || gr.g[g].M > 64) return fail(AMLA_EINVAL, "grouped skinny GEMM: M=%d", gr.g[g].M);
+    if (pl.kparts > 1 && !gr.g[g].part) return fail(AMLA_EWORKSPACE, "grouped skinny GEMM: missing partial sums");
+    max_m = std::max(max_m, gr.g[g].M);
+  }
+  if (p.N % 16 || p.K % 128 || pl.kparts > GEMV_MAX_PARTS || (p.w1 && p.n_split % 128))
+    return fail(AMLA_EUNSUPPORTED, "grouped skinny GEMM: unsupported shape N=%d K=%d", p.N, p.K);
+  if (gemv_lds_bytes(max_m, max_m <= 16 ? 1 : (max_m <= 32 ? 2 : 4), pl.kpb, pl.rg) > pl.lds)
+    return fail(AMLA_EINVAL, "grouped skinny GEMM: plan for a smaller M");
+  gr.units = pl.groups;
+  const int MT = max_m <= 16 ? 1 : (max_m <= 32 ? 2 : 4);
+  if (MT == 1) launch_grouped_mt<1>(p, gr, pl, st);
+  else if (MT == 2) launch_grouped_mt<2>(p, gr, pl, st);
+  else launch_grouped_mt<4>(p, gr, pl, st);
+  if (pl.kparts > 1) {
+    GemvGroups fr = gr;
+    fr.units = (int)(((int64_t)max_m * (p.N / 4) + 63) / 64);
+    gemv_finish_grouped<<<dim3((unsigned)(fr.n * fr.units)), 64, 0, st>>>(p, fr, pl.kparts);
+  }
+  return check_launch("grouped fp8 skinny GEMM");
 }
 
 // ---------------------------------------------------------------- rms_norm
