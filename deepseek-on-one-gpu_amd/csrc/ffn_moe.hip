@@ -52,6 +52,23 @@ static int launch_silu_mul(const uint16_t *g, const uint16_t *u, int64_t n, uint
   return check_launch("silu_mul");
 }
 
+// h[r, j] = bf16( bf16(silu(gu[r, j])) * gu[r, n + j] ) for rows r of [gate | up]
+__global__ __launch_bounds__(256) void silu_mul_rows_kernel(const uint16_t *__restrict__ gu, int rows, int n,
+                                                            uint16_t *__restrict__ h) {
+  for (int r = blockIdx.y; r < rows; r += gridDim.y) {
+    const uint16_t *g = gu + (size_t)r * 2 * n, *u = g + n;
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < n / 8; c += gridDim.x * blockDim.x) {
+      const u32x4 gv = *reinterpret_cast<const u32x4 *>(g + c * 8);
+      const u32x4 uv = *reinterpret_cast<const u32x4 *>(u + c * 8);
+      u32x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o[i] = pack_bf16(silu_bf16(lo_bf(gv[i])) * lo_bf(uv[i]), silu_bf16(hi_bf(gv[i])) * hi_bf(uv[i]));
+      *reinterpret_cast<u32x4 *>(h + (size_t)r * n + c * 8) = o;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- swiglu
 
 // One fp8 linear (y = bf16(x W^T)), skinny or large-M path.
@@ -76,19 +93,20 @@ static int fp8_linear_into(const uint16_t *x, int m, int k, const uint8_t *w, co
 }
 
 struct SwigluLayout {
-  size_t g, u, part, total;
+  size_t gu, h, part, total;
 };
 
+// [gate | up] rows (m, 2n), then h (m, n), then the K-part sums of the skinny path
 static SwigluLayout swiglu_layout(int64_t m, int64_t k, int64_t n) {
   SwigluLayout L;
   size_t off = 0;
-  L.g = off;
-  off = align_up(off + (size_t)m * n * 2, 256);
-  L.u = off;
+  L.gu = off;
+  off = align_up(off + (size_t)m * 2 * n * 2, 256);
+  L.h = off;
   off = align_up(off + (size_t)m * n * 2, 256);
   size_t part = 0;
   if (m <= 64 && m > 0)
-    part = std::max(plan_gemv((int)m, (int)n, (int)k).part_bytes, plan_gemv((int)m, (int)k, (int)n).part_bytes);
+    part = std::max(plan_gemv((int)m, (int)(2 * n), (int)k).part_bytes, plan_gemv((int)m, (int)k, (int)n).part_bytes);
   L.part = off;
   off = align_up(off + part, 256);
   L.total = off;
@@ -134,18 +152,51 @@ int amla_swiglu(const void *x, int64_t m, int64_t k, const void *gate_w, const f
     return fail(AMLA_EWORKSPACE, "swiglu: needs %zu bytes of 16-byte aligned workspace (got %zu)", L.total,
                 workspace ? workspace_bytes : (size_t)0);
   uint8_t *ws = static_cast<uint8_t *>(workspace);
-  uint16_t *g = reinterpret_cast<uint16_t *>(ws + L.g);
-  uint16_t *u = reinterpret_cast<uint16_t *>(ws + L.u);
+  uint16_t *gu = reinterpret_cast<uint16_t *>(ws + L.gu);
+  uint16_t *h = reinterpret_cast<uint16_t *>(ws + L.h);
   float *part = reinterpret_cast<float *>(ws + L.part);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const uint16_t *xb = static_cast<const uint16_t *>(x);
   int rc;
-  if ((rc = fp8_linear_into(xb, (int)m, (int)k, static_cast<const uint8_t *>(gate_w), gate_s, (int)n, g, part, st)))
-    return rc;
-  if ((rc = fp8_linear_into(xb, (int)m, (int)k, static_cast<const uint8_t *>(up_w), up_s, (int)n, u, part, st)))
-    return rc;
-  if ((rc = launch_silu_mul(g, u, m * n, g, st))) return rc;
-  return fp8_linear_into(g, (int)m, (int)n, static_cast<const uint8_t *>(down_w), down_s, (int)k,
+  // gate and up as one GEMM over the two stacked weights: rows (m, [gate | up])
+  GemvParams p = {};
+  p.x = static_cast<const uint16_t *>(x);
+  p.M = (int)m;
+  p.ldx = (int)k;
+  p.w0 = static_cast<const uint8_t *>(gate_w);
+  p.s0 = gate_s;
+  p.w1 = static_cast<const uint8_t *>(up_w);
+  p.s1 = up_s;
+  p.N = (int)(2 * n);
+  p.K = (int)k;
+  p.n_split = (int)n;
+  p.y = gu;
+  p.ldy = (int)(2 * n);
+  p.seq_len = 1;
+  p.part = part;
+  if (m > 64 && n % 256 == 0) rc = launch_gemm(p, GEMV_PLAIN, st);
+  else if (m > 64) {
+    // the large-M GEMM tiles 256 rows: a 128-row split point takes two launches
+    GemvParams a = p, b = p;
+    a.w1 = nullptr;
+    a.N = (int)n;
+    a.n_split = (int)n;
+    b.w0 = p.w1;
+    b.s0 = p.s1;
+    b.w1 = nullptr;
+    b.N = (int)n;
+    b.n_split = (int)n;
+    b.y = gu + n;
+    rc = launch_gemm(a, GEMV_PLAIN, st);
+    if (!rc) rc = launch_gemm(b, GEMV_PLAIN, st);
+  } else {
+    rc = launch_gemv(p, GEMV_PLAIN, plan_gemv((int)m, (int)(2 * n), (int)k), st);
+  }
+  if (rc) return rc;
+  silu_mul_rows_kernel<<<dim3((unsigned)std::max<int64_t>(1, std::min<int64_t>(n / 8 / 256, 16)),
+                              (unsigned)std::min<int64_t>(m, 65535)),
+                         256, 0, st>>>(gu, (int)m, (int)n, h);
+  if ((rc = check_launch("swiglu silu_mul"))) return rc;
+  return fp8_linear_into(h, (int)m, (int)n, static_cast<const uint8_t *>(down_w), down_s, (int)k,
                          static_cast<uint16_t *>(y), part, st);
 }
 
@@ -361,23 +412,6 @@ __global__ __launch_bounds__(256) void move_rows_kernel(const uint16_t *__restri
   uint16_t *t = dst + (size_t)(SCATTER ? list.row[i] : i) * d;
   for (int64_t c = threadIdx.x; c < d / 8; c += blockDim.x)
     *reinterpret_cast<u32x4 *>(t + c * 8) = *reinterpret_cast<const u32x4 *>(s + c * 8);
-}
-
-// h[r, j] = bf16( bf16(silu(gu[r, j])) * gu[r, n + j] ) for rows r of [gate | up]
-__global__ __launch_bounds__(256) void silu_mul_rows_kernel(const uint16_t *__restrict__ gu, int rows, int n,
-                                                            uint16_t *__restrict__ h) {
-  const int r = blockIdx.y;
-  if (r >= rows) return;
-  const uint16_t *g = gu + (size_t)r * 2 * n, *u = g + n;
-  for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < n / 8; c += gridDim.x * blockDim.x) {
-    const u32x4 gv = *reinterpret_cast<const u32x4 *>(g + c * 8);
-    const u32x4 uv = *reinterpret_cast<const u32x4 *>(u + c * 8);
-    u32x4 o;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      o[i] = pack_bf16(silu_bf16(lo_bf(gv[i])) * lo_bf(uv[i]), silu_bf16(hi_bf(gv[i])) * hi_bf(uv[i]));
-    *reinterpret_cast<u32x4 *>(h + (size_t)r * n + c * 8) = o;
-  }
 }
 
 struct MoeLayout {
