@@ -16,6 +16,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 from __future__ import annotations
 
 import argparse
+import gc
 import ctypes
 import json
 import os
@@ -191,12 +192,17 @@ def _fp8_on_device(n, k, gen, dev):
 def _time_eager(fn, reps):
     fn()
     torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(reps):
-        fn()
-    e.record()
-    torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()      # a collection of the 256-expert tables inside the timed loop costs tens of ms
+    try:
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+    finally:
+        gc.enable()
     return s.elapsed_time(e) / reps
 
 
