@@ -100,3 +100,56 @@ def test_python_api_rejects_cpu_tensors():
         ops.rms_norm(x, torch.ones(128, dtype=torch.bfloat16))
     with pytest.raises(ValueError):
         ops.fp8_linear(x, torch.zeros(16, 128).to(torch.float8_e4m3fn), torch.ones(1, 1))
+
+
+def test_ffn_moe_arguments_fail_before_launch():
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(256)
+    p0 = ctypes.cast(buf, ctypes.c_void_p).value
+    p = p0 + 16 - p0 % 16 if p0 % 16 else p0          # 16-byte aligned host address, never dereferenced
+    # swiglu
+    assert L.amla_swiglu(None, 1, 256, p, p, p, p, 256, p, p, p, p, 64, None) == -1
+    assert L.amla_swiglu(p, 1, 200, p, p, p, p, 256, p, p, p, p, 64, None) == -3     # k % 128
+    assert L.amla_swiglu(p, 1, 256, p, p, p, p, 256, p, p, p, p, 16, None) == -2     # workspace too small
+    assert b"workspace" in L.amla_last_error()
+    assert L.amla_swiglu_workspace_bytes(8, 7168, 2048) >= 8 * 3 * 2048 * 2
+    assert L.amla_silu_mul(None, p, 8, p, None) == -1
+    assert L.amla_silu_mul(p, p, -1, p, None) == -1
+    # route: config constraints
+    idx = ctypes.create_string_buffer(8 * 64)
+    w = ctypes.create_string_buffer(4 * 64)
+    ip, wp = ctypes.addressof(idx), ctypes.addressof(w)
+    assert L.amla_moe_route(None, 1, 256, p, 16, 4, 2, 4, 1, ip, wp, p, 1 << 20, None) == -1
+    assert L.amla_moe_route(p, 1, 256, p, 18, 4, 2, 4, 1, ip, wp, p, 1 << 20, None) == -1   # 18 % 4 != 0
+    assert L.amla_moe_route(p, 1, 256, p, 16, 4, 5, 4, 1, ip, wp, p, 1 << 20, None) == -1   # topk_group > n_group
+    assert L.amla_moe_route(p, 1, 256, p, 16, 4, 1, 5, 1, ip, wp, p, 1 << 20, None) == -1   # top_k > 1 group of 4
+    assert L.amla_moe_route(p, 1, 100, p, 16, 4, 2, 4, 1, ip, wp, p, 1 << 20, None) == -3   # d % 32
+    assert L.amla_moe_route(p, 1, 256, p, 16, 4, 2, 4, 1, ip, wp, p, 8, None) == -2          # workspace
+    assert L.amla_moe_route_workspace_bytes(8, 256) >= 8 * 256 * 4
+    # combine
+    assert L.amla_moe_combine(None, p, p, 1, 8, 256, 2.5, p, None) == -1
+    assert L.amla_moe_combine(p, p, p, 1, 0, 256, 2.5, p, None) == -1
+
+
+def test_moe_experts_checks_indices_and_tables_on_the_host():
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(256)
+    p0 = ctypes.cast(buf, ctypes.c_void_p).value
+    p = p0 + 16 - p0 % 16 if p0 % 16 else p0
+    E, m, top_k, d, n = 4, 2, 2, 256, 256
+    tables = [(ctypes.c_void_p * E)(*([p] * E)) for _ in range(6)]
+    args = lambda idx, ws=1 << 30: (p, m, d, top_k, ctypes.addressof(idx), n, E,
+                                    *[ctypes.cast(t, ctypes.c_void_p) for t in tables], p, p, ws, None)
+    bad = (ctypes.c_int64 * (m * top_k))(0, 1, 2, 4)          # expert 4 of 4
+    assert L.amla_moe_experts(*args(bad)) == -1
+    assert b"out of range" in L.amla_last_error()
+    ok = (ctypes.c_int64 * (m * top_k))(0, 1, 2, 3)
+    tables[4][2] = None                                         # expert 2 has no down weight
+    assert L.amla_moe_experts(*args(ok)) == -1
+    assert b"expert 2" in L.amla_last_error()
+    tables[4][2] = p
+    assert L.amla_moe_experts(*args(ok, ws=64)) == -2           # workspace too small
+    assert L.amla_moe_experts(p, m, 200, top_k, ctypes.addressof(ok), n, E,
+                              *[ctypes.cast(t, ctypes.c_void_p) for t in tables], p, p, 1 << 30, None) == -3
+    need = L.amla_moe_experts_workspace_bytes(m, d, top_k, n)
+    assert need >= 2 * m * top_k * d * 2
