@@ -505,14 +505,15 @@ GemvPlan plan_gemv(int M, int N, int K) {
   }
   pl.kpb = kpb;
   pl.kparts = (KB + kpb - 1) / kpb;
-  // tiles per unit: fewest rounds of 256 workgroups x tiles per unit, then
-  // the largest unit (fewer x stagings), within the LDS budget
+  // tiles per unit: fewest rounds of 256 workgroups x (tiles per unit + one
+  // tile's worth of per-workgroup start-up), then the largest unit (fewer x
+  // stagings), within the LDS budget
   int best_rg = 1;
   int64_t best_cost = INT64_MAX;
   for (int rg = 1; rg <= GEMV_MAX_RG; ++rg) {
     if (gemv_lds_bytes(M, MT, kpb, rg) > LDS_MAX) break;
     const int64_t units = (int64_t)((tiles + rg - 1) / rg) * pl.kparts;
-    const int64_t cost = ((units + 255) / 256) * rg;
+    const int64_t cost = ((units + 255) / 256) * (rg + 1);
     if (cost <= best_cost) {
       best_cost = cost;
       best_rg = rg;
