@@ -237,6 +237,24 @@ def ffn_extras(B, dev):
     return out
 
 
+def head_extras(B, dev):
+    """Output head at decode batch B: final norm + lm_head logits (129280 x 7168 bf16) and sampling."""
+    d, V = CFG.hidden_size, CFG.vocab_size
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(synth.seed_of("bench", "head") & 0x7FFFFFFF)
+    x = torch.randn(B, 1, d, generator=gen, device=dev).to(torch.bfloat16)
+    w = (torch.randn(V, d, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    g = torch.ones(d, dtype=torch.bfloat16, device=dev)
+    ms = _time_eager(lambda: ops.final_logits(x, g, w, CFG), 20)
+    out = {"lm_head_b8_us": round(ms * 1000, 2), "lm_head_b8_hbm_gbs": round(V * d * 2 / (ms * 1e-3) / 1e9, 1)}
+    logits = ops.final_logits(x, g, w, CFG).reshape(B, V)
+    out["sample_top_p_b8_us"] = round(_time_eager(lambda: ops.sample(logits, 0.7, 0.9, seed=1), 20) * 1000, 2)
+    out["sample_greedy_b8_us"] = round(_time_eager(lambda: ops.sample(logits, 0.0, 0.9), 20) * 1000, 2)
+    del w
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -322,6 +340,7 @@ def main():
         extras["prefill_frac_bf16_peak"] = round(extras["prefill_4096_tflops"] / BF16_PEAK_TFLOPS, 4)
         del hp, cp
         extras.update(ffn_extras(B, dev))
+        extras.update(head_extras(B, dev))
         log(f"[bench] extras: {extras}")
 
     result = {

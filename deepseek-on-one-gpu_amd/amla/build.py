@@ -15,7 +15,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(ROOT, "csrc")
 INCLUDE = os.path.join(os.path.dirname(ROOT), "include")
 LIB = os.path.join(PKG, "libamla.so")
-SOURCES = ["fp8_linear.hip", "mla_decode.hip", "mla_prefill.hip", "ffn_moe.hip"]
+SOURCES = ["fp8_linear.hip", "mla_decode.hip", "mla_prefill.hip", "ffn_moe.hip", "lm_head.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

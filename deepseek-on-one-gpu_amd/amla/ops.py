@@ -456,3 +456,59 @@ def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: d
                                  float(config.routed_scaling_factor), out.data_ptr(), stream), "moe_combine")
     del keep
     return out
+
+
+# ------------------------------------------------------------------ output head
+
+def lm_head_logits(hidden: torch.Tensor, lm_head_w: torch.Tensor) -> torch.Tensor:
+    """inference/forward.py:72: ``hidden.float() @ lm_head_w.float().T`` without the fp32 copy of
+    the weight: exact bf16 products summed in fp32.  Returns fp32 (*hidden.shape[:-1], vocab)."""
+    _need_cuda(hidden, "hidden")
+    if hidden.dtype != BF16:
+        raise TypeError(f"lm_head_logits: hidden must be bfloat16 (got {hidden.dtype})")
+    _need(lm_head_w, "lm_head_w", BF16, hidden.device)
+    n, k = lm_head_w.shape
+    if hidden.shape[-1] != k:
+        raise ValueError(f"lm_head_logits: hidden has {hidden.shape[-1]} features, lm_head_w expects {k}")
+    h2 = hidden.reshape(-1, k)
+    if not h2.is_contiguous() or h2.data_ptr() % 16:
+        h2 = h2.contiguous()
+    m = h2.shape[0]
+    out = torch.empty(m, n, dtype=torch.float32, device=hidden.device)
+    if m:
+        check(lib().amla_bf16_logits(h2.data_ptr(), m, k, lm_head_w.data_ptr(), n, out.data_ptr(), n,
+                                     _stream_ptr(hidden)), "lm_head_logits")
+    return out.view(*hidden.shape[:-1], n)
+
+
+def final_logits(hidden: torch.Tensor, final_norm: torch.Tensor, lm_head_w: torch.Tensor, config) -> torch.Tensor:
+    """inference/forward.py:67-72: final RMSNorm, then the lm_head projection in fp32."""
+    return lm_head_logits(rms_norm(hidden, final_norm, config.rms_norm_eps), lm_head_w)
+
+
+def sample(logits: torch.Tensor, temperature: float, top_p: float, *, seed: int | None = None) -> torch.Tensor:
+    """inference/engine.py:166-186: (B, vocab) fp32 logits -> (B,) int64 token ids.
+
+    temperature 0 is the argmax (ties to the lower index).  Otherwise nucleus
+    sampling with the reference's rule (softmax(logits / T), drop a token when the
+    mass strictly before it exceeds top_p, renormalise, draw one); the draw uses
+    a counter-based generator keyed by ``seed`` (default: drawn from torch's CPU
+    generator), so it follows the same distribution as torch.multinomial but not
+    its random stream.
+    """
+    _need_cuda(logits, "logits")
+    if logits.dtype != torch.float32 or logits.dim() != 2:
+        raise TypeError("sample: logits must be a (B, vocab) float32 tensor")
+    lg = logits if logits.stride(-1) == 1 else logits.contiguous()
+    B, n = lg.shape
+    out = torch.empty(B, dtype=torch.int64, device=logits.device)
+    if B == 0:
+        return out
+    if temperature == 0:
+        check(lib().amla_argmax(lg.data_ptr(), B, n, lg.stride(0), out.data_ptr(), _stream_ptr(logits)), "sample")
+        return out
+    if seed is None:
+        seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+    check(lib().amla_sample_top_p(lg.data_ptr(), B, n, lg.stride(0), float(temperature), float(top_p),
+                                  int(seed) & (2 ** 64 - 1), out.data_ptr(), _stream_ptr(logits)), "sample")
+    return out

@@ -197,6 +197,27 @@ size_t amla_moe_experts_workspace_bytes(int64_t m, int64_t d, int top_k, int64_t
 int amla_moe_combine(const void *shared_out, const void *expert_out, const float *weights, int64_t m, int top_k,
                      int64_t d, float routed_scaling_factor, void *out, void *stream);
 
+/* ---- output head ---- */
+
+/* The lm_head projection of forward.py:70-72 (hidden.float() @ lm_head_w.float().T):
+ *   logits[i, j] = sum_k f32(x[i, k]) * f32(weight[j, k])   (fp32 sums of exact products)
+ * x (m, k) bf16; weight (n, k) bf16 (k % 32 == 0); logits (m, n) fp32 with row stride ld_logits. */
+int amla_bf16_logits(const void *x, int64_t m, int64_t k, const void *weight, int64_t n, float *logits,
+                     int64_t ld_logits, void *stream);
+
+/* sample(logits, temperature=0, ...) of engine.py:166-173: out[r] = index of the largest
+ * logits[r, :] (ties to the lower index).  logits (rows, n) fp32, row stride ld; out int64. */
+int amla_argmax(const float *logits, int64_t rows, int64_t n, int64_t ld, int64_t *out, void *stream);
+
+/* sample(logits, temperature, top_p) of engine.py:166-186 for temperature > 0:
+ * p = softmax(logits / temperature); sorted by p descending, a token is dropped when the
+ * mass strictly before it exceeds top_p (tokens tied with the last kept one are all kept);
+ * one token is drawn from the renormalised kept p with a counter-based generator keyed
+ * by (seed, row).  Same distribution as the reference's torch.multinomial, not the same
+ * random stream. */
+int amla_sample_top_p(const float *logits, int64_t rows, int64_t n, int64_t ld, float temperature, float top_p,
+                      uint64_t seed, int64_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

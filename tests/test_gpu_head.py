@@ -1,0 +1,73 @@
+"""GPU parity of the output head (lm_head logits, greedy and nucleus sampling) against the
+CPU oracle (oracle/ref_head.py)."""
+import pytest
+import torch
+
+from oracle import ref_head as H
+from amla import ops, synth
+from amla.config import DeepSeekConfig
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+R1 = DeepSeekConfig()
+
+
+def test_lm_head_logits_r1():
+    print("[case] lm_head logits r1 B=8", flush=True)
+    d, V = R1.hidden_size, R1.vocab_size
+    h = synth.randn((8, 1, d), synth.seed_of("head", "h"), 1.0).to(torch.bfloat16)
+    g = synth.gamma(d, synth.seed_of("head", "g"))
+    w = synth.randn((V, d), synth.seed_of("head", "w"), 0.02).to(torch.bfloat16)
+    got = ops.final_logits(h.to(DEV), g.to(DEV), w.to(DEV), R1)
+    torch.cuda.synchronize()
+    want = H.lm_head_logits(h, g, w, R1.rms_norm_eps)
+    assert got.shape == want.shape and got.dtype == torch.float32
+    # fp32 sums of the same exact products in another order
+    torch.testing.assert_close(got.cpu(), want, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 64, 48), (37, 256, 1000), (300, 96, 160)])
+def test_bf16_logits_small(M, K, N):
+    x = synth.randn((M, K), synth.seed_of("hx", M, K), 1.0).to(torch.bfloat16)
+    w = synth.randn((N, K), synth.seed_of("hw", N, K), 0.5).to(torch.bfloat16)
+    got = ops.lm_head_logits(x.to(DEV), w.to(DEV)).cpu()
+    torch.testing.assert_close(got.double(), x.double() @ w.double().T, rtol=1e-5, atol=1e-5)
+
+
+def test_argmax_exact_with_ties():
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(6, 129280, generator=g)
+    logits[1, 500] = logits[1, 70000] = 100.0      # tie: lower index wins
+    logits[2] = 0.0                                 # all equal: index 0
+    logits[3, -1] = 50.0                            # last position
+    got = ops.sample(logits.to(DEV), 0.0, 0.9).cpu()
+    assert got.tolist() == H.greedy(logits).tolist()
+    assert got[1].item() == 500 and got[2].item() == 0 and got[3].item() == 129279
+
+
+def test_top_p_draws_from_the_nucleus():
+    g = torch.Generator().manual_seed(4)
+    for top_p, temp in ((0.0, 1.0), (0.5, 0.7), (0.9, 1.0), (0.99, 1.3)):
+        print(f"[case] top_p {top_p} T {temp}", flush=True)
+        logits = torch.randn(64, 5000, generator=g) * 2
+        kept, _ = H.nucleus(logits, temp, top_p)
+        got = ops.sample(logits.to(DEV), temp, top_p, seed=1234).cpu()
+        assert kept[torch.arange(64), got].all()
+        if top_p == 0.0:
+            assert got.tolist() == H.greedy(logits).tolist()
+
+
+def test_top_p_distribution():
+    # one row repeated: every row draws with its own counter, so the rows are independent samples
+    logits = torch.tensor([2.0, 1.5, 1.0, 0.5, 0.0, -0.5, -1.0, -3.0])
+    rows = 40000
+    lg = logits.repeat(rows, 1)
+    got = ops.sample(lg.to(DEV), 0.8, 0.9, seed=99).cpu()
+    _, p = H.nucleus(logits[None], 0.8, 0.9)
+    freq = torch.bincount(got, minlength=8).double() / rows
+    # binomial standard error <= 0.0025 at 40000 draws: 5 sigma
+    assert (freq - p[0].double()).abs().max() < 0.0125, (freq, p)
+    assert (freq[p[0] == 0] == 0).all()
+    # another seed gives another stream
+    got2 = ops.sample(lg.to(DEV), 0.8, 0.9, seed=100).cpu()
+    assert not torch.equal(got, got2)
