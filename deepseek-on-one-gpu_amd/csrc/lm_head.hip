@@ -18,35 +18,45 @@
 
 namespace amla {
 
-// logits[m, n] = sum_k f32(x[m, k]) * f32(w[n, k]); 16 tokens x 16 rows of w per
-// workgroup, the four waves take interleaved 32-wide K steps and add their
-// tiles in wave order.
+// logits[m, n] = sum_k f32(x[m, k]) * f32(w[n, k]).  A workgroup takes 16
+// tokens and 64 rows of w (four tiles of 16); its four waves take interleaved
+// 32-wide K steps, so one x fragment feeds four MFMAs (four accumulator
+// chains), and add their partial tiles in wave order through LDS.
+constexpr int LOGIT_ROWS = 64;
 __global__ __launch_bounds__(256) void bf16_logits_kernel(const uint16_t *__restrict__ x,
                                                           const uint16_t *__restrict__ w, int M, int K, int N,
                                                           float *__restrict__ out, int64_t ldo) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  const int n0 = blockIdx.x * LOGIT_ROWS, m0 = blockIdx.y * 16;
   const int r = lane & 15, kq = lane >> 4;
   const uint16_t *xp = x + (size_t)min(m0 + r, M - 1) * K + 8 * kq;
-  const uint16_t *wp = w + (size_t)min(n0 + r, N - 1) * K + 8 * kq;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const uint16_t *wp[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) wp[t] = w + (size_t)min(n0 + 16 * t + r, N - 1) * K + 8 * kq;
+  f32x4 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int steps = K / 32;
-#pragma unroll 8
-  for (int ks = wave; ks < steps; ks += 4)
-    acc = mfma16(as_bf16x8(ldg16(xp + ks * 32)), as_bf16x8(ldg16_nt(wp + ks * 32)), acc);
-  __shared__ f32x4 red[4][64];
-  red[wave][lane] = acc;
+#pragma unroll 4
+  for (int ks = wave; ks < steps; ks += 4) {
+    const bf16x8 a = as_bf16x8(ldg16(xp + ks * 32));
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = mfma16(a, as_bf16x8(ldg16_nt(wp[t] + ks * 32)), acc[t]);
+  }
+  __shared__ f32x4 red[4][4][64];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) red[wave][t][lane] = acc[t];
   __syncthreads();
-  if (wave == 0) {
-    f32x4 v = red[0][lane];
+  // wave t sums tile t in wave order; C layout: tokens 4 (lane/16) .. +3 of row lane % 16
+  const int t = wave;
+  f32x4 v = red[0][t][lane];
 #pragma unroll
-    for (int q = 1; q < 4; ++q) v += red[q][lane];
-    const int n = n0 + (lane & 15);
+  for (int q = 1; q < 4; ++q) v += red[q][t][lane];
+  const int n = n0 + 16 * t + (lane & 15);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = m0 + 4 * (lane >> 4) + i;
-      if (m < M && n < N) out[(size_t)m * ldo + n] = v[i];
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + 4 * (lane >> 4) + i;
+    if (m < M && n < N) out[(size_t)m * ldo + n] = v[i];
   }
 }
 
@@ -285,7 +295,7 @@ int amla_bf16_logits(const void *x, int64_t m, int64_t k, const void *weight, in
   if (m == 0) return AMLA_OK;
   if (k % 32 || !aligned16(x) || !aligned16(weight) || k > INT32_MAX || n > INT32_MAX || m > (int64_t)65535 * 16)
     return fail(AMLA_EUNSUPPORTED, "bf16_logits: needs k %% 32 == 0 and 16-byte aligned x and weight");
-  bf16_logits_kernel<<<dim3((unsigned)((n + 15) / 16), (unsigned)((m + 15) / 16)), 256, 0,
+  bf16_logits_kernel<<<dim3((unsigned)((n + LOGIT_ROWS - 1) / LOGIT_ROWS), (unsigned)((m + 15) / 16)), 256, 0,
                        reinterpret_cast<hipStream_t>(stream)>>>(static_cast<const uint16_t *>(x),
                                                                 static_cast<const uint16_t *>(weight), (int)m, (int)k,
                                                                 (int)n, logits, ld_logits);
