@@ -396,35 +396,43 @@ namespace amla {
 
 // ---------------------------------------------------------------- routed experts
 
-constexpr int MOE_MAX_SLOTS = 512;  // (token, k) slots per chunk; their row lists travel as kernel arguments
+// (token, k) slots whose row lists travel as kernel arguments; larger chunks
+// copy their lists into the workspace
+constexpr int MOE_ARG_SLOTS = 512;
+constexpr int MOE_MAX_SLOTS = 65536;  // slots per chunk
 
 struct RowList {
-  int32_t row[MOE_MAX_SLOTS];
+  int32_t row[MOE_ARG_SLOTS];
 };
 
-// dst row i (of `rows`) = src row list.row[i]  (gather), or dst row list.row[i] = src row i (scatter)
+// dst row i (of `rows`) = src row L[i]  (gather), or dst row L[i] = src row i
+// (scatter); L = dlist when given (device memory), else the by-value list
 template <bool SCATTER>
 __global__ __launch_bounds__(256) void move_rows_kernel(const uint16_t *__restrict__ src, int64_t d, int rows,
-                                                        RowList list, uint16_t *__restrict__ dst) {
+                                                        RowList list, const int32_t *__restrict__ dlist,
+                                                        uint16_t *__restrict__ dst) {
   const int i = blockIdx.x;
   if (i >= rows) return;
-  const uint16_t *s = src + (size_t)(SCATTER ? i : list.row[i]) * d;
-  uint16_t *t = dst + (size_t)(SCATTER ? list.row[i] : i) * d;
+  const int li = dlist ? dlist[i] : list.row[i];
+  const uint16_t *s = src + (size_t)(SCATTER ? i : li) * d;
+  uint16_t *t = dst + (size_t)(SCATTER ? li : i) * d;
   for (int64_t c = threadIdx.x; c < d / 8; c += blockDim.x)
     *reinterpret_cast<u32x4 *>(t + c * 8) = *reinterpret_cast<const u32x4 *>(s + c * 8);
 }
 
 struct MoeLayout {
   int chunk_tokens;
-  size_t xs, ys, gu, h, part, total;
+  size_t lists, xs, ys, gu, h, part, total;
 };
 
 static MoeLayout moe_layout(int64_t m, int64_t d, int top_k, int64_t n) {
   MoeLayout L;
-  L.chunk_tokens = (int)std::min<int64_t>(m, MOE_MAX_SLOTS / top_k);
+  L.chunk_tokens = (int)std::min<int64_t>(m, (m * top_k <= MOE_ARG_SLOTS ? MOE_ARG_SLOTS : MOE_MAX_SLOTS) / top_k);
   const size_t slots = (size_t)L.chunk_tokens * top_k;
   const int mg = std::min(L.chunk_tokens, 64);  // largest expert group on the skinny path
   size_t off = 0;
+  L.lists = off;
+  off = align_up(off + (slots > MOE_ARG_SLOTS ? 2 * slots * 4 : 0), 256);
   L.xs = off;
   off = align_up(off + slots * d * 2, 256);
   L.ys = off;
@@ -496,11 +504,27 @@ int amla_moe_experts(const void *hidden, int64_t m, int64_t d, int top_k, const 
     const int64_t *ix = indices + t0 * top_k;
     std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return ix[a] < ix[b]; });
     RowList gather, scatter;
-    for (int i = 0; i < ns; ++i) {
-      gather.row[i] = (int32_t)(t0 + order[i] / top_k);
-      scatter.row[i] = (int32_t)(t0 * top_k + order[i]);
+    int32_t *dg = nullptr, *dsc = nullptr;
+    if (ns <= MOE_ARG_SLOTS) {
+      for (int i = 0; i < ns; ++i) {
+        gather.row[i] = (int32_t)(t0 + order[i] / top_k);
+        scatter.row[i] = (int32_t)(t0 * top_k + order[i]);
+      }
+    } else {
+      // long lists go through the workspace; the host array must outlive the
+      // copy, so this path waits for the stream once
+      std::vector<int32_t> hl(2 * (size_t)ns);
+      for (int i = 0; i < ns; ++i) {
+        hl[i] = (int32_t)(t0 + order[i] / top_k);
+        hl[ns + i] = (int32_t)(t0 * top_k + order[i]);
+      }
+      dg = reinterpret_cast<int32_t *>(ws + L.lists);
+      dsc = dg + ns;
+      hipError_t e = hipMemcpyAsync(dg, hl.data(), hl.size() * 4, hipMemcpyHostToDevice, st);
+      if (e == hipSuccess) e = hipStreamSynchronize(st);
+      if (e != hipSuccess) return fail((int)e, "moe_experts: row list copy failed: %s", hipGetErrorString(e));
     }
-    move_rows_kernel<false><<<ns, 256, 0, st>>>(hid, d, ns, gather, xs);
+    move_rows_kernel<false><<<ns, 256, 0, st>>>(hid, d, ns, gather, dg, xs);
     if ((rc = check_launch("moe_experts gather"))) return rc;
     // runs of one expert: [run_begin[r], run_begin[r + 1])
     std::vector<int> run_begin;
@@ -599,7 +623,7 @@ int amla_moe_experts(const void *hidden, int64_t m, int64_t d, int top_k, const 
       q.y = ys + (size_t)i0 * D;
       if ((rc = launch_gemm(q, GEMV_PLAIN, st))) return rc;
     }
-    move_rows_kernel<true><<<ns, 256, 0, st>>>(ys, d, ns, scatter, eout);
+    move_rows_kernel<true><<<ns, 256, 0, st>>>(ys, d, ns, scatter, dsc, eout);
     if ((rc = check_launch("moe_experts scatter"))) return rc;
   }
   return AMLA_OK;

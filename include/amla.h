@@ -182,7 +182,10 @@ size_t amla_moe_route_workspace_bytes(int64_t m, int64_t n_experts);
  * chosen expert runs once over all of its tokens (gather, [gate | up] in one
  * skinny GEMM, silu * up, down, scatter).  hidden (m, d) bf16, expert_out
  * (m, top_k, d) bf16; d % 128 == 0, n_inter % 256 == 0, top_k <= 64.
- * Workspace of amla_moe_experts_workspace_bytes(m, d, top_k, n_inter) bytes. */
+ * Workspace of amla_moe_experts_workspace_bytes(m, d, top_k, n_inter) bytes.
+ * Up to 512 (token, k) slots the call is asynchronous like the others; above
+ * that the slot lists are copied from host memory and the call waits for
+ * `stream` once per 65536 slots. */
 int amla_moe_experts(const void *hidden, int64_t m, int64_t d, int top_k, const int64_t *indices, int64_t n_inter,
                      int64_t n_experts, const void *const *gate_w, const float *const *gate_s,
                      const void *const *up_w, const float *const *up_s, const void *const *down_w,

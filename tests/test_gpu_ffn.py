@@ -171,7 +171,7 @@ def test_moe_block(E, G, TG, K, B, S):
     assert_parity(got, want, f"moe_block E={E}")
 
 
-@pytest.mark.parametrize("E,K,m", [(2, 1, 300), (6, 3, 150), (256, 8, 8)])
+@pytest.mark.parametrize("E,K,m", [(2, 1, 300), (6, 3, 150), (256, 8, 8), (16, 8, 200)])
 def test_moe_experts_vs_expert_ffn(E, K, m):
     """amla_moe_experts (chunks of 512 slots; large expert groups take the GEMM path) against
     expert_ffn of every (token, k) pair."""
