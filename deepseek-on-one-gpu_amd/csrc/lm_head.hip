@@ -124,33 +124,27 @@ AMLA_DEV float uniform01(uint64_t seed, uint64_t ctr) {
 // Nucleus sampling of one row, the reference's rule: p = softmax(logits / T);
 // sorted descending, token k is dropped when the mass strictly before it
 // exceeds top_p; the kept probabilities are renormalised and one is drawn.
-// The kept set is {i : p_i >= t*}, t* the smallest probability whose mass of
-// strictly larger probabilities is <= top_p.
+// Everything works on e = exp(logits / T - max) (p = e / sum e; the
+// normalisation cancels): with e1 > e2 > .. sorted and C_k their prefix sums,
+// the reference keeps e_1 .. e_{K+1}, K the last k with C_k <= top_p * sum e,
+// i.e. every token with e >= t, t the smallest value whose strictly larger
+// mass is <= top_p * sum e.  t is always the value of a token (or 0), found on
+// the fp32 bit pattern (e >= 0: bit order = value order) by a three-level
+// radix search: per level a histogram of the mass over the next 11 / 11 / 10
+// bits in 2^-40 fixed point (integer sums: independent of the atomics' order).
 __global__ __launch_bounds__(SAMPLE_THREADS) void top_p_kernel(const float *__restrict__ logits, int64_t n,
                                                                int64_t ld, float temp, float top_p, uint64_t seed,
                                                                int64_t *__restrict__ out) {
   const float *row = logits + (size_t)blockIdx.x * ld;
   const int tid = threadIdx.x;
-  // softmax statistics of logits / T (fp32, as softmax(logits / temperature))
   float mx = -INFINITY;
   int dummy = 0;
   for (int64_t j = tid; j < n; j += SAMPLE_THREADS) mx = fmaxf(mx, row[j] / temp);
   block_argmax<SAMPLE_THREADS>(mx, dummy);
-  float z = 0.f;
-  for (int64_t j = tid; j < n; j += SAMPLE_THREADS) z += expf(row[j] / temp - mx);
-  z = block_sum<SAMPLE_THREADS>(z);
-  auto prob = [&](int64_t j) { return expf(row[j] / temp - mx) / z; };
-  // smallest threshold t with mass(p > t) <= top_p; with q1 > q2 > .. sorted and
-  // C_k their prefix sums this is t = q_{K+1}, K the last k with C_k <= top_p,
-  // and the reference keeps exactly q_1 .. q_{K+1} (mass before each <= top_p).
-  // t is found on the fp32 bit pattern (p >= 0: bit order = value order) by a
-  // three-level radix search: per level a histogram of the probability mass
-  // over the next 11 / 11 / 10 bits, in 2^-40 fixed point (integer sums, so the
-  // result does not depend on the order of the atomics).
+  auto ev = [&](int64_t j) { return expf(row[j] / temp - mx); };
   constexpr double FX = 1099511627776.0;  // 2^40
-  const uint64_t top_fx = (uint64_t)((double)top_p * FX);
   __shared__ unsigned long long hist[2048];
-  __shared__ unsigned long long above_s;
+  __shared__ unsigned long long above_s, total_s;
   __shared__ uint32_t prefix_s;
   if (tid == 0) {
     above_s = 0;
@@ -164,21 +158,29 @@ __global__ __launch_bounds__(SAMPLE_THREADS) void top_p_kernel(const float *__re
     const uint32_t prefix = prefix_s;
     const int pshift = shift + (level == 2 ? 10 : 11);  // bits above this level's bins
     for (int64_t j = tid; j < n; j += SAMPLE_THREADS) {
-      const float pj = prob(j);
-      const uint32_t key = __float_as_uint(pj);
+      const float e = ev(j);
+      const uint32_t key = __float_as_uint(e);
       if (level == 0 || (key >> pshift) == (prefix >> pshift))
-        atomicAdd(&hist[(key >> shift) & (nb - 1)], (unsigned long long)((double)pj * FX));
+        atomicAdd(&hist[(key >> shift) & (nb - 1)], (unsigned long long)((double)e * FX));
     }
     __syncthreads();
+    if (level == 0 && tid < 64) {
+      unsigned long long t = 0;
+      for (int q = tid; q < 2048; q += 64) t += hist[q];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+      if (tid == 0) total_s = t;
+    }
+    __syncthreads();
+    const unsigned long long top_fx = (unsigned long long)((double)top_p * (double)total_s);
     // smallest bin b whose mass above (bins > b, plus everything above this
-    // level's prefix) is <= top_p: wave 0, 32 bins per lane from the top
+    // level's prefix) is <= top_p * sum: wave 0, nb / 64 bins per lane from the top
     if (tid < 64) {
       const int per = nb / 64;
       const int b_hi = nb - 1 - tid * per;  // this lane's bins: b_hi down to b_hi - per + 1
       unsigned long long own = 0;
       for (int q = 0; q < per; ++q) own += hist[b_hi - q];
-      // exclusive prefix over lanes 0..tid-1 (higher bins first)
-      unsigned long long ex = own;
+      unsigned long long ex = own;  // inclusive prefix over lanes 0..tid (higher bins first)
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const unsigned long long v = __shfl_up(ex, o, 64);
@@ -186,55 +188,40 @@ __global__ __launch_bounds__(SAMPLE_THREADS) void top_p_kernel(const float *__re
       }
       ex -= own;
       const unsigned long long base = above_s;
-      // mass above bin b = base + ex + (bins of this lane above b)
       unsigned long long run = base + ex;
       int found = -1;
+      unsigned long long mass_above = 0;
       for (int q = 0; q < per; ++q) {
         const int bb = b_hi - q;
-        if (run <= top_fx) found = bb;  // bins are visited downwards: keep the smallest
-        else break;
+        if (run > top_fx) break;
+        found = bb;  // bins are visited downwards: keep the smallest
+        mass_above = run;
         run += hist[bb];
-      }
-      // the smallest qualifying bin overall: the lane with the lowest bins that found one
-      int lane_best = found;
-      unsigned long long mass_above = 0;
-      if (found >= 0) {
-        mass_above = base + ex;
-        for (int bb = b_hi; bb > found; --bb) mass_above += hist[bb];
       }
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) {
-        const int ob = __shfl_xor(lane_best, o, 64);
+        const int ob = __shfl_xor(found, o, 64);
         const unsigned long long om = __shfl_xor(mass_above, o, 64);
-        if (ob >= 0 && (lane_best < 0 || ob < lane_best)) {
-          lane_best = ob;
+        if (ob >= 0 && (found < 0 || ob < found)) {
+          found = ob;
           mass_above = om;
         }
       }
       if (tid == 0) {
-        prefix_s = prefix | ((uint32_t)lane_best << shift);
+        prefix_s = prefix | ((uint32_t)found << shift);
         above_s = mass_above;
       }
     }
     __syncthreads();
   }
-  // t* = the largest probability <= t (-1 when no token is below: all kept)
-  const float thr = __uint_as_float(prefix_s);
-  float best = -1.f;
-  int bi = 0;
-  for (int64_t j = tid; j < n; j += SAMPLE_THREADS) {
-    const float pj = prob(j);
-    if (pj <= thr) argmax_merge(best, bi, pj, (int)j);
-  }
-  block_argmax<SAMPLE_THREADS>(best, bi);
-  const float tstar = best;
-  // kept mass, then an inverse-CDF draw in index order over contiguous chunks
+  const float tstar = __uint_as_float(prefix_s);  // keep e >= t*
+  // kept mass, then an inverse-CDF draw in vocabulary order over contiguous chunks
   const int64_t chunk = (n + SAMPLE_THREADS - 1) / SAMPLE_THREADS;
   const int64_t c0 = std::min<int64_t>(n, tid * chunk), c1 = std::min<int64_t>(n, c0 + chunk);
   float mine = 0.f;
   for (int64_t j = c0; j < c1; ++j) {
-    const float pj = prob(j);
-    if (pj >= tstar) mine += pj;
+    const float e = ev(j);
+    if (e >= tstar) mine += e;
   }
   // exclusive prefix of the per-thread kept mass
   __shared__ float pre[SAMPLE_THREADS];
@@ -260,10 +247,10 @@ __global__ __launch_bounds__(SAMPLE_THREADS) void top_p_kernel(const float *__re
     float acc = pre[tid];
     int64_t last = -1;
     for (int64_t j = c0; j < c1; ++j) {
-      const float pj = prob(j);
-      if (pj < tstar) continue;
+      const float e = ev(j);
+      if (e < tstar) continue;
       last = j;
-      acc += pj;
+      acc += e;
       if (u < acc) break;
     }
     atomicMax(&pick, (int)last);
@@ -273,7 +260,7 @@ __global__ __launch_bounds__(SAMPLE_THREADS) void top_p_kernel(const float *__re
     int r = pick;
     if (r < 0) {  // u fell on the rounding edge of the last chunk: take the last kept token
       for (int64_t j = n - 1; j >= 0; --j)
-        if (prob(j) >= tstar) {
+        if (ev(j) >= tstar) {
           r = (int)j;
           break;
         }
