@@ -1,7 +1,7 @@
 """CPU oracle of the MLA + block-FP8 path (TEST INFRASTRUCTURE ONLY).
 
 Only tests/, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-bench.py import this package, as the checker.  The product package never does.
+bench.py import this package, to check results.  The product package never does.
 
 * ref_ops.py  - torch-CPU restatement of inference/ops.py:10-183 (the rounding
                 points of the reference) and forward.py:92-94.

@@ -2,7 +2,7 @@
 inference/forward.py:112-153.
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product package imports this module;
-tests/ and the bench's CPU leg use it as the checker, never as a fallback.
+tests/ and the bench's CPU leg use it to check results, never as a fallback.
 
 The reference's numerics are defined by its rounding points, so each function
 follows its op sequence: every fp8 linear returns bf16, F.silu on a bf16 tensor

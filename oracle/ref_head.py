@@ -1,7 +1,7 @@
 """CPU oracle for the output head: inference/forward.py:67-72 (final norm + lm_head) and
 the deterministic part of inference/engine.py:166-186 (sample).
 
-TEST INFRASTRUCTURE ONLY: used by tests/ as the checker, never as a fallback.
+TEST INFRASTRUCTURE ONLY: used by tests/ to check results, never as a fallback.
 
 ``sample`` draws with torch.multinomial, so its random stream cannot be matched;
 the oracle restates what the draw is taken from (``nucleus``: the kept tokens and

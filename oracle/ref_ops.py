@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product package imports this module;
 it is used by tests/, by ``__graft_entry__.smoke()`` and by the ``cpu_baseline``
-leg of bench.py, and there only as the checker (or the timed CPU baseline),
+leg of bench.py, and there only to check results (or as the timed CPU baseline),
 never as a fallback for the GPU path.
 
 Each function follows the reference's torch op sequence step by step, because
