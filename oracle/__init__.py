@@ -1,4 +1,4 @@
-"""CPU oracle of the MLA + block-FP8 path (TEST INFRASTRUCTURE ONLY).
+"""CPU oracle of the MLA + block-FP8 path and its neighbours (TEST INFRASTRUCTURE ONLY).
 
 Only tests/, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 bench.py import this package, to check results.  The product package never does.
@@ -6,8 +6,12 @@ bench.py import this package, to check results.  The product package never does.
 * ref_ops.py  - torch-CPU restatement of inference/ops.py:10-183 (the rounding
                 points of the reference) and forward.py:92-94.
 * truth.py    - the same maths in float64, naive and absorbed.
+* ref_ffn.py  - SwiGLU, routing and the MoE block (inference/ops.py:186-257,
+                forward.py:112-153).
+* ref_head.py - final norm + lm_head and the nucleus rule of sample
+                (forward.py:67-72, engine.py:166-186).
 * fp8_ref.c   - C restatement of the e4m3fn decode and block dequant
-                (bit-exact checker), built by oracle/Makefile into _build/.
+                (bit-exact reference table), built by oracle/Makefile into _build/.
 """
 from __future__ import annotations
 
