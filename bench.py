@@ -220,8 +220,11 @@ def ffn_extras(B, dev):
     out["dense_ffn_b8_us"] = round(ms * 1000, 2)
     out["dense_ffn_b8_hbm_gbs"] = round(3 * di * d / (ms * 1e-3) / 1e9, 1)
     del dense
-    experts = [{"gate_proj": _fp8_on_device(mi, d, gen, dev), "up_proj": _fp8_on_device(mi, d, gen, dev),
-                "down_proj": _fp8_on_device(d, mi, gen, dev)} for _ in range(E)]
+    # all experts of the layer stacked (E, rows, cols): pointer tables without per-expert host work
+    experts = {}
+    for key, (r, c) in (("gate_proj", (mi, d)), ("up_proj", (mi, d)), ("down_proj", (d, mi))):
+        w, sc = _fp8_on_device(E * r, c, gen, dev)
+        experts[key] = (w.view(E, r, c), torch.rand(E, (r + 127) // 128, (c + 127) // 128, generator=gen, device=dev) + 0.5)
     shared = {"gate_proj": _fp8_on_device(mi, d, gen, dev), "up_proj": _fp8_on_device(mi, d, gen, dev),
               "down_proj": _fp8_on_device(d, mi, gen, dev)}
     gw = (torch.randn(E, d, generator=gen, device=dev) * 0.02).to(torch.bfloat16)

@@ -395,19 +395,52 @@ def route(hidden: torch.Tensor, gate_weight: torch.Tensor, config) -> tuple[torc
     return idx.view(shape), w.view(shape)
 
 
+_stacked_cache: dict = {}
+
+
+def _stacked_expert_tables(experts: dict, E: int, d: int, dev):
+    """Pointer tables of stacked expert weights (validated once per set of tensors)."""
+    key = tuple((experts[k][0].data_ptr(), experts[k][1].data_ptr(), tuple(experts[k][0].shape),
+                 tuple(experts[k][1].shape), experts[k][0].dtype, experts[k][1].dtype, experts[k][0].stride(),
+                 experts[k][1].stride(), str(experts[k][0].device)) for k in ("gate_proj", "up_proj", "down_proj")) + (E, d)
+    hit = _stacked_cache.get(key)
+    if hit is not None:
+        return hit
+    tabs = []
+    n_inter = experts["gate_proj"][0].shape[1]
+    for key_name, shape in (("gate_proj", (E, n_inter, d)), ("up_proj", (E, n_inter, d)), ("down_proj", (E, d, n_inter))):
+        wt, sc = experts[key_name]
+        if wt.dtype != FP8 or sc.dtype != torch.float32 or wt.device != dev or sc.device != dev or \
+                not (wt.is_contiguous() and sc.is_contiguous()):
+            raise ValueError(f"moe_block: stacked {key_name} must be contiguous e4m3fn weights with fp32 scales on {dev}")
+        if tuple(wt.shape) != shape or tuple(sc.shape) != (E, math.ceil(shape[1] / 128), math.ceil(shape[2] / 128)):
+            raise ValueError(f"moe_block: stacked {key_name} has shape {tuple(wt.shape)} / {tuple(sc.shape)}, "
+                             f"expected {shape}")
+        for t in (wt, sc):
+            step = t[0].numel() * t.element_size()
+            tabs.append((ctypes.c_void_p * E)(*[t.data_ptr() + e * step for e in range(E)]))
+    if len(_stacked_cache) > 64:
+        _stacked_cache.clear()
+    _stacked_cache[key] = (tabs, n_inter)
+    return tabs, n_inter
+
+
 def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: dict, experts, config) -> torch.Tensor:
     """inference/forward.py:112-153 with the routed experts handed in.
 
     ``experts`` maps an expert index to its weight dict (a Mapping, or a
-    callable taking the index) on the same device; the reference's
-    weight_store / gpu_transfer streaming is out of scope here.  As in the
+    callable taking the index) on the same device, or is one dict of stacked
+    weights ``{"gate_proj": (w (E, n, k), s (E, ceil(n/128), ceil(k/128))), ...}``
+    (all experts of the layer contiguous: no per-expert host work); the
+    reference's weight_store / gpu_transfer streaming is out of scope here.  As in the
     reference, the chosen indices come to the host once (one synchronisation).
     amla_moe_experts then runs each chosen expert once over all tokens that
     chose it (the reference loops over (token, k) pairs), and the combine keeps
     the reference's order and bf16 roundings: per token, k = 0.. accumulates
     bf16(bf16(w_k) * expert_k(x)) into a bf16 sum, then shared + sum * 2.5.
     """
-    get = experts if callable(experts) else experts.__getitem__
+    stacked = isinstance(experts, dict) and "gate_proj" in experts and experts["gate_proj"][0].dim() == 3
+    get = None if stacked else (experts if callable(experts) else experts.__getitem__)
     idx, w = route(hidden, gate_weight, config)
     shared_out = expert_ffn(hidden, shared_weights)
     d = hidden.shape[-1]
@@ -421,11 +454,17 @@ def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: d
     if m == 0:
         return out
     idx_host = idx.reshape(m, top_k).cpu().contiguous()
-    tables = [(ctypes.c_void_p * E)() for _ in range(6)]
     dev = hidden.device
-    n_inter = None
-    keep = []
-    for e in torch.unique(idx_host).tolist():
+    if stacked:
+        tables, n_inter = _stacked_expert_tables(experts, E, d, dev)
+        keep = []
+        chosen = []
+    else:
+        tables = [(ctypes.c_void_p * E)() for _ in range(6)]
+        n_inter = None
+        keep = []
+        chosen = torch.unique(idx_host).tolist()
+    for e in chosen:
         ew = get(int(e))
         for j, key in enumerate(("gate_proj", "up_proj", "down_proj")):
             wt, sc = ew[key]

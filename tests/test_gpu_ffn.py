@@ -203,3 +203,21 @@ def test_moe_experts_vs_expert_ffn(E, K, m):
             y = F.expert_ffn(h[sel[:, 0]], table[e])
             want[sel[:, 0], sel[:, 1]] = y
     assert_parity(eout, want, f"moe_experts E={E} K={K} m={m}")
+
+
+def test_moe_block_stacked_experts():
+    print("[case] moe_block stacked", flush=True)
+    E, d, i = 32, 256, 256
+    cfg = _cfg(E, 4, 2, 4)
+    h = _x((3, 2, d), "moe-stacked")
+    gw = synth.randn((E, d), synth.seed_of("moe-router-st", E), 0.1).to(torch.bfloat16)
+    shared = _mlp(d, i, "shared-st")
+    table = {e: _mlp(d, i, f"st-expert{e}") for e in range(E)}
+    stacked = {k: (torch.stack([table[e][k][0] for e in range(E)]).to(DEV),
+                   torch.stack([table[e][k][1] for e in range(E)]).to(DEV)) for k in ("gate_proj", "up_proj", "down_proj")}
+    got = ops.moe_block(h.to(DEV), gw.to(DEV), _dev(shared), stacked, cfg)
+    got2 = ops.moe_block(h.to(DEV), gw.to(DEV), _dev(shared), stacked, cfg)    # cached tables
+    torch.cuda.synchronize()
+    want = F.moe_block(h, gw, shared, lambda e: table[e], cfg)
+    assert_parity(got, want, "moe_block stacked")
+    assert torch.equal(got, got2)
