@@ -221,3 +221,15 @@ def test_moe_block_stacked_experts():
     want = F.moe_block(h, gw, shared, lambda e: table[e], cfg)
     assert_parity(got, want, "moe_block stacked")
     assert torch.equal(got, got2)
+
+
+def test_empty_inputs():
+    d, i = 256, 256
+    w = _dev(_mlp(d, i, "empty"))
+    x = torch.zeros(2, 0, d, dtype=torch.bfloat16, device=DEV)
+    assert ops.dense_ffn(x, w).shape == (2, 0, d)
+    cfg = _cfg(16, 4, 2, 4)
+    gw = torch.zeros(16, d, dtype=torch.bfloat16, device=DEV)
+    idx, wt = ops.route(x, gw, cfg)
+    assert idx.shape == (2, 0, 4) and wt.shape == (2, 0, 4)
+    assert ops.moe_block(x, gw, w, {e: w for e in range(16)}, cfg).shape == (2, 0, d)

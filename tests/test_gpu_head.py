@@ -71,3 +71,12 @@ def test_top_p_distribution():
     # another seed gives another stream
     got2 = ops.sample(lg.to(DEV), 0.8, 0.9, seed=100).cpu()
     assert not torch.equal(got, got2)
+
+
+def test_empty_inputs():
+    w = torch.zeros(48, 64, dtype=torch.bfloat16, device=DEV)
+    x = torch.zeros(0, 64, dtype=torch.bfloat16, device=DEV)
+    assert ops.lm_head_logits(x, w).shape == (0, 48)
+    lg = torch.zeros(0, 48, device=DEV)
+    assert ops.sample(lg, 0.0, 0.9).shape == (0,)
+    assert ops.sample(lg, 1.0, 0.9).shape == (0,)
