@@ -222,7 +222,6 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t *__res
   const uint16_t *wp = gw + (size_t)min(e0 + r, E - 1) * D + 8 * kq;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int steps = D / 32;
-#pragma unroll 4
   for (int ks = wave + 4 * z; ks < steps; ks += 4 * nz)
     acc = mfma16(as_bf16x8(ldg16(hp + ks * 32)), as_bf16x8(ldg16(wp + ks * 32)), acc);
   __shared__ f32x4 red[4][64];
