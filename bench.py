@@ -258,6 +258,30 @@ def head_extras(B, dev):
     return out
 
 
+def stream_extras(dev):
+    """Expert streaming: 8 R1 experts (gate/up/down fp8 + scales, 44 MB each) from pinned host memory
+    into the device slot pool on the side stream, the compute stream waiting on the device."""
+    from amla.experts import ExpertStreamer
+    d, mi = CFG.hidden_size, CFG.moe_intermediate_size
+    host = {}
+    for e in range(16):
+        host[e] = {p: (torch.randint(0, 126, shp, dtype=torch.uint8).view(torch.float8_e4m3fn).pin_memory(),
+                       torch.rand((shp[0] + 127) // 128, (shp[1] + 127) // 128).pin_memory())
+                   for p, shp in (("gate_proj", (mi, d)), ("up_proj", (mi, d)), ("down_proj", (d, mi)))}
+    st = ExpertStreamer(CFG, lambda l, e: host[e], dev, slots=8)
+    st.transfer_experts(0, list(range(8, 16)))
+    torch.cuda.synchronize()
+    nbytes = sum(t.numel() * t.element_size() for e in range(8) for pair in host[e].values() for t in pair)
+    s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_.record()
+    st.transfer_experts(1, list(range(8)))    # 8 new experts: every slot evicted and refilled
+    e_.record()
+    torch.cuda.synchronize()
+    ms = s_.elapsed_time(e_)
+    del st, host
+    return {"expert_stream_8_us": round(ms * 1000, 1), "expert_stream_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -344,6 +368,7 @@ def main():
         del hp, cp
         extras.update(ffn_extras(B, dev))
         extras.update(head_extras(B, dev))
+        extras.update(stream_extras(dev))
         log(f"[bench] extras: {extras}")
 
     result = {
