@@ -6,12 +6,14 @@
 //   amla_moe_experts  <- the routed-expert loop of moe_block, inference/forward.py:139-151
 //   amla_moe_combine  <- the combine of moe_block, inference/forward.py:138-153
 //
-// swiglu runs the gate and up projections with the skinny (M <= 64) or large
-// fp8 GEMM, one elementwise pass for silu * up, and the down projection; the
-// rounding points are the reference's (bf16 after every linear, after silu and
-// after the product).  Routing computes the fp32 logits with bf16 MFMAs (exact
-// products, fp32 sums), then one wave per token does the sigmoid, the group
-// ranking and the top-k in fp32.
+// swiglu runs gate and up as one skinny (M <= 64) or large fp8 GEMM over the
+// two stacked weights, one elementwise pass for silu * up over the stacked
+// rows, and the down projection; the rounding points are the reference's (bf16
+// after every linear, after silu and after the product).  The routed experts
+// of a MoE layer run as grouped skinny GEMMs (up to 32 experts per launch).
+// Routing computes the fp32 logits with bf16 MFMAs (exact products, fp32
+// sums), then one wave per token does the sigmoid, the group ranking and the
+// top-k in fp32.
 #include <math.h>
 
 #include <algorithm>
