@@ -28,8 +28,8 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "deepseek-on-one-gpu_amd")]
 
 import torch  # noqa: E402
 
-from amla import ops, synth  # noqa: E402
-from amla._lib import MlaArgs, check, lib  # noqa: E402
+from amla import ops, synth, torch_ops  # noqa: E402
+from amla._lib import check, lib  # noqa: E402
 from amla.config import DeepSeekConfig  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
@@ -122,8 +122,9 @@ def decode_stage_times(stack, caches, hidden, pos, rope, ctx, reps=2):
     k = 0
     for _ in range(reps):
         for lay, cache in zip(stack, caches):
-            a, _p = ops._fill_args(hidden, lay.attn_weights, cache, pos, rope, CFG, out=out,
-                                   input_gamma=lay.input_layernorm, residual=hidden, max_context=ctx)
+            operands = ops._mla_operands(hidden, lay.attn_weights, cache, pos, rope, CFG,
+                                         input_gamma=lay.input_layernorm, residual=hidden, max_context=ctx)
+            a = torch_ops.fill_mla_args(out=out, **operands)
             ws = ops.workspace(dev, lib().amla_mla_decode_workspace_bytes(a))
             a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
             arr = (ctypes.c_void_p * nev)(*[e.cuda_event for e in evs[k]])

@@ -34,6 +34,7 @@ class MlaArgs(ctypes.Structure):
         ("gamma_q", c_void_p), ("gamma_kv", c_void_p),
         ("ckv_cache", c_void_p), ("kpe_cache", c_void_p), ("rope_table", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+        ("attn_out", c_void_p),
     ]
 
 

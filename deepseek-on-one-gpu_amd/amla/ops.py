@@ -23,8 +23,8 @@ from typing import Sequence
 
 import torch
 
-from . import _lib
-from ._lib import MlaArgs, check, lib
+from . import _lib, torch_ops
+from ._lib import check, lib
 
 BF16 = torch.bfloat16
 FP8 = torch.float8_e4m3fn
@@ -51,21 +51,14 @@ def _need(t: torch.Tensor, name: str, dtype, dev=None) -> None:
 
 # ------------------------------------------------------------------ workspace
 
-_workspaces: dict = {}
-
-
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device scratch for the MLA entry points, grown on demand.
+    """Scratch for one call, from torch's caching allocator on the current stream.
 
-    Size it (one eager call) before a HIP graph capture so that no allocation
-    happens while capturing.
+    A fresh buffer per call: inside a HIP graph capture it comes from the
+    graph's private pool (a replay never touches memory another call owns),
+    and calls on different streams never share it.
     """
-    key = (device.type, device.index)
-    buf = _workspaces.get(key)
-    if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[key] = buf
-    return buf
+    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
 
 
 # ------------------------------------------------------------------ elementwise / linear
@@ -80,11 +73,8 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.
         raise ValueError(f"rms_norm: weight shape {tuple(weight.shape)} != ({dim},)")
     xc = x.contiguous()
     w = weight.contiguous()
-    y = torch.empty_like(xc)
     rows = xc.numel() // dim if dim else 0
-    check(lib().amla_rms_norm(xc.data_ptr(), rows, dim, dim, w.data_ptr(), float(eps), y.data_ptr(), dim,
-                              _stream_ptr(xc)), "rms_norm")
-    return y
+    return torch.ops.amla.rms_norm(xc.view(rows, dim), w, float(eps)).view(x.shape)
 
 
 def fp8_block_dequant(weight: torch.Tensor, scale_inv: torch.Tensor) -> torch.Tensor:
@@ -118,15 +108,7 @@ def fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Tensor,
     x2 = x.reshape(-1, k)
     if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
         x2 = x2.contiguous()
-    m = x2.shape[0]
-    y = torch.empty(m, n, dtype=BF16, device=x.device)
-    if m:
-        need = lib().amla_fp8_linear_workspace_bytes(m, n, k)
-        ws = workspace(x.device, need) if need else None
-        check(lib().amla_fp8_linear(x2.data_ptr(), m, k, x2.stride(0), weight.data_ptr(), scale_inv.data_ptr(),
-                                    n, y.data_ptr(), n, ws.data_ptr() if ws is not None else None,
-                                    ws.numel() if ws is not None else 0, _stream_ptr(x)), "fp8_linear")
-    return y.view(*x.shape[:-1], n)
+    return torch.ops.amla.fp8_linear(x2, weight, scale_inv).view(*x.shape[:-1], n)
 
 
 # ------------------------------------------------------------------ RoPE
@@ -173,12 +155,8 @@ def apply_rope(x: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
     if freqs.shape != (S, dim // 2):
         raise ValueError(f"apply_rope: freqs shape {tuple(freqs.shape)} != ({S}, {dim // 2})")
     xc = x.contiguous()
-    f = torch.view_as_real(freqs.contiguous())
-    y = torch.empty_like(xc)
     groups = xc.numel() // (S * dim) if S * dim else 0
-    check(lib().amla_apply_rope(xc.data_ptr(), groups, S, dim, f.data_ptr(), y.data_ptr(), _stream_ptr(xc)),
-          "apply_rope")
-    return y
+    return torch.ops.amla.apply_rope(xc.view(groups, S, dim), freqs.contiguous()).view(x.shape)
 
 
 # ------------------------------------------------------------------ MLA
@@ -190,7 +168,7 @@ def softmax_scale(config) -> float:
 
 
 def _positions(position, B: int, S: int, device, max_context):
-    """(int32 device tensor (B,), max position+S) from an int, a sequence or a tensor."""
+    """(int32 device tensor (B,), max position+S or None) from an int, a sequence or a tensor."""
     if isinstance(position, torch.Tensor):
         if position.dtype != torch.int32 or position.device != device or position.shape != (B,):
             raise ValueError("position tensor must be int32 (B,) on the hidden states' device")
@@ -205,8 +183,14 @@ def _positions(position, B: int, S: int, device, max_context):
     return torch.tensor(pos, dtype=torch.int32, device=device), max(pos) + S
 
 
-def _fill_args(hidden, attn_weights, kv_cache, position, rope_freqs, config, *, out, input_gamma=None,
-               residual=None, max_context=None):
+_PROJ = (("q_a_proj", "w_q_a"), ("q_b_proj", "w_q_b"), ("kv_a_proj_with_mqa", "w_kv_a"),
+         ("kv_b_proj", "w_kv_b"), ("o_proj", "w_o"))
+
+
+def _mla_operands(hidden, attn_weights, kv_cache, position, rope_freqs, config, *, input_gamma=None,
+                  residual=None, attn_out=None, max_context=None) -> dict:
+    """Validates the reference's arguments and unpacks them into the operands of
+    ``torch.ops.amla.mla_decode`` / ``mla_prefill`` (raises before any launch)."""
     _need(hidden, "hidden", BF16)
     dev = hidden.device
     if hidden.dim() != 3:
@@ -224,7 +208,7 @@ def _fill_args(hidden, attn_weights, kv_cache, position, rope_freqs, config, *, 
     max_seq = ckv.shape[1]
     if rope_freqs.dtype != torch.complex64 or rope_freqs.device != dev or not rope_freqs.is_contiguous():
         raise TypeError("rope_freqs must be a contiguous complex64 tensor on the same device")
-    if rope_freqs.shape[1] != config.qk_rope_head_dim // 2:
+    if rope_freqs.dim() != 2 or rope_freqs.shape[1] != config.qk_rope_head_dim // 2:
         raise ValueError("rope_freqs must have qk_rope_head_dim/2 columns")
     pos_t, mc = _positions(position, B, S, dev, max_context)
     if mc is None:
@@ -233,17 +217,8 @@ def _fill_args(hidden, attn_weights, kv_cache, position, rope_freqs, config, *, 
         raise ValueError(f"position + seq_len = {mc} exceeds the cache length {max_seq}")
     if mc > rope_freqs.shape[0]:
         raise ValueError(f"position + seq_len = {mc} exceeds the rope table length {rope_freqs.shape[0]}")
-    a = MlaArgs()
-    a.batch, a.seq_len, a.hidden = B, S, D
-    a.heads, a.q_lora, a.kv_lora = config.num_attention_heads, config.q_lora_rank, config.kv_lora_rank
-    a.qk_nope, a.qk_rope, a.v_dim = config.qk_nope_head_dim, config.qk_rope_head_dim, config.v_head_dim
-    a.max_seq, a.rope_rows, a.max_context = max_seq, rope_freqs.shape[0], mc
-    a.eps = float(config.rms_norm_eps)
-    a.softmax_scale = float(softmax_scale(config))
-    a.positions = pos_t.data_ptr()
-    a.hidden_states, a.out = hidden.data_ptr(), out.data_ptr()
-    a.input_gamma = input_gamma.data_ptr() if input_gamma is not None else None
-    a.residual = residual.data_ptr() if residual is not None else None
+    if mc < S:
+        raise ValueError(f"max_context {mc} is below seq_len {S}")
     H = config.num_attention_heads
     shapes = {
         "q_a_proj": (config.q_lora_rank, D),
@@ -252,66 +227,70 @@ def _fill_args(hidden, attn_weights, kv_cache, position, rope_freqs, config, *, 
         "kv_b_proj": (H * (config.qk_nope_head_dim + config.v_head_dim), config.kv_lora_rank),
         "o_proj": (D, H * config.v_head_dim),
     }
-    fields = {"q_a_proj": ("w_q_a", "s_q_a"), "q_b_proj": ("w_q_b", "s_q_b"),
-              "kv_a_proj_with_mqa": ("w_kv_a", "s_kv_a"), "kv_b_proj": ("w_kv_b", "s_kv_b"),
-              "o_proj": ("w_o", "s_o")}
-    for name, (wf, sf) in fields.items():
-        w, s = attn_weights[name]
+    ops = {"hidden": hidden}
+    for name, field in _PROJ:
+        w, sc = attn_weights[name]
         _need(w, f"{name}.weight", FP8, dev)
-        _need(s, f"{name}.weight_scale_inv", torch.float32, dev)
+        _need(sc, f"{name}.weight_scale_inv", torch.float32, dev)
         n, k = shapes[name]
-        if tuple(w.shape) != (n, k) or tuple(s.shape) != (math.ceil(n / 128), math.ceil(k / 128)):
-            raise ValueError(f"{name}: weight {tuple(w.shape)} / scale {tuple(s.shape)} do not match ({n}, {k})")
-        setattr(a, wf, w.data_ptr())
-        setattr(a, sf, s.data_ptr())
+        if tuple(w.shape) != (n, k) or tuple(sc.shape) != (math.ceil(n / 128), math.ceil(k / 128)):
+            raise ValueError(f"{name}: weight {tuple(w.shape)} / scale {tuple(sc.shape)} do not match ({n}, {k})")
+        ops[field] = w
+        ops["s" + field[1:]] = sc
     gq, gkv = attn_weights["q_a_layernorm"], attn_weights["kv_a_layernorm"]
     _need(gq, "q_a_layernorm", BF16, dev)
     _need(gkv, "kv_a_layernorm", BF16, dev)
-    a.gamma_q, a.gamma_kv = gq.data_ptr(), gkv.data_ptr()
-    a.ckv_cache, a.kpe_cache = ckv.data_ptr(), kpe.data_ptr()
-    a.rope_table = rope_freqs.data_ptr()
-    return a, pos_t
+    if gq.shape != (config.q_lora_rank,) or gkv.shape != (config.kv_lora_rank,):
+        raise ValueError("q_a_layernorm / kv_a_layernorm do not match q_lora_rank / kv_lora_rank")
+    if input_gamma is not None:
+        _need(input_gamma, "input_layernorm", BF16, dev)
+        if input_gamma.shape != (D,):
+            raise ValueError("input_layernorm must be (hidden_size,)")
+    if residual is not None:
+        _need(residual, "residual", BF16, dev)
+        if residual.shape != hidden.shape:
+            raise ValueError("residual must have the hidden states' shape")
+    if attn_out is not None:
+        _need(attn_out, "attn_out", BF16, dev)
+        if tuple(attn_out.shape) != (B, S, H * config.v_head_dim) or attn_out.data_ptr() % 16:
+            raise ValueError(f"attn_out must be a 16-byte aligned (B, S, {H * config.v_head_dim}) bf16 tensor")
+    ops.update(gamma_q=gq, gamma_kv=gkv, ckv_cache=ckv, kpe_cache=kpe, positions=pos_t, rope_freqs=rope_freqs,
+               input_gamma=input_gamma, residual=residual, attn_out=attn_out, max_context=int(mc),
+               eps=float(config.rms_norm_eps), softmax_scale=float(softmax_scale(config)), heads=H,
+               qk_nope=config.qk_nope_head_dim, v_dim=config.v_head_dim)
+    return ops
 
 
-def _run_mla(a: MlaArgs, device, stream: int, keep) -> None:
-    L = lib()
-    decode = a.seq_len == 1
-    need = (L.amla_mla_decode_workspace_bytes if decode else L.amla_mla_prefill_workspace_bytes)(a)
-    ws = workspace(device, need)
-    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-    rc = (L.amla_mla_decode if decode else L.amla_mla_prefill)(a, stream)
-    check(rc, "mla_decode" if decode else "mla_prefill")
-    del keep
+def _mla(ops: dict) -> torch.Tensor:
+    fn = torch.ops.amla.mla_decode if ops["hidden"].shape[1] == 1 else torch.ops.amla.mla_prefill
+    return fn(**ops)
 
 
 def mla_attention(hidden: torch.Tensor, attn_weights: dict, kv_cache: tuple, position, rope_freqs: torch.Tensor,
-                  config, *, max_context: int | None = None) -> torch.Tensor:
-    """inference/ops.py:100-183 on gfx950.
+                  config, *, max_context: int | None = None, attn_out: torch.Tensor | None = None) -> torch.Tensor:
+    """inference/ops.py:100-183 on gfx950 (``torch.ops.amla.mla_decode`` / ``mla_prefill``).
 
     S == 1 runs the absorbed decode; S > 1 the kv_b decompression + causal
     flash prefill.  Writes the raw new rows into ``kv_cache`` at
     [position, position+S) like the reference.  ``max_context`` (largest
-    position+S) is only needed when ``position`` is a device tensor.
+    position+S) is only needed when ``position`` is a device tensor.  When
+    ``attn_out`` ((B, S, heads * v_head_dim) bf16) is given, the per-head
+    attention output before o_proj is written into it.
     """
-    out = torch.empty_like(hidden)
-    a, pos_t = _fill_args(hidden, attn_weights, kv_cache, position, rope_freqs, config, out=out,
-                          max_context=max_context)
-    _run_mla(a, hidden.device, _stream_ptr(hidden), pos_t)
-    return out
+    return _mla(_mla_operands(hidden, attn_weights, kv_cache, position, rope_freqs, config,
+                              max_context=max_context, attn_out=attn_out))
 
 
 def mla_layer(hidden: torch.Tensor, input_layernorm: torch.Tensor, attn_weights: dict, kv_cache: tuple,
-              position, rope_freqs: torch.Tensor, config, *, max_context: int | None = None) -> torch.Tensor:
+              position, rope_freqs: torch.Tensor, config, *, max_context: int | None = None,
+              attn_out: torch.Tensor | None = None) -> torch.Tensor:
     """Attention half of transformer_layer (inference/forward.py:92-94), fused:
     ``hidden + mla_attention(rms_norm(hidden, input_layernorm), ...)`` with the
-    norm in the first projection's input and the bf16 residual add in o_proj's
+    norm as the layer's first launch and the bf16 residual add in o_proj's
     epilogue."""
-    _need(input_layernorm, "input_layernorm", BF16, hidden.device)
-    out = torch.empty_like(hidden)
-    a, pos_t = _fill_args(hidden, attn_weights, kv_cache, position, rope_freqs, config, out=out,
-                          input_gamma=input_layernorm, residual=hidden, max_context=max_context)
-    _run_mla(a, hidden.device, _stream_ptr(hidden), pos_t)
-    return out
+    return _mla(_mla_operands(hidden, attn_weights, kv_cache, position, rope_freqs, config,
+                              input_gamma=input_layernorm, residual=hidden, max_context=max_context,
+                              attn_out=attn_out))
 
 
 # ------------------------------------------------------------------ FFN / MoE

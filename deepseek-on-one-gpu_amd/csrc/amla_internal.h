@@ -43,6 +43,8 @@ struct GemvParams {
   int kv_lora, rope;
   const int32_t *pos;   // per-m positions (QKVA, QROPE); m indexes (b * S + s)
   int seq_len;          // S: position of row m is pos[m / S] + m % S
+  int max_rows;         // QKVA: cache rows per sequence (stores to rows >= max_rows are dropped)
+  int rope_rows;        // QROPE: rows of rope_table (positions are clamped to rope_rows - 1)
   const float *rope_table;
   int head_dim, nope;   // QROPE
   float *part;          // fp32 partial sums of the K parts (GemvPlan::part_bytes), else unused
@@ -96,5 +98,12 @@ int launch_gemm(const GemvParams &p, int mode, hipStream_t stream);
 
 int launch_rms_norm(const uint16_t *x, int64_t rows, int64_t dim, int64_t ldx, const uint16_t *gamma,
                     float eps, uint16_t *y, int64_t ldy, hipStream_t stream);
+
+// Host checks shared by the MLA entry points (dimensions, null pointers,
+// alignment, context bounds); returns AMLA_OK or the failure code.
+int check_mla_common(const amla_mla_args *a, const char *who);
+// Rows of context the kernels may read for these args: max_context when set
+// (> 0), else max_seq.
+inline int mla_context_bound(const amla_mla_args &a) { return a.max_context > 0 ? a.max_context : a.max_seq; }
 
 }  // namespace amla

@@ -423,14 +423,17 @@ __global__ __launch_bounds__(256) void move_rows_kernel(const uint16_t *__restri
 
 struct MoeLayout {
   int chunk_tokens;
-  size_t lists, xs, ys, gu, h, part, total;
+  size_t lists, xs, ys, gu, h, part, part_bytes, total;
 };
 
 static MoeLayout moe_layout(int64_t m, int64_t d, int top_k, int64_t n) {
   MoeLayout L;
   L.chunk_tokens = (int)std::min<int64_t>(m, (m * top_k <= MOE_ARG_SLOTS ? MOE_ARG_SLOTS : MOE_MAX_SLOTS) / top_k);
   const size_t slots = (size_t)L.chunk_tokens * top_k;
-  const int mg = std::min(L.chunk_tokens, 64);  // largest expert group on the skinny path
+  // largest expert group on the skinny path: any run of one expert up to 64
+  // slots (a token may list an expert more than once, so a run can be longer
+  // than the chunk's token count); the K-part count grows with the group size
+  const int mg = (int)std::min<size_t>(slots, 64);
   size_t off = 0;
   L.lists = off;
   off = align_up(off + (slots > MOE_ARG_SLOTS ? 2 * slots * 4 : 0), 256);
@@ -447,7 +450,8 @@ static MoeLayout moe_layout(int64_t m, int64_t d, int top_k, int64_t n) {
   const GemvPlan a = plan_gemv(mg, (int)(2 * n), (int)d), b = plan_gemv(mg, (int)d, (int)n);
   const size_t pa = a.kparts > 1 ? (size_t)a.kparts * slots * 2 * n * 4 : 0;
   const size_t pb = b.kparts > 1 ? (size_t)b.kparts * slots * d * 4 : 0;
-  off = align_up(off + std::max(pa, pb), 256);
+  L.part_bytes = std::max(pa, pb);
+  off = align_up(off + L.part_bytes, 256);
   L.total = off;
   return L;
 }
@@ -577,6 +581,9 @@ int amla_moe_experts(const void *hidden, int64_t m, int64_t d, int top_k, const 
       }
       const GemvPlan &pl = pass == 0 ? plan_g : plan_d;
       const GemvParams &base = pass == 0 ? pg : pd;
+      if (pl.kparts > 1 && (size_t)pl.kparts * ns * base.N * 4 > L.part_bytes)
+        return fail(AMLA_EWORKSPACE, "moe_experts: K-part sums (%d parts x %d slots x %d) exceed the workspace plan",
+                    pl.kparts, ns, base.N);
       GemvGroups gr;
       gr.n = 0;
       gr.units = 0;

@@ -111,6 +111,7 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
     } else {
       const int b = m / p.seq_len;
       const int64_t row = row_position(p, m);
+      if (row >= p.max_rows) return;  // a device position past the cache: nothing is written
       const int nn = n - p.n_split;
       uint16_t *dst = nn < p.kv_lora
                           ? p.ckv + b * p.ckv_bstride + row * p.kv_lora + nn
@@ -122,7 +123,7 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
     const int d = n % p.head_dim;
     if (d >= p.nope) {
       const int i = (d - p.nope) >> 1;
-      const int64_t row = row_position(p, m);
+      const int64_t row = min(row_position(p, m), p.rope_rows - 1);  // in bounds for any device position
       const f32x4 cs = *reinterpret_cast<const f32x4 *>(p.rope_table + (row * (p.rope >> 1) + i) * 2);
       // (x0 + i x1) * (c + i s), each product rounded, no fused multiply-add
       const float r0 = __fsub_rn(__fmul_rn(a0, cs.x), __fmul_rn(a1, cs.y));
@@ -572,6 +573,8 @@ int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t 
     return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM: K=%d is too long for M=%d (more than %d K parts)", p0.K, p0.M,
                 GEMV_MAX_PARTS);
   if (pl.kparts > 1 && !p0.part) return fail(AMLA_EWORKSPACE, "skinny fp8 GEMM: missing partial-sum workspace");
+  if ((mode == GEMV_QKVA && p0.max_rows <= 0) || (mode == GEMV_QROPE && p0.rope_rows <= 0))
+    return fail(AMLA_EINVAL, "skinny fp8 GEMM: cache rows / rope rows of the epilogue not set");
   if (p0.w1 && p0.n_split % 128)
     return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM: the first weight segment must be a multiple of 128 rows");
   const int MT = p0.M <= 16 ? 1 : (p0.M <= 32 ? 2 : 4);
@@ -725,7 +728,7 @@ using namespace amla;
 
 extern "C" {
 
-int amla_abi_version(void) { return 101; }
+int amla_abi_version(void) { return 102; }
 
 const char *amla_last_error(void) { return g_last_error.c_str(); }
 

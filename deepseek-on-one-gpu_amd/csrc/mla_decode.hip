@@ -133,7 +133,8 @@ struct AttnParams {
   const uint16_t *kpe;   // cache (B_alloc, max_seq, 64)
   int64_t ckv_bstride, kpe_bstride;  // elements per sequence
   const float *rope_table;           // (rows, 32, 2)
-  const int32_t *pos;                // decode position per sequence; context T = pos + 1
+  const int32_t *pos;                // decode position per sequence; context T = min(pos + 1, tmax)
+  int tmax;                          // context bound (rows of cache and rope table that may be read)
   int splits, tiles_per_split;
   float scale_log2;  // softmax scale * log2(e)
   float eps;
@@ -312,7 +313,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
-  const int T = p.pos[b] + 1;
+  const int T = min(p.pos[b] + 1, p.tmax);
   const int ntiles = (T + TT - 1) / TT;
   const int tb = split * p.tiles_per_split;
   const int te = min(tb + p.tiles_per_split, ntiles);
@@ -658,7 +659,7 @@ AMLA_DEV float block_reduce(float v, float *red, bool is_max) {
 AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, int split, float *qs, float *ps, float *red,
                               float &m_out, float &l_out, float &o0, float &o1) {
   const int tid = threadIdx.x;
-  const int T = p.pos[b] + 1;
+  const int T = min(p.pos[b] + 1, p.tmax);
   const int t0 = split * p.tiles_per_split * TT;
   const int t1 = min(t0 + p.tiles_per_split * TT, T);
   __syncthreads();
@@ -893,7 +894,7 @@ static DecodeLayout decode_layout(const amla_mla_args &a) {
   L.pa = plan_gemv(B, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
   L.pb = plan_gemv(B, a.heads * HD, a.q_lora);
   L.po = plan_gemv(B, a.hidden, a.heads * a.v_dim);
-  const int maxT = a.max_context > 0 ? a.max_context : a.max_seq;
+  const int maxT = mla_context_bound(a);
   const int ntiles = (maxT + TT - 1) / TT;
   int splits = (256 + B - 1) / B;
   splits = std::max(1, std::min(splits, (ntiles + 1) / 2));
@@ -913,7 +914,7 @@ static DecodeLayout decode_layout(const amla_mla_args &a) {
   return L;
 }
 
-static int check_common(const amla_mla_args *a, const char *who) {
+int check_mla_common(const amla_mla_args *a, const char *who) {
   if (!a) return fail(AMLA_EINVAL, "%s: null args", who);
   if (a->heads != HEADS || a->kv_lora != LORA || a->qk_rope != ROPE || a->qk_nope != NOPE || a->v_dim != VD)
     return fail(AMLA_EUNSUPPORTED,
@@ -923,13 +924,20 @@ static int check_common(const amla_mla_args *a, const char *who) {
     return fail(AMLA_EUNSUPPORTED, "%s: hidden and q_lora must be positive multiples of 128", who);
   if (a->batch <= 0 || a->seq_len <= 0) return fail(AMLA_EINVAL, "%s: batch and seq_len must be >= 1", who);
   if (a->max_seq <= 0 || a->rope_rows <= 0) return fail(AMLA_EINVAL, "%s: max_seq / rope_rows must be >= 1", who);
+  if (a->max_context < 0) return fail(AMLA_EINVAL, "%s: max_context must be >= 0 (0: max_seq)", who);
+  const int bound = mla_context_bound(*a);
+  if (bound > a->max_seq || bound > a->rope_rows)
+    return fail(AMLA_EINVAL, "%s: context bound %d exceeds the cache (%d rows) or the rope table (%d rows)", who,
+                bound, a->max_seq, a->rope_rows);
+  if (bound < a->seq_len)
+    return fail(AMLA_EINVAL, "%s: context bound %d is below seq_len %d", who, bound, a->seq_len);
   const void *ptrs[] = {a->positions, a->hidden_states, a->out, a->w_q_a, a->s_q_a, a->w_q_b, a->s_q_b,
                         a->w_kv_a, a->s_kv_a, a->w_kv_b, a->s_kv_b, a->w_o, a->s_o, a->gamma_q,
                         a->gamma_kv, a->ckv_cache, a->kpe_cache, a->rope_table, a->workspace};
   for (const void *q : ptrs)
     if (!q) return fail(AMLA_EINVAL, "%s: a required pointer is null", who);
   if (!aligned16(a->hidden_states) || !aligned16(a->ckv_cache) || !aligned16(a->kpe_cache) ||
-      !aligned16(a->rope_table) || !aligned16(a->out) || !aligned16(a->workspace))
+      !aligned16(a->rope_table) || !aligned16(a->out) || !aligned16(a->workspace) || !aligned16(a->attn_out))
     return fail(AMLA_EINVAL, "%s: activations, caches, rope table and workspace must be 16-byte aligned", who);
   return AMLA_OK;
 }
@@ -943,7 +951,7 @@ static inline void mark(hipEvent_t const *ev, int i, hipStream_t st) {
 }
 
 static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const *ev = nullptr) {
-  int rc = check_common(a, "mla_decode");
+  int rc = check_mla_common(a, "mla_decode");
   if (rc) return rc;
   if (a->seq_len != 1) return fail(AMLA_EINVAL, "mla_decode: seq_len must be 1 (use mla_prefill)");
   if (a->batch > 64) return fail(AMLA_EUNSUPPORTED, "mla_decode: batch > 64 not supported");
@@ -979,7 +987,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pa.ckv = reinterpret_cast<uint16_t *>(a->ckv_cache);
   pa.kpe = reinterpret_cast<uint16_t *>(a->kpe_cache);
   pa.ckv_bstride = (int64_t)a->max_seq * LORA; pa.kpe_bstride = (int64_t)a->max_seq * ROPE;
-  pa.kv_lora = LORA; pa.rope = ROPE; pa.pos = a->positions; pa.seq_len = 1;
+  pa.kv_lora = LORA; pa.rope = ROPE; pa.pos = a->positions; pa.seq_len = 1; pa.max_rows = a->max_seq;
   pa.part = reinterpret_cast<float *>(ws + L.lin);
   // 2. q_a_layernorm (inference/ops.py:130): fused into the K-part finish, or
   //    a row norm in place when the GEMV needs no finishing pass
@@ -1000,7 +1008,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pb.w0 = reinterpret_cast<const uint8_t *>(a->w_q_b); pb.s0 = a->s_q_b;
   pb.N = a->heads * HD; pb.K = a->q_lora; pb.n_split = pb.N;
   pb.y = q; pb.ldy = pb.N;
-  pb.pos = a->positions; pb.seq_len = 1; pb.rope = ROPE; pb.rope_table = a->rope_table;
+  pb.pos = a->positions; pb.seq_len = 1; pb.rope = ROPE; pb.rope_table = a->rope_table; pb.rope_rows = a->rope_rows;
   pb.head_dim = HD; pb.nope = a->qk_nope;
   pb.part = reinterpret_cast<float *>(ws + L.lin);
   if ((rc = launch_gemv(pb, GEMV_QROPE, L.pb, st))) return rc;
@@ -1019,7 +1027,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   ap.ckv = reinterpret_cast<const uint16_t *>(a->ckv_cache);
   ap.kpe = reinterpret_cast<const uint16_t *>(a->kpe_cache);
   ap.ckv_bstride = (int64_t)a->max_seq * LORA; ap.kpe_bstride = (int64_t)a->max_seq * ROPE;
-  ap.rope_table = a->rope_table; ap.pos = a->positions;
+  ap.rope_table = a->rope_table; ap.pos = a->positions; ap.tmax = mla_context_bound(*a);
   ap.splits = L.splits; ap.tiles_per_split = L.tiles_per_split;
   ap.scale_log2 = a->softmax_scale * 1.4426950408889634f;
   ap.eps = a->eps;
@@ -1030,7 +1038,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
 
   // 6. merge splits, W_UV
   mark(ev, 5, st);
-  uint16_t *attn = reinterpret_cast<uint16_t *>(ws + L.attn);
+  uint16_t *attn = reinterpret_cast<uint16_t *>(a->attn_out ? a->attn_out : ws + L.attn);
   combine_uv_kernel<<<dim3(HEADS, (B + 3) / 4), 256, 0, st>>>(ap, reinterpret_cast<const uint8_t *>(a->w_kv_b),
                                                               a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv),
                                                               B, attn);
@@ -1053,6 +1061,16 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
 
 static bool g_attr_set = false;
 
+static void set_attn_attr() {
+  if (!g_attr_set) {
+    // Opt in to more than 64 KB of dynamic LDS (gfx950 has 160 KB per CU).
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)ATTN_LDS);
+    (void)hipGetLastError();
+    g_attr_set = true;
+  }
+}
+
 }  // namespace amla
 
 using namespace amla;
@@ -1065,13 +1083,7 @@ size_t amla_mla_decode_workspace_bytes(const amla_mla_args *a) {
 }
 
 int amla_mla_decode(const amla_mla_args *a, void *stream) {
-  if (!g_attr_set) {
-    // Opt in to more than 64 KB of dynamic LDS (gfx950 has 160 KB per CU).
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)ATTN_LDS);
-    (void)hipGetLastError();
-    g_attr_set = true;
-  }
+  set_attn_attr();
   return decode_impl(a, reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -1079,12 +1091,7 @@ int amla_mla_decode_profiled(const amla_mla_args *a, void *stream, void *const *
   if (!events) return fail(AMLA_EINVAL, "mla_decode_profiled: null events");
   for (int i = 0; i <= NSTAGE; ++i)
     if (!events[i]) return fail(AMLA_EINVAL, "mla_decode_profiled: null event %d", i);
-  if (!g_attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)ATTN_LDS);
-    (void)hipGetLastError();
-    g_attr_set = true;
-  }
+  set_attn_attr();
   return decode_impl(a, reinterpret_cast<hipStream_t>(stream), reinterpret_cast<hipEvent_t const *>(events));
 }
 

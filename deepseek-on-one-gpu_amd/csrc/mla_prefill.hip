@@ -40,6 +40,7 @@ AMLA_DEV void pstore4(const GemvParams &p, int m, int n, f32x4 v) {
     } else {
       const int b = m / p.seq_len;
       const int64_t row = prow_position(p, m);
+      if (row >= p.max_rows) return;  // a device position past the cache: nothing is written
       const int nn = n - p.n_split;
       uint16_t *dst = nn < p.kv_lora ? p.ckv + b * p.ckv_bstride + row * p.kv_lora + nn
                                      : p.kpe + b * p.kpe_bstride + row * p.rope + (nn - p.kv_lora);
@@ -50,7 +51,7 @@ AMLA_DEV void pstore4(const GemvParams &p, int m, int n, f32x4 v) {
     const int d = n % p.head_dim;
     if (d >= p.nope) {
       const int i = (d - p.nope) >> 1;
-      const int64_t row = prow_position(p, m);
+      const int64_t row = min(prow_position(p, m), p.rope_rows - 1);  // in bounds for any device position
       const f32x4 cs = *reinterpret_cast<const f32x4 *>(p.rope_table + (row * (p.rope >> 1) + i) * 2);
       const float r0 = __fsub_rn(__fmul_rn(a0, cs.x), __fmul_rn(a1, cs.y));
       const float r1 = __fadd_rn(__fmul_rn(a0, cs.y), __fmul_rn(a1, cs.x));
@@ -83,6 +84,7 @@ AMLA_DEV void pstore8(const GemvParams &p, int m, int n, u32x4 v) {
     } else {
       const int b = m / p.seq_len;
       const int64_t row = prow_position(p, m);
+      if (row >= p.max_rows) return;  // a device position past the cache: nothing is written
       const int nn = n - p.n_split;
       uint16_t *dst = nn < p.kv_lora ? p.ckv + b * p.ckv_bstride + row * p.kv_lora + nn
                                      : p.kpe + b * p.kpe_bstride + row * p.rope + (nn - p.kv_lora);
@@ -92,7 +94,7 @@ AMLA_DEV void pstore8(const GemvParams &p, int m, int n, u32x4 v) {
     const int d = n % p.head_dim;
     u32x4 o = v;
     if (d >= p.nope) {
-      const int64_t row = prow_position(p, m);
+      const int64_t row = min(prow_position(p, m), p.rope_rows - 1);  // in bounds for any device position
       const float *tab = p.rope_table + (row * (p.rope >> 1) + ((d - p.nope) >> 1)) * 2;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -318,6 +320,8 @@ size_t gemm_ws_bytes(int, int, int) { return 0; }
 int launch_gemm(const GemvParams &p, int mode, hipStream_t st) {
   if (p.K % 128 || p.N % 4) return fail(AMLA_EUNSUPPORTED, "fp8 GEMM needs K %% 128 == 0 and N %% 4 == 0");
   if (p.ldx % 8) return fail(AMLA_EUNSUPPORTED, "fp8 GEMM needs 16-byte aligned activation rows");
+  if ((mode == GEMV_QKVA && p.max_rows <= 0) || (mode == GEMV_QROPE && p.rope_rows <= 0))
+    return fail(AMLA_EINVAL, "fp8 GEMM: cache rows / rope rows of the epilogue not set");
   if ((mode == GEMV_QKVA || p.w1) && p.n_split % G_BN)
     return fail(AMLA_EUNSUPPORTED, "fp8 GEMM: the first weight segment must be a multiple of 256 rows");
   static bool attr_set[4] = {false, false, false, false};  // dynamic LDS above 64 KB, once per mode
@@ -372,6 +376,7 @@ struct FlashParams {
   uint16_t *out;          // (rows, H*128)
   const int32_t *pos;
   int b, S, nqb;  // nqb: query blocks of 256 per head
+  int tmax;       // key rows held (first positions are clamped to tmax - S)
   float scale_log2;
 };
 
@@ -485,7 +490,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j32 = lane & 31, hh = lane >> 5;
-  const int pos0 = p.pos[p.b];
+  const int pos0 = min(p.pos[p.b], p.tmax - p.S);  // keys [0, pos0 + S) are in the workspace
   const int s_begin = qblk * F_QB;
   const int s_wave = s_begin + wave * F_QW;
   const int s_last_blk = min(s_begin + F_QB, p.S) - 1;
@@ -812,7 +817,7 @@ static PrefillLayout prefill_layout(const amla_mla_args &a) {
   PrefillLayout L = {};
   const size_t M = (size_t)a.batch * a.seq_len;
   const int HD = a.qk_nope + a.qk_rope;
-  L.Tmax = a.max_context > 0 ? std::min(a.max_context, a.max_seq) : a.max_seq;
+  L.Tmax = std::min(mla_context_bound(a), a.max_seq);
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes, 256); return o; };
   L.xn = take(M * a.hidden * 2);
@@ -858,26 +863,14 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st);
 namespace amla {
 
 int prefill_impl(const amla_mla_args *a, hipStream_t st) {
-  if (!a) return fail(AMLA_EINVAL, "mla_prefill: null args");
-  if (a->heads != P_H || a->kv_lora != 512 || a->qk_rope != P_ROPE || a->qk_nope != P_NOPE || a->v_dim != P_V)
-    return fail(AMLA_EUNSUPPORTED, "mla_prefill: kernels are built for R1 head dimensions");
-  if (a->batch <= 0 || a->seq_len <= 0) return fail(AMLA_EINVAL, "mla_prefill: batch and seq_len must be >= 1");
-  if (a->hidden <= 0 || a->hidden % 128 || a->q_lora <= 0 || a->q_lora % 128)
-    return fail(AMLA_EUNSUPPORTED, "mla_prefill: hidden and q_lora must be positive multiples of 128");
-  const void *ptrs[] = {a->positions, a->hidden_states, a->out, a->w_q_a, a->s_q_a, a->w_q_b, a->s_q_b,
-                        a->w_kv_a, a->s_kv_a, a->w_kv_b, a->s_kv_b, a->w_o, a->s_o, a->gamma_q,
-                        a->gamma_kv, a->ckv_cache, a->kpe_cache, a->rope_table, a->workspace};
-  for (const void *q : ptrs)
-    if (!q) return fail(AMLA_EINVAL, "mla_prefill: a required pointer is null");
+  int rc = check_mla_common(a, "mla_prefill");
+  if (rc) return rc;
   const PrefillLayout L = prefill_layout(*a);
-  if (a->max_context < a->seq_len)
-    return fail(AMLA_EINVAL, "mla_prefill: max_context (%d) must be >= seq_len (%d)", a->max_context, a->seq_len);
   if (a->workspace_bytes < L.total)
     return fail(AMLA_EWORKSPACE, "mla_prefill: workspace %zu bytes < %zu needed", a->workspace_bytes, L.total);
   char *ws = reinterpret_cast<char *>(a->workspace);
   const int B = a->batch, S = a->seq_len, M = B * S;
   const int HD = a->qk_nope + a->qk_rope;
-  int rc;
 
   const uint16_t *x = reinterpret_cast<const uint16_t *>(a->hidden_states);
   if (a->input_gamma) {
@@ -893,7 +886,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   uint16_t *kvn = reinterpret_cast<uint16_t *>(ws + L.kvn);
   uint16_t *kpe = reinterpret_cast<uint16_t *>(ws + L.kpe);
   uint16_t *kvb = reinterpret_cast<uint16_t *>(ws + L.kvb);
-  uint16_t *attn = reinterpret_cast<uint16_t *>(ws + L.attn);
+  uint16_t *attn = reinterpret_cast<uint16_t *>(a->attn_out ? a->attn_out : ws + L.attn);
 
   GemvParams pa = {};
   pa.part = reinterpret_cast<float *>(ws + L.lin);
@@ -905,7 +898,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   pa.ckv = reinterpret_cast<uint16_t *>(a->ckv_cache);
   pa.kpe = reinterpret_cast<uint16_t *>(a->kpe_cache);
   pa.ckv_bstride = (int64_t)a->max_seq * a->kv_lora; pa.kpe_bstride = (int64_t)a->max_seq * a->qk_rope;
-  pa.kv_lora = a->kv_lora; pa.rope = a->qk_rope; pa.pos = a->positions; pa.seq_len = S;
+  pa.kv_lora = a->kv_lora; pa.rope = a->qk_rope; pa.pos = a->positions; pa.seq_len = S; pa.max_rows = a->max_seq;
   if ((rc = run_linear(pa, GEMV_QKVA, st))) return rc;
 
   if ((rc = launch_rms_norm(qa, M, a->q_lora, a->q_lora, reinterpret_cast<const uint16_t *>(a->gamma_q), a->eps,
@@ -919,12 +912,13 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   pb.N = a->heads * HD; pb.K = a->q_lora; pb.n_split = pb.N;
   pb.y = q; pb.ldy = pb.N;
   pb.pos = a->positions; pb.seq_len = S; pb.rope = a->qk_rope; pb.rope_table = a->rope_table;
+  pb.rope_rows = a->rope_rows;
   pb.head_dim = HD; pb.nope = a->qk_nope;
   if ((rc = run_linear(pb, GEMV_QROPE, st))) return rc;
 
   const int T = L.Tmax;
   FlashParams fp = {};
-  fp.q = q; fp.kvb = kvb; fp.kpe = kpe; fp.out = attn; fp.pos = a->positions; fp.S = S;
+  fp.q = q; fp.kvb = kvb; fp.kpe = kpe; fp.out = attn; fp.pos = a->positions; fp.S = S; fp.tmax = T;
   fp.scale_log2 = a->softmax_scale * 1.4426950408889634f;
   for (int b = 0; b < B; ++b) {
     const uint16_t *ckv_b = reinterpret_cast<const uint16_t *>(a->ckv_cache) + (size_t)b * a->max_seq * a->kv_lora;

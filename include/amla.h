@@ -115,6 +115,11 @@ typedef struct amla_mla_args {
   const float *rope_table;  /* (rope_rows, qk_rope/2, 2) fp32 cos/sin */
   void *workspace;
   size_t workspace_bytes;
+  /* optional (B, S, heads * v_dim) bf16, 16-byte aligned: when set, the
+   * per-head attention output before o_proj (the `out` of inference/ops.py:182,
+   * heads-major columns h * v_dim + d) is written here instead of the workspace,
+   * and o_proj reads it from here. */
+  void *attn_out;
 } amla_mla_args;
 
 /* Replaces mla_attention(...) for S == 1, inference/ops.py:100-183, computed in

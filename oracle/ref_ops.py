@@ -113,6 +113,15 @@ def _split_heads(t: torch.Tensor, H: int) -> torch.Tensor:
 
 def mla_attention(hidden, attn_weights, kv_cache, position: int, rope_freqs, cfg) -> torch.Tensor:
     """inference/ops.py:100-183 (naive MLA; mutates kv_cache rows [position, position+S))."""
+    return mla_attention_parts(hidden, attn_weights, kv_cache, position, rope_freqs, cfg)[1]
+
+
+def mla_attention_parts(hidden, attn_weights, kv_cache, position: int, rope_freqs, cfg):
+    """inference/ops.py:100-183 returning (per-head output before o_proj (B, S, H*v), final output).
+
+    The first tensor is the ``out`` of inference/ops.py:182 (heads-major
+    columns h*v_head_dim + d), the input of the o_proj linear at :183.
+    """
     B, S, _ = hidden.shape
     H = cfg.num_attention_heads
     nope, rope_d, vd, lora = cfg.qk_nope_head_dim, cfg.qk_rope_head_dim, cfg.v_head_dim, cfg.kv_lora_rank
@@ -157,7 +166,7 @@ def mla_attention(hidden, attn_weights, kv_cache, position: int, rope_freqs, cfg
     probs = torch.softmax(scores, dim=-1, dtype=torch.float32).to(hidden.dtype)   # ops.py:179
     out = torch.matmul(probs, v)                                                 # ops.py:180
     out = out.permute(0, 2, 1, 3).reshape(B, S, H * vd)                          # ops.py:182
-    return fp8_linear(out, *attn_weights["o_proj"])                              # ops.py:183
+    return out, fp8_linear(out, *attn_weights["o_proj"])                         # ops.py:183
 
 
 def mla_attention_per_sequence(hidden, attn_weights, kv_cache, positions, rope_freqs, cfg) -> torch.Tensor:
@@ -167,12 +176,19 @@ def mla_attention_per_sequence(hidden, attn_weights, kv_cache, positions, rope_f
     (inference/ops.py:104, :140-145), so per-sequence positions can only be
     expressed as this loop.
     """
+    return mla_attention_per_sequence_parts(hidden, attn_weights, kv_cache, positions, rope_freqs, cfg)[1]
+
+
+def mla_attention_per_sequence_parts(hidden, attn_weights, kv_cache, positions, rope_freqs, cfg):
+    """mla_attention_per_sequence returning (per-head output before o_proj, final output)."""
     ckv, kpe = kv_cache
-    outs = []
+    heads, outs = [], []
     for b, p in enumerate(positions):
-        outs.append(mla_attention(hidden[b:b + 1], attn_weights, (ckv[b:b + 1], kpe[b:b + 1]),
-                                  int(p), rope_freqs, cfg))
-    return torch.cat(outs, dim=0)
+        a, o = mla_attention_parts(hidden[b:b + 1], attn_weights, (ckv[b:b + 1], kpe[b:b + 1]), int(p),
+                                   rope_freqs, cfg)
+        heads.append(a)
+        outs.append(o)
+    return torch.cat(heads, dim=0), torch.cat(outs, dim=0)
 
 
 def transformer_layer_attention(hidden, input_layernorm, attn_weights, kv_cache, position, rope_freqs, cfg):

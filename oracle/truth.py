@@ -53,6 +53,11 @@ def project_queries_f64(hidden, aw, position, rope_freqs, cfg):
 
 def mla_naive_f64(hidden, aw, ckv_rows, kpe_rows, position, rope_freqs, cfg):
     """Reference math in fp64.  ckv_rows/kpe_rows: (B, T, .) cache contents *after* the new rows."""
+    return mla_naive_parts_f64(hidden, aw, ckv_rows, kpe_rows, position, rope_freqs, cfg)[1]
+
+
+def mla_naive_parts_f64(hidden, aw, ckv_rows, kpe_rows, position, rope_freqs, cfg):
+    """mla_naive_f64 returning (per-head output before o_proj (B, S, H*v), output (B, S, hidden))."""
     B, S, _ = hidden.shape
     H, nope, vd = cfg.num_attention_heads, cfg.qk_nope_head_dim, cfg.v_head_dim
     T = position + S
@@ -69,11 +74,16 @@ def mla_naive_f64(hidden, aw, ckv_rows, kpe_rows, position, rope_freqs, cfg):
         s = s.masked_fill(j > i, float("-inf"))
     p = torch.softmax(s, -1)
     o = (p @ v).permute(0, 2, 1, 3).reshape(B, S, H * vd)
-    return o @ _w64(aw["o_proj"]).T
+    return o, o @ _w64(aw["o_proj"]).T
 
 
 def mla_decode_absorbed_f64(hidden, aw, ckv_rows, kpe_rows, positions, rope_freqs, cfg):
     """Absorbed decode (S = 1), one position per sequence; returns (B, 1, hidden) fp64."""
+    return mla_decode_absorbed_parts_f64(hidden, aw, ckv_rows, kpe_rows, positions, rope_freqs, cfg)[1]
+
+
+def mla_decode_absorbed_parts_f64(hidden, aw, ckv_rows, kpe_rows, positions, rope_freqs, cfg):
+    """Absorbed decode in fp64: (per-head output before o_proj (B, 1, H*v), output (B, 1, hidden))."""
     B = hidden.shape[0]
     H, nope, vd, lora = cfg.num_attention_heads, cfg.qk_nope_head_dim, cfg.v_head_dim, cfg.kv_lora_rank
     gamma = aw["kv_a_layernorm"].double()
@@ -81,19 +91,54 @@ def mla_decode_absorbed_f64(hidden, aw, ckv_rows, kpe_rows, positions, rope_freq
     w_uk, w_uv = wkvb[:, :nope], wkvb[:, nope:]
     wo = _w64(aw["o_proj"])
     sigma = yarn_get_mscale(cfg.rope_scaling_factor, cfg.rope_scaling_mscale_all_dim) / math.sqrt(cfg.qk_head_dim)
-    outs = []
+    heads, outs = [], []
     for b in range(B):
         p = int(positions[b])
         T = p + 1
         q_nope, q_pe, _ = project_queries_f64(hidden[b:b + 1], aw, p, rope_freqs, cfg)
         q_nope, q_pe = q_nope[0, :, 0], q_pe[0, :, 0]                        # (H, nope), (H, rope)
-        qt = torch.einsum("hd,hdc->hc", q_nope, w_uk) * gamma                # (H, lora)
-        c = ckv_rows[b, :T].double()
-        r = torch.rsqrt(c.pow(2).mean(-1) + cfg.rms_norm_eps)                # (T,)
-        kpe = _rope64(kpe_rows[b, :T].double(), rope_freqs[:T])              # (T, rope)
-        s = sigma * (r[None] * (qt @ c.T) + q_pe @ kpe.T)                    # (H, T)
-        w = torch.softmax(s, -1)
-        lat = (w * r[None]) @ c * gamma                                      # (H, lora)
-        o = torch.einsum("hvc,hc->hv", w_uv, lat).reshape(1, H * vd)
+        o = _absorbed_row(q_nope, q_pe, ckv_rows[b, :T], kpe_rows[b, :T], rope_freqs, w_uk, w_uv, gamma, sigma,
+                          cfg.rms_norm_eps).reshape(1, H * vd)
+        heads.append(o)
         outs.append(o @ wo.T)
-    return torch.stack(outs, 0)
+    return torch.stack(heads, 0), torch.stack(outs, 0)
+
+
+def _absorbed_row(q_nope, q_pe, ckv, kpe, rope_freqs, w_uk, w_uv, gamma, sigma, eps):
+    """One query (H heads) over the cache rows ckv/kpe (T, .), absorbed form in fp64: (H, v)."""
+    T = ckv.shape[0]
+    qt = torch.einsum("hd,hdc->hc", q_nope, w_uk) * gamma                    # (H, lora)
+    c = ckv.double()
+    r = torch.rsqrt(c.pow(2).mean(-1) + eps)                                 # (T,)
+    kpe = _rope64(kpe.double(), rope_freqs[:T])                              # (T, rope)
+    s = sigma * (r[None] * (qt @ c.T) + q_pe @ kpe.T)                        # (H, T)
+    w = torch.softmax(s, -1)
+    lat = (w * r[None]) @ c * gamma                                          # (H, lora)
+    return torch.einsum("hvc,hc->hv", w_uv, lat)
+
+
+def mla_prefill_rows_f64(hidden, aw, ckv_rows, kpe_rows, position, rows, rope_freqs, cfg):
+    """Exact outputs of chosen query rows of a causal prefill of B = 1 sequence.
+
+    Query row i (position ``position + i``) attends to cache rows
+    [0, position + i]; ckv_rows / kpe_rows hold the cache after the new rows
+    were written.  Returns (per-head outputs (len(rows), H*v), outputs
+    (len(rows), hidden)), fp64.  The absorbed form equals the naive one in exact
+    arithmetic (checked by tests/test_oracle.py), and costs O(T) per row.
+    """
+    H, nope, vd, lora = cfg.num_attention_heads, cfg.qk_nope_head_dim, cfg.v_head_dim, cfg.kv_lora_rank
+    gamma = aw["kv_a_layernorm"].double()
+    wkvb = _w64(aw["kv_b_proj"]).view(H, nope + vd, lora)
+    w_uk, w_uv = wkvb[:, :nope], wkvb[:, nope:]
+    wo = _w64(aw["o_proj"])
+    sigma = yarn_get_mscale(cfg.rope_scaling_factor, cfg.rope_scaling_mscale_all_dim) / math.sqrt(cfg.qk_head_dim)
+    heads = []
+    for i in rows:
+        i = int(i)
+        T = position + i + 1
+        # queries are per row: only the chosen rows are projected (at their own positions)
+        q_nope, q_pe, _ = project_queries_f64(hidden[:1, i:i + 1], aw, position + i, rope_freqs, cfg)
+        heads.append(_absorbed_row(q_nope[0, :, 0], q_pe[0, :, 0], ckv_rows[0, :T], kpe_rows[0, :T], rope_freqs,
+                                   w_uk, w_uv, gamma, sigma, cfg.rms_norm_eps).reshape(H * vd))
+    h = torch.stack(heads, 0)
+    return h, h @ wo.T

@@ -233,3 +233,34 @@ def test_empty_inputs():
     idx, wt = ops.route(x, gw, cfg)
     assert idx.shape == (2, 0, 4) and wt.shape == (2, 0, 4)
     assert ops.moe_block(x, gw, w, {e: w for e in range(16)}, cfg).shape == (2, 0, d)
+
+
+def test_moe_experts_duplicate_indices_r1_shape():
+    """Every (token, k) slot of 8 tokens on one expert (a token may list an expert more than
+    once): one 64-row group at the R1 expert shape, whose K-part sums need the workspace
+    sized for 64 rows, not for the 8 tokens."""
+    print("[case] moe_experts duplicates m=8 K=8 R1 shape", flush=True)
+    E, K, m, d, i = 4, 8, 8, 7168, 2048
+    h = _x((m, d), "mxdup")
+    idx = torch.full((m, K), 3, dtype=torch.int64)
+    idx[0, 0] = 1                                           # one slot elsewhere: two runs
+    table = {e: _mlp(d, i, f"mxdup-expert{e}") for e in (1, 3)}
+    dev_table = {e: _dev(v) for e, v in table.items()}
+    ptrs = [(ctypes.c_void_p * E)() for _ in range(6)]
+    for e, v in dev_table.items():
+        for j, key in enumerate(("gate_proj", "up_proj", "down_proj")):
+            ptrs[2 * j][e] = v[key][0].data_ptr()
+            ptrs[2 * j + 1][e] = v[key][1].data_ptr()
+    hd = h.to(DEV)
+    eout = torch.empty(m, K, d, dtype=torch.bfloat16, device=DEV)
+    need = ops.lib().amla_moe_experts_workspace_bytes(m, d, K, i)
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    ops.check(ops.lib().amla_moe_experts(hd.data_ptr(), m, d, K, idx.data_ptr(), i, E,
+                                         *[ctypes.cast(t, ctypes.c_void_p) for t in ptrs], eout.data_ptr(),
+                                         ws.data_ptr(), need, ops._stream_ptr(hd)), "moe_experts")
+    torch.cuda.synchronize()
+    want = torch.empty(m, K, d, dtype=torch.bfloat16)
+    for e in (1, 3):
+        sel = (idx == e).nonzero()
+        want[sel[:, 0], sel[:, 1]] = F.expert_ffn(h[sel[:, 0]], table[e])
+    assert_parity(eout, want, "moe_experts duplicate indices")

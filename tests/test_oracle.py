@@ -259,3 +259,50 @@ def test_oracle_within_tolerance_of_truth():
     t = T.mla_naive_f64(hidden, lay.attn_weights, ckv, kpe, 33, tab, cfg)
     err = (y.double() - t).abs()
     assert torch.all(err <= 2e-2 + 2e-2 * t.abs())
+
+
+def test_absorbed_heads_equal_naive_heads_fp64():
+    """The per-head outputs (before o_proj) of the absorbed and naive fp64 forms agree."""
+    cfg = DeepSeekConfig(**SMALL)
+    lay = synth.make_layer(cfg, "absorb-heads")
+    positions = [9, 2]
+    ckv, kpe = synth.make_kv_cache(cfg, 2, 16, [p + 1 for p in positions], "absorb-heads")
+    hidden = synth.make_hidden(cfg, 2, 1, "absorb-heads")
+    tab = R.precompute_rope_freqs(cfg, 16)
+    heads, out = T.mla_decode_absorbed_parts_f64(hidden, lay.attn_weights, ckv, kpe, positions, tab, cfg)
+    for b, p in enumerate(positions):
+        nh, no = T.mla_naive_parts_f64(hidden[b:b + 1], lay.attn_weights, ckv[b:b + 1], kpe[b:b + 1], p, tab, cfg)
+        assert torch.allclose(heads[b], nh[0], rtol=1e-10, atol=1e-12)
+        assert torch.allclose(out[b], no[0], rtol=1e-10, atol=1e-12)
+    # o_proj of the heads is the output (the split of the two parts is where ops.py:182-183 puts it)
+    assert torch.allclose(heads @ T._w64(lay.attn_weights["o_proj"]).T, out, rtol=1e-12)
+
+
+def test_prefill_rows_f64_equal_naive_prefill():
+    """mla_prefill_rows_f64 (absorbed, per query row) equals rows of the naive fp64 causal prefill,
+    including a first position > 0 (a chunk after cached rows)."""
+    cfg = DeepSeekConfig(**SMALL)
+    lay = synth.make_layer(cfg, "rows")
+    S, p = 7, 4
+    ckv, kpe = synth.make_kv_cache(cfg, 1, 16, p + S, "rows")
+    hidden = synth.make_hidden(cfg, 1, S, "rows")
+    tab = R.precompute_rope_freqs(cfg, 16)
+    nh, no = T.mla_naive_parts_f64(hidden, lay.attn_weights, ckv, kpe, p, tab, cfg)
+    rows = [0, 3, 6]
+    h, o = T.mla_prefill_rows_f64(hidden, lay.attn_weights, ckv, kpe, p, rows, tab, cfg)
+    assert torch.allclose(h, nh[0, rows], rtol=1e-10, atol=1e-12)
+    assert torch.allclose(o, no[0, rows], rtol=1e-10, atol=1e-12)
+
+
+def test_parts_final_is_o_proj_of_heads(golden):
+    """mla_attention_parts: the final output is fp8_linear(heads, o_proj), equal to the
+    reference's own output bit for bit (golden vector), so the heads tensor is the
+    reference's pre-o_proj activation."""
+    tens, man = golden
+    e = man["r1_decode_t257"]
+    cfg, lay, hidden, ckv, kpe = _rebuild(e)
+    tab = R.precompute_rope_freqs(cfg, e["max_seq"])
+    heads, out = R.mla_attention_parts(hidden, lay.attn_weights, (ckv, kpe), e["position"], tab, cfg)
+    assert heads.shape == (1, 1, cfg.num_attention_heads * cfg.v_head_dim)
+    assert torch.equal(R.fp8_linear(heads, *lay.attn_weights["o_proj"]).view(torch.int16), out.view(torch.int16))
+    assert torch.equal(out.view(torch.int16), tens["r1_decode_t257.out"])
