@@ -25,6 +25,8 @@
 //   gemv  PLAIN/RESID : wo
 #include <math.h>
 
+#include <mutex>
+
 #include "amla_common.h"
 #include "amla_internal.h"
 
@@ -1071,6 +1073,48 @@ static void set_attn_attr() {
   }
 }
 
+// ---------------------------------------------------------------- no-allocation decode
+
+// Scratch of amla_mla_decode_noalloc: one array per device (each GPU the
+// library runs on holds its own copy, at its own address, until the process
+// ends).  In host code `scratch` names a host-side stand-in, never the
+// device memory: the device address comes from hipGetSymbolAddress, per
+// device, and only that address is passed to kernels.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)AMLA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static void *g_scratch_ptr[NOALLOC_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch array (looked up once per
+// device, with that device current); nullptr and a message on failure.
+static void *noalloc_scratch(int *rc) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *rc = fail((int)e, "mla_decode_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
+    *rc = fail(AMLA_EUNSUPPORTED, "mla_decode_noalloc: device %d beyond %d", dev, NOALLOC_MAX_DEVICES);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      *rc = fail(e != hipSuccess ? (int)e : AMLA_EINVAL, "mla_decode_noalloc: hipGetSymbolAddress failed: %s",
+                 hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *rc = AMLA_OK;
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace amla
 
 using namespace amla;
@@ -1085,6 +1129,23 @@ size_t amla_mla_decode_workspace_bytes(const amla_mla_args *a) {
 int amla_mla_decode(const amla_mla_args *a, void *stream) {
   set_attn_attr();
   return decode_impl(a, reinterpret_cast<hipStream_t>(stream));
+}
+
+int amla_mla_decode_noalloc(const amla_mla_args *a, void *stream) {
+  if (!a) return fail(AMLA_EINVAL, "mla_decode_noalloc: null args");
+  if (a->batch <= 0) return fail(AMLA_EINVAL, "mla_decode_noalloc: batch must be >= 1");
+  const size_t need = decode_layout(*a).total;
+  if (need > NOALLOC_SCRATCH_BYTES)
+    return fail(AMLA_EWORKSPACE, "mla_decode_noalloc: needs %zu bytes of scratch, the static array holds %zu",
+                need, NOALLOC_SCRATCH_BYTES);
+  int rc = AMLA_OK;
+  void *ptr = noalloc_scratch(&rc);
+  if (!ptr) return rc;
+  amla_mla_args b = *a;
+  b.workspace = ptr;
+  b.workspace_bytes = NOALLOC_SCRATCH_BYTES;
+  set_attn_attr();
+  return decode_impl(&b, reinterpret_cast<hipStream_t>(stream));
 }
 
 int amla_mla_decode_profiled(const amla_mla_args *a, void *stream, void *const *events) {

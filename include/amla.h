@@ -134,6 +134,19 @@ int amla_mla_decode(const amla_mla_args *args, void *stream);
  * benchmark can time each kernel on the stream it runs on. */
 int amla_mla_decode_profiled(const amla_mla_args *args, void *stream, void *const *events);
 
+/* No counterpart in the reference: for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * amla_mla_decode with its scratch taken from a per-device static device array
+ * of AMLA_NOALLOC_SCRATCH_BYTES (enough for batch <= 32 at any context);
+ * args->workspace and args->workspace_bytes are ignored.  Calls no allocating
+ * routine.  Every call on one device shares that device's array (it holds the
+ * last call's intermediates; nothing in it needs to start at zero): calls that
+ * overlap in time on one device (two streams, two threads) race and must be
+ * serialised by the caller.  Returns AMLA_EWORKSPACE, launching nothing, when
+ * amla_mla_decode_workspace_bytes(args) exceeds the array. */
+#define AMLA_NOALLOC_SCRATCH_BYTES (56u << 20)
+int amla_mla_decode_noalloc(const amla_mla_args *args, void *stream);
+
 /* Replaces mla_attention(...) for S >= 1 with a causal mask over the new rows
  * (inference/ops.py:100-183 incl. :172-177): kv_b decompression of the cached
  * rows and flash attention with bf16 MFMA. */
