@@ -154,33 +154,116 @@ def attn_traffic(B, T):
 
 # ------------------------------------------------------------------ CPU baseline
 
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_s(fn, reps=3):
+    fn()                                     # warm-up (thread pool, allocator)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
 def cpu_baseline(T, B):
-    """The oracle (torch-CPU restatement of the reference) on the host cores:
-    one layer x one sequence at the full context, scaled x B sequences."""
+    """The oracle (the torch-CPU restatement of the reference's op sequence) on
+    the host cores.  Headline: one layer x one sequence at the full context,
+    median of 3 after a warm-up, scaled x B sequences (the reference's position
+    is one int, so a batch is B independent sequences).  Also one timed run each
+    (after the warm-up above) of decode B=1 at context 257 and 4096, the 15
+    fp8_linear calls of the 5 projection shapes x M in {1, 8, 64}, and prefill of
+    4096 tokens; these are in cpu_baseline_configs."""
     from oracle import ref_ops as R
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     lay = synth.make_layer(CFG, "cpu")
-    ckv, kpe = synth.make_kv_cache(CFG, 1, T, T - 1, "cpu")
     h = synth.make_hidden(CFG, 1, 1, "cpu")
-    tab = R.precompute_rope_freqs(CFG, T)
+
+    def decode(Tc):
+        ckv, kpe = synth.make_kv_cache(CFG, 1, Tc, Tc - 1, "cpu")
+        tab = R.precompute_rope_freqs(CFG, Tc)
+        return lambda: R.mla_attention(h, lay.attn_weights, (ckv, kpe), Tc - 1, tab, CFG)
+
+    dt = _median_s(decode(T))
+    cfgs = {}
+    f = decode(257)
+    t0 = time.perf_counter(); f(); cfgs["decode_b1_ctx257_us"] = round((time.perf_counter() - t0) * 1e6, 1)
+    f = decode(4096)
+    t0 = time.perf_counter(); f(); cfgs["decode_b1_ctx4096_us"] = round((time.perf_counter() - t0) * 1e6, 1)
+    lin = {}
+    for name in synth.projection_shapes(CFG):
+        w, sc = lay.attn_weights[name]
+        for M in (1, 8, 64):
+            x = synth.randn((M, w.shape[1]), synth.seed_of("cpu", name, M), 1.0).to(torch.bfloat16)
+            t0 = time.perf_counter()
+            R.fp8_linear(x, w, sc)
+            lin[f"{name}_m{M}"] = round((time.perf_counter() - t0) * 1e6, 1)
+    cfgs["fp8_linear_us"] = lin
+    S = 4096
+    hp = synth.make_hidden(CFG, 1, S, "cpu-prefill")
+    cp = (torch.zeros(1, S, 512, dtype=torch.bfloat16), torch.zeros(1, S, 64, dtype=torch.bfloat16))
+    tab = R.precompute_rope_freqs(CFG, S)
     t0 = time.perf_counter()
-    R.mla_attention(h, lay.attn_weights, (ckv, kpe), T - 1, tab, CFG)
-    dt = time.perf_counter() - t0
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(dt * B * 1e6, 1), "unit": "us/layer", "cores": cores, "kind": "port",
-            "sample": f"oracle mla_attention, 1 layer x 1 sequence at context {T} measured ({dt:.2f} s), "
-                      f"x{B} sequences (extrapolated); host {cpu_model}"}
+    R.mla_attention(hp, lay.attn_weights, cp, 0, tab, CFG)
+    cfgs["prefill_4096_us"] = round((time.perf_counter() - t0) * 1e6, 1)
+    return ({"value": round(dt * B * 1e6, 1), "unit": "us/layer", "cores": cores, "kind": "port",
+             "sample": f"oracle mla_attention, 1 layer x 1 sequence at context {T}: median of 3 after a warm-up "
+                       f"{dt:.3f} s, x{B} sequences (extrapolated); host {_cpu_model()}, {cores} threads"},
+            cfgs)
 
 
 # ------------------------------------------------------------------ main
+
+def linear_extras(stack, dev, steps, warmup):
+    """fp8_linear alone (inference/ops.py:15-44): the five projection shapes x
+    M in {1, 8, 64}.  One graph replay runs the linear once over every layer's
+    weight of that shape (61 distinct weights, 0.9-7.2 GB: the 256 MB MALL
+    cannot serve them); us per call and GB/s of N*K + scales + 2*M*K + 2*M*N."""
+    out = {}
+    for name, (n, k) in synth.projection_shapes(CFG).items():
+        ws = [lay.attn_weights[name] for lay in stack]
+        for M in (1, 8, 64):
+            x = synth.randn((M, k), synth.seed_of("bench", "lin", name, M), 1.0, dev).to(torch.bfloat16)
+
+            def f():
+                for w, sc in ws:
+                    ops.fp8_linear(x, w, sc)
+
+            ms, _ = time_graph(f, steps, warmup)
+            per_ms = ms / len(ws)
+            nbytes = n * k + 4 * -(-n // 128) * -(-k // 128) + 2 * M * k + 2 * M * n
+            out[f"{name}_m{M}"] = {"us": round(per_ms * 1000, 2), "gbs": round(nbytes / (per_ms * 1e-3) / 1e9, 1)}
+    return out
+
+
+def decode_extra(stack, dev, steps, warmup, lengths, tag):
+    """Decode over the whole stack at one context length per sequence
+    (position = length - 1), one HIP graph per step: (us per layer, HBM GB/s of
+    weights + cached rows + new rows + hidden, attention-kernel ms)."""
+    B = len(lengths)
+    maxL = max(lengths)
+    caches = make_caches(len(stack), B, maxL, dev, tag=tag)
+    rope = ops.precompute_rope_freqs(CFG, maxL, dev)
+    pos = torch.tensor([L - 1 for L in lengths], dtype=torch.int32, device=dev)
+    h = synth.randn((B, 1, CFG.hidden_size), synth.seed_of("bench", tag, "hidden"), 1.0, dev).to(torch.bfloat16)
+    ms, _ = time_graph(lambda: run_stack(stack, caches, h, pos, rope, maxL), steps, warmup)
+    us = ms * 1000 / len(stack)
+    nbytes = WEIGHT_BYTES + SCALE_BYTES + GAMMA_BYTES + sum(lengths) * ROW_BYTES + B * ROW_BYTES + \
+        B * CFG.hidden_size * 4
+    stages = decode_stage_times(stack, caches, h, pos, rope, maxL, reps=1)
+    del caches
+    torch.cuda.empty_cache()
+    return us, nbytes / (us * 1e-6) / 1e9, stages
+
 
 def _fp8_on_device(n, k, gen, dev):
     """Random e4m3fn codes (no NaN codes) and scales in [0.5, 1.5) generated on the device."""
@@ -337,16 +420,22 @@ def main():
 
     extras = {}
     if not args.no_extras:
-        # decode B=1, ctx 4096 over the same 61 layers (MALL-proof: 11.4 GB of weights per step)
-        c4 = make_caches(NL, 1, 4096, dev, tag="bench4k")
-        rope4 = ops.precompute_rope_freqs(CFG, 4096, dev)
-        pos4 = torch.full((1,), 4095, dtype=torch.int32, device=dev)
-        h4 = hidden[:1].contiguous()
-        ms4, _ = time_graph(lambda: run_stack(stack, c4, h4, pos4, rope4, 4096), args.steps, args.warmup)
-        us4 = ms4 * 1000 / NL
-        extras["decode_ctx4096_b1_us_per_layer"] = round(us4, 2)
-        extras["decode_ctx4096_b1_hbm_gbs"] = round(decode_layer_bytes(1, 4096) / (us4 * 1e-6) / 1e9, 1)
-        del c4
+        # decode over the same 61 layers (MALL-proof: 11.4 GB of weights per step):
+        # batch 1 at context 257 and 4096, batch 32 at ragged contexts U[1024, 16384]
+        for key, lengths in (("decode_ctx257_b1", [257]), ("decode_ctx4096_b1", [4096])):
+            us, g, _ = decode_extra(stack, dev, args.steps, args.warmup, lengths, key)
+            extras[f"{key}_us_per_layer"] = round(us, 2)
+            extras[f"{key}_hbm_gbs"] = round(g, 1)
+        lengths = synth.ragged_lengths(32, 1024, 16384, "config3")
+        us, g, st3 = decode_extra(stack, dev, args.steps, args.warmup, lengths, "decode_ragged_b32")
+        extras["decode_ragged_b32_us_per_layer"] = round(us, 2)
+        extras["decode_ragged_b32_hbm_gbs"] = round(g, 1)
+        extras["decode_ragged_b32_sum_context"] = int(sum(lengths))
+        extras["decode_ragged_b32_attention_us"] = round(st3["attention"] * 1000, 2)
+        # the same rows at the batch-8 attention bandwidth (balance check of the split plan)
+        extras["decode_ragged_b32_attention_us_at_b8_rate"] = round(
+            sum(lengths) * ROW_BYTES / (achieved * 1e9) * 1e6, 2)
+        extras["fp8_linear"] = linear_extras(stack, dev, args.steps, args.warmup)
         # prefill 4096 tokens, one layer (rotating over up to 4 layers' weights)
         S = 4096
         hp = synth.randn((1, S, CFG.hidden_size), synth.seed_of("bench", "prefill"), 1.0, dev).to(torch.bfloat16)
@@ -394,12 +483,17 @@ def main():
         "roofline": {"kernel": "attn_kernel (latent-cache attention, split over context)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": attn_traffic(B, T),
-                     "bytes_per_launch": attn_bytes, "avg_ms": round(attn_ms, 4)},
+                     "bytes_per_launch": attn_bytes, "avg_ms": round(attn_ms, 4),
+                     "avg_ms_source": "HIP events recorded on attn_kernel's launch stream around each launch "
+                                      "(eager decode of every layer, twice), mean",
+                     "traffic_source": f"profiles/attn_kernel_b{B}_ctx{T}_traffic.md: rocprofv3 --pmc FETCH_SIZE "
+                                       "and WRITE_SIZE of this workload, each scaled by the same counter on a "
+                                       "1 GiB device copy"},
         **extras,
     }
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle) ...")
-        result["cpu_baseline"] = cpu_baseline(T, B)
+        result["cpu_baseline"], result["cpu_baseline_configs"] = cpu_baseline(T, B)
     print(json.dumps(result), flush=True)
 
 

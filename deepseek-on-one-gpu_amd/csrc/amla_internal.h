@@ -92,6 +92,17 @@ struct GemvGroups {
 // plan: plan_gemv_grouped(max M of the groups, N, K) (or plan_gemv).
 GemvPlan plan_gemv_grouped(int M, int N, int K);
 int launch_gemv_grouped(const GemvParams &p, GemvGroups groups, const GemvPlan &plan, hipStream_t stream);
+// Register-streaming skinny GEMM for M <= 16 (weights HBM -> VGPRs, x in
+// LDS).  Blocks per wave per tile: at most RS_NARROW_NB with three tiles in
+// flight, or RS_WIDE_NB (one part of up to 4 * RS_WIDE_NB blocks) with one.
+constexpr int RS_NARROW_NB = 4;
+constexpr int RS_WIDE_NB = 16;
+GemvPlan plan_gemv_rs(int M, int N, int K);
+size_t gemv_rs_lds_bytes(int M, int kpb, int rg);
+// xgamma != nullptr: x rows are replaced by rms_norm(x, xgamma, eps) first
+// (needs plan.kparts == 1).
+int launch_gemv_rs(const GemvParams &p, int mode, const GemvPlan &plan, const uint16_t *xgamma, float eps,
+                   hipStream_t stream, bool finish = true);
 // Large-M fp8 GEMM with the same modes (M > 64).
 size_t gemm_ws_bytes(int M, int N, int K);
 int launch_gemm(const GemvParams &p, int mode, hipStream_t stream);

@@ -13,11 +13,14 @@
 // the rotation of the raw cached rope key (ops.py:158-159), both applied on the
 // fly, once per row instead of once per row and head.
 //
-// Launch sequence per layer:
-//   rms_norm   : input RMSNorm of hidden (layer mode only)
-//   gemv  QKVA : fp32 K-part sums of q_a | kv_a from hidden
-//   finish     : kv_a straight into the caches, q_a_layernorm(q_a) fused
-//   gemv  QROPE: q = q_a_norm W_qb^T; RoPE on the q_pe rows at pos[b]
+// Launch sequence per layer (batch <= 16):
+//   gemv  QKVA : q_a | kv_a from hidden in one pass over K, the input RMSNorm
+//                (layer mode) fused into the x staging; kv_a straight into
+//                the caches, q_a (bf16) to the workspace
+//   gemv  QROPE: q = rms_norm(q_a) W_qb^T with q_a_layernorm fused into the x
+//                staging; RoPE on the q_pe rows at pos[b]
+// (larger batches: rms_norm, K-part q_a | kv_a GEMV, a finish with the q_a
+// norm fused, then q_b)
 //   absorb     : qt = gamma_kv * W_UK^T q_nope  -> qbuf (B, H, 576) with q_pe,
 //                stored in attn_kernel's fragment order
 //   attn       : split over context, online softmax, bf16 partial O, (m, l)
@@ -137,13 +140,53 @@ struct AttnParams {
   const float *rope_table;           // (rows, 32, 2)
   const int32_t *pos;                // decode position per sequence; context T = min(pos + 1, tmax)
   int tmax;                          // context bound (rows of cache and rope table that may be read)
-  int splits, tiles_per_split;
+  int units;         // splits shared out over the batch (the grid has units + batch workgroups)
+  int batch;
   float scale_log2;  // softmax scale * log2(e)
   float eps;
-  uint16_t *part_o;  // (B, splits, H, 512) bf16: sum_t p_t r_t c_t, p relative to the split's reference max
-  float *part_ml;  // (B, splits, H, 2) reference max (log2 units) and sum of p; sum < 0 marks a
+  uint16_t *part_o;  // (units + B, H, 512) bf16 by split slot: sum_t p_t r_t c_t, p relative to the split's reference max
+  float *part_ml;  // (units + B, H, 2) reference max (log2 units) and sum of p; sum < 0 marks a
                    // (split, head) whose scores overflowed the reference (recomputed by the combine)
 };
+
+// Split plan of a decode batch, computed from the device positions by every
+// attention workgroup and by the combine (no host synchronisation, the same
+// integers everywhere): sequence b has N_b = ceil(T_b / TT) tiles
+// (T_b = min(pos[b] + 1, tmax)) and gets s_b = max(1, floor(units * N_b / N))
+// splits (N = sum of N_b), in consecutive slots first_b = s_0 + .. + s_{b-1};
+// split j of b covers tiles [j N_b / s_b, (j + 1) N_b / s_b).  So every split
+// holds about N / units tiles whatever the spread of contexts (a ragged batch
+// is balanced by its total tokens, not by its longest sequence), and
+// sum s_b <= units + B slots.
+struct SeqSplits {
+  int first, count, ntiles;
+};
+
+AMLA_DEV int seq_tiles(const AttnParams &p, int b) {
+  const int T = min(p.pos[b] + 1, p.tmax);
+  return T > 0 ? (T + TT - 1) / TT : 0;
+}
+
+AMLA_DEV int total_tiles(const AttnParams &p) {
+  int n = 0;
+  for (int b = 0; b < p.batch; ++b) n += seq_tiles(p, b);
+  return n;
+}
+
+AMLA_DEV int seq_split_count(const AttnParams &p, int nb, int N) {
+  return N > 0 ? max(1, (int)(((int64_t)p.units * nb) / N)) : 1;
+}
+
+AMLA_DEV SeqSplits seq_splits(const AttnParams &p, int b) {
+  const int N = total_tiles(p);
+  int first = 0;
+  for (int c = 0; c < b; ++c) first += seq_split_count(p, seq_tiles(p, c), N);
+  const int nb = seq_tiles(p, b);
+  return SeqSplits{first, seq_split_count(p, nb, N), nb};
+}
+
+// tile range of split j of a sequence with nb tiles in s splits
+AMLA_DEV int split_tile(int nb, int s, int j) { return (int)(((int64_t)j * nb) / s); }
 
 // LDS: a ring of NST stages, each one tile of TT cache rows
 //   K   [TT][KROW] bf16: raw latent row (DMA) | rotated rope key / r_t (written after DMA)
@@ -152,7 +195,10 @@ struct AttnParams {
 // plus two (cos, sin) table blocks (tiles of even / odd index), copied two
 // tiles ahead like the rows, and the tile's probabilities P^T of all heads.
 constexpr int NST = 3;
-constexpr int KROW = QKD + 8;  // 1168 B rows: the 16 B pad spreads 16 rows over all LDS banks
+// 1184 B rows (592 bf16): the score fragment reads (32 lanes: 16 rows x two
+// 16 B chunks) and the transpose reads (64 lanes: 16 rows x 4 x 8 B) both land
+// on distinct banks of the 512 B bank window (row stride = 74 x 16 B = 148 x 8 B)
+constexpr int KROW = QKD + 16;
 constexpr int K_BYTES = TT * KROW * 2;
 constexpr int RAW_BYTES = TT * ROPE * 2;
 constexpr int RT_OFF = K_BYTES + RAW_BYTES;  // r_t of the tile's rows, fp32
@@ -165,7 +211,9 @@ constexpr int ATTN_LDS_BYTES = P_OFF + HEADS * PROW;
 constexpr int OROW = LORA * 2 + 32;  // LDS row of one head's partial O at the end (bf16, padded)
 static_assert(HEADS * OROW <= ATTN_LDS_BYTES, "partial O staging must fit the attention LDS");
 constexpr int TILE_DMA = 11;  // copies per wave per tile: 8 latent rows, 1 block of rope keys, 2 table blocks
-constexpr float REF_HEADROOM = 64.f;      // p = 2^(s - m_ref) <= 2^64: no overflow anywhere
+// p = 2^(s - m_ref): a split whose sum of p reaches 2^64 (a later score far
+// above the first tile's maximum) is flagged and recomputed exactly
+constexpr float REF_HEADROOM_SUM = 18446744073709551616.f;  // 2^64
 
 // Wave w copies rows 8w .. 8w+7 of a tile straight into LDS (no VGPRs):
 // every global_load_lds_dwordx4 writes 64 lanes x 16 B contiguously at its
@@ -175,8 +223,8 @@ constexpr float REF_HEADROOM = 64.f;      // p = 2^(s - m_ref) <= 2^64: no overf
 // (cos, sin) table rows of the 8 rows (2 x 1 KB), into the table block of the
 // tile's parity.  The tile loop issues one piece per score step: a burst of
 // LDS copies stalls the issuing wave for tens of cycles per copy.
-AMLA_DEV void dma_piece(const AttnParams &p, int b, int tile, int T, uint8_t *smem, uint8_t *stage, int wave, int lane,
-                        int piece) {
+AMLA_DEV void dma_piece(const AttnParams &p, int b, int tile, int parity, int T, uint8_t *smem, uint8_t *stage,
+                        int wave, int lane, int piece) {
   const int t0 = tile * TT + wave * 8;
   const int t0c = min(t0, T - 1);
   // lane-derived offsets are unsigned (scalar base + 32-bit lane offset
@@ -199,13 +247,13 @@ AMLA_DEV void dma_piece(const AttnParams &p, int b, int tile, int T, uint8_t *sm
     const uint32_t row = static_cast<uint32_t>(min(t0 + static_cast<int>(e >> 4), T - 1) - t0c);
     __builtin_amdgcn_global_load_lds(
         tb + row * (ROPE * 4) + (e & 15u) * 16u,
-        LDS_PTR(smem + TAB_OFF + (tile & 1) * TAB_BYTES + wave * 2048 + (piece - 9) * 1024), 16, 0, 0);
+        LDS_PTR(smem + TAB_OFF + (parity & 1) * TAB_BYTES + wave * 2048 + (piece - 9) * 1024), 16, 0, 0);
   }
 }
 
 AMLA_DEV void dma_tile(const AttnParams &p, int b, int tile, int T, uint8_t *smem, uint8_t *stage, int wave, int lane) {
 #pragma unroll
-  for (int piece = 0; piece < TILE_DMA; ++piece) dma_piece(p, b, tile, T, smem, stage, wave, lane, piece);
+  for (int piece = 0; piece < TILE_DMA; ++piece) dma_piece(p, b, tile, tile, T, smem, stage, wave, lane, piece);
 }
 
 AMLA_DEV uint32_t rot_pair(uint32_t x, float c, float s) {
@@ -284,7 +332,8 @@ AMLA_DEV float max_lane_groups(float v) {
 }
 
 
-// Grid (splits, B), 256 threads, one workgroup per CU (~148 KB of LDS).
+// Grid: one workgroup per split slot (seq_splits), 256 threads, one
+// workgroup per CU (~150 KB of LDS).
 // Scores: wave w owns heads 32w .. 32w+31; values: wave w owns latent columns
 // 128w .. 128w+127 of every head.  Per tile of 32 cache rows:
 //   each wave computes r_t of its 8 copied rows and rotates their rope keys,
@@ -295,7 +344,8 @@ AMLA_DEV float max_lane_groups(float v) {
 //     fragments read from LDS three steps ahead;
 //   p = 2^(s - m_ref): m_ref is the head's max over the split's first tile and
 //     stays fixed, so O^T is only ever touched by MFMA (no rescaling); a head
-//     whose later tile exceeds m_ref by REF_HEADROOM is flagged instead;
+//     whose sum of p reaches 2^64 (a later score far above m_ref) is flagged
+//     instead and recomputed exactly by the combine;
 //   P^T (p * r_t as bf16) of the wave's heads goes to LDS; after a barrier
 //   O^T (128 latent x 128 heads, fp32) += C^T (128 x t) . P^T (t x 128), C^T
 //     by transpose reads of the wave's 128 columns of the raw tile.
@@ -311,14 +361,33 @@ AMLA_DEV float max_lane_groups(float v) {
 // operations complete in order, so any other LDS operation issued in between
 // only makes a wait stricter; nothing in the loop uses scalar memory loads.
 __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
-  const int split = blockIdx.x, b = blockIdx.y;
+  const int slot = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
+  // this workgroup's (sequence, split) from the batch's split plan; slots past
+  // the plan have no work
+  int b = 0, split = 0, nb = 0, ns = 1;
+  {
+    const int N = total_tiles(p);
+    int first = 0;
+    b = -1;
+    for (int c = 0; c < p.batch; ++c) {
+      const int t = seq_tiles(p, c);
+      const int sc = seq_split_count(p, t, N);
+      if (b < 0 && slot < first + sc) {
+        b = c;
+        split = slot - first;
+        nb = t;
+        ns = sc;
+      }
+      first += sc;
+    }
+    if (b < 0) return;
+  }
   const int T = min(p.pos[b] + 1, p.tmax);
-  const int ntiles = (T + TT - 1) / TT;
-  const int tb = split * p.tiles_per_split;
-  const int te = min(tb + p.tiles_per_split, ntiles);
+  const int tb = split_tile(nb, ns, split);
+  const int te = split_tile(nb, ns, split + 1);
   extern __shared__ __align__(16) uint8_t smem[];
   const int head0 = wave * 32;
 
@@ -337,7 +406,6 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) o[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_ref[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
-  bool bad[2] = {false, false};
 
   if (tb < te) {
     dma_tile(p, b, tb, T, smem, smem, wave, lane);
@@ -356,7 +424,6 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       // copies of the tile after next, one per score step below (its stage was
       // last read in the previous tile; the table block only ever holds this
       // wave's rows)
-      const bool dma_next = tile + 2 < te;
       uint8_t *const nst = smem + ((it + 2) % NST) * STAGE_BYTES;
       const uint16_t *K = reinterpret_cast<const uint16_t *>(cur);
 
@@ -434,8 +501,11 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
               asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(sc[mt][nt]) : "v"(ab[c][mt]), "v"(qf[nt][ks]));
           }
         // consume a batch of the next tile's rows (landed: this step's wait
-        // covers every operation issued before step ks's reads)
+        // covers every operation issued before step ks's reads).  The empty
+        // asm names the registers, so the compiler cannot hoist their use
+        // above the wait: a wait orders memory operations, not register uses.
         if (ks == 5 || ks == 10) {
+          asm volatile("" : "+v"(pv4[0]), "+v"(pv4[1]), "+v"(pv4[2]), "+v"(pv4[3]));
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             pss = dot2_bf16(pv4[i].x, pss);
@@ -447,7 +517,9 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
         if (ks == 15) {
           // r_t = rsqrt(mean(c_t^2) + eps): sum over the row's 8 lanes (every
           // lane of the row ends with the total); rope key rotated in fp32,
-          // rounded to bf16 (inference/ops.py:10-12, :93-97)
+          // rounded to bf16 (inference/ops.py:10-12, :93-97); the reads of
+          // iteration 10 are pinned after this step's wait like pv4 above
+          asm volatile("" : "+v"(praw), "+v"(pc0), "+v"(pc1));
           pss += dpp_f32<0xB1>(pss);   // quad_perm [1,0,3,2]
           pss += dpp_f32<0x4E>(pss);   // quad_perm [2,3,0,1]
           pss += dpp_f32<0x141>(pss);  // row_half_mirror
@@ -495,7 +567,11 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
               (__attribute__((address_space(3))) const uint8_t *)(cur + RT_OFF + (4 * lg) * 4)));
           asm volatile("ds_read_b128 %0, %2 offset:0\n\tds_read_b128 %1, %2 offset:64" : "=v"(rc[0]), "=v"(rc[1]) : "v"(ra));
         }
-        if (ks < TILE_DMA && dma_next) dma_piece(p, b, tile + 2, T, smem, nst, wave, lane, ks);
+        // unconditional (no branch per copy): past the split's end the last
+        // tile is copied again (an L2 hit) into a stage nothing reads any more;
+        // the table block is the parity of tile + 2, never the one the
+        // preparation of tile + 1 reads
+        if (ks < TILE_DMA) dma_piece(p, b, min(tile + 2, te - 1), tile + 2, T, smem, nst, wave, lane, ks);
       }
       // the softmax reads sc: MFMA write -> VALU read wait states
       asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sc[0][0]), "+v"(sc[0][1]), "+v"(sc[1][0]), "+v"(sc[1][1])::"memory");
@@ -523,10 +599,11 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
           for (int e = 0; e < 8; ++e)
             if (tbase + (e >> 2) * 16 + 4 * lg + (e & 3) >= T) sv[e] = -INFINITY;
         }
-        float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        mx = p.scale_log2 * max_lane_groups(mx);
-        if (!have_ref) m_ref[nt] = mx;
-        bad[nt] = bad[nt] || (mx > m_ref[nt] + REF_HEADROOM);
+        if (!have_ref) {  // the split's first tile fixes the reference max (a wave-uniform branch)
+          const float mx =
+              fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+          m_ref[nt] = p.scale_log2 * max_lane_groups(mx);
+        }
         float pv[8];
         float lsum = 0.f;
 #pragma unroll
@@ -618,15 +695,21 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
     const int head = head0 + nt * 16 + li;
-    const size_t row = ((size_t)b * p.splits + split) * HEADS + head;
+    const size_t row = (size_t)slot * HEADS + head;
+    // a sum at or above 2^64 (or inf / NaN) means a score rose far above the
+    // reference max: the combine recomputes this (split, head) exactly
+    const bool bad = !(l < REF_HEADROOM_SUM);
     if (lg == 0) {
       p.part_ml[row * 2] = m_ref[nt];
-      p.part_ml[row * 2 + 1] = bad[nt] ? -1.f : l;
+      p.part_ml[row * 2 + 1] = bad ? -1.f : l;
     }
   }
-  // O goes out through LDS (the loop's last barrier follows its last LDS read
-  // and every copy has landed): head rows of 512 bf16, then 1 KB contiguous
-  // per wave-wide store
+  // O goes out through LDS, over the stages and table blocks: the copies the
+  // last iterations issued (into stages nothing reads) must have landed in
+  // every wave before any wave writes there; then head rows of 512 bf16, and
+  // 1 KB contiguous per wave-wide store
+  wait_vmcnt<0>();
+  __syncthreads();
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
@@ -634,7 +717,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       *reinterpret_cast<u32x2 *>(smem + (nt * 16 + li) * OROW + (wave * 128 + mt * 16 + 4 * lg) * 2) =
           u32x2{pack_bf16(o[mt][nt].x, o[mt][nt].y), pack_bf16(o[mt][nt].z, o[mt][nt].w)};
   __syncthreads();
-  uint8_t *const dst = reinterpret_cast<uint8_t *>(p.part_o + ((size_t)b * p.splits + split) * HEADS * LORA);
+  uint8_t *const dst = reinterpret_cast<uint8_t *>(p.part_o + (size_t)slot * HEADS * LORA);
 #pragma unroll 8
   for (int i = 0; i < HEADS * LORA * 2 / (256 * 16); ++i) {
     const int chunk = i * 256 + tid, head = chunk >> 6, c16 = chunk & 63;
@@ -656,14 +739,14 @@ AMLA_DEV float block_reduce(float v, float *red, bool is_max) {
 }
 
 // Exact online-softmax recomputation of one (split, head) in fp32, used only
-// for heads attn_kernel flagged (a score more than REF_HEADROOM above the
-// split's reference max).  Thread tid owns latent columns 2*tid and 2*tid+1.
-AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, int split, float *qs, float *ps, float *red,
-                              float &m_out, float &l_out, float &o0, float &o1) {
+// for heads attn_kernel flagged (a sum of p = 2^(s - m_ref) at or above 2^64:
+// scores far above the split's reference max).  Thread tid owns latent columns 2*tid and 2*tid+1.
+AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, const SeqSplits &sp, int split, float *qs,
+                              float *ps, float *red, float &m_out, float &l_out, float &o0, float &o1) {
   const int tid = threadIdx.x;
   const int T = min(p.pos[b] + 1, p.tmax);
-  const int t0 = split * p.tiles_per_split * TT;
-  const int t1 = min(t0 + p.tiles_per_split * TT, T);
+  const int t0 = split_tile(sp.ntiles, sp.count, split) * TT;
+  const int t1 = min(split_tile(sp.ntiles, sp.count, split + 1) * TT, T);
   __syncthreads();
   for (int c = tid; c < QKD; c += 256) qs[c] = bf2f(p.qbuf[qfrag_index(b, h, c)]);
   __syncthreads();
@@ -761,10 +844,11 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
   // rows are in flight while the max and the weights are formed.
   if (wave < nb) {
     const int b = b0 + wave;
-    const size_t base = (size_t)b * ap.splits * HEADS + h;
+    const SeqSplits sp = seq_splits(ap, b);
+    const size_t base = (size_t)sp.first * HEADS + h;
     const u32x4 *po = reinterpret_cast<const u32x4 *>(ap.part_o + base * LORA) + lane;
     const size_t stride = (size_t)HEADS * LORA / 8;
-    const int nsp = ap.splits;
+    const int nsp = sp.count;
     u32x4 v[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) v[j] = po[(size_t)min(j, nsp - 1) * stride];
@@ -826,13 +910,14 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
   for (int bb = 0; bb < nb; ++bb) {
     if (!s_flag[bb]) continue;
     const int b = b0 + bb;
-    const size_t base = (size_t)b * ap.splits * HEADS + h;
+    const SeqSplits sp = seq_splits(ap, b);
+    const size_t base = (size_t)sp.first * HEADS + h;
     float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
-    for (int s = 0; s < ap.splits; ++s) {
+    for (int s = 0; s < sp.count; ++s) {
       const size_t row = base + (size_t)s * HEADS;
       float m1 = ap.part_ml[row * 2], l1 = ap.part_ml[row * 2 + 1], o0, o1;
       if (l1 < 0.f) {
-        recompute_split(ap, b, h, s, qs, ps, red, m1, l1, o0, o1);
+        recompute_split(ap, b, h, sp, s, qs, ps, red, m1, l1, o0, o1);
       } else {
         const uint32_t v = reinterpret_cast<const uint32_t *>(ap.part_o + row * LORA)[tid];
         o0 = lo_bf(v);
@@ -883,33 +968,51 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
 
 // ---------------------------------------------------------------- orchestration
 
+// The register-streaming decode GEMVs with fused norms are built but not
+// dispatched: in their present form they are slower than the LDS-streaming
+// GEMVs (their weight prefetch is cut short by conservative waits).
+constexpr bool kDecodeFusedNorms = false;
+
 struct DecodeLayout {
   size_t xn, qa, q, qbuf, part_ml, part_o, attn, lin, total;
   GemvPlan pa, pb, po;
-  int splits, tiles_per_split;
+  bool rs;  // register-streaming skinny GEMMs with fused norms (batch <= 16)
+  int units, slots;  // split plan size (device side: seq_splits) and partial slots
 };
 
 static DecodeLayout decode_layout(const amla_mla_args &a) {
   DecodeLayout L = {};
   const int B = a.batch;
   const int HD = a.qk_nope + a.qk_rope;
-  L.pa = plan_gemv(B, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
-  L.pb = plan_gemv(B, a.heads * HD, a.q_lora);
-  L.po = plan_gemv(B, a.hidden, a.heads * a.v_dim);
+  // batch <= 16: q_a | kv_a reads the whole K in one pass (the input RMSNorm
+  // fused into its x staging, no finishing pass), q_b fuses q_a_layernorm the
+  // same way; larger batches take the LDS-streaming GEMM with K-part finishes
+  L.rs = kDecodeFusedNorms && B <= 16 && plan_gemv_rs(B, a.q_lora + a.kv_lora + a.qk_rope, a.hidden).kparts == 1 &&
+         plan_gemv_rs(B, a.heads * HD, a.q_lora).kparts == 1;
+  if (L.rs) {
+    L.pa = plan_gemv_rs(B, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
+    L.pb = plan_gemv_rs(B, a.heads * HD, a.q_lora);
+    L.po = plan_gemv_rs(B, a.hidden, a.heads * a.v_dim);
+  } else {
+    L.pa = plan_gemv(B, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
+    L.pb = plan_gemv(B, a.heads * HD, a.q_lora);
+    L.po = plan_gemv(B, a.hidden, a.heads * a.v_dim);
+  }
+  // splits over the batch: one per CU, at least two tiles each for the
+  // longest possible context; the plan itself is made on the device from the
+  // positions (seq_splits), so a ragged batch is balanced by its total tokens
   const int maxT = mla_context_bound(a);
   const int ntiles = (maxT + TT - 1) / TT;
-  int splits = (256 + B - 1) / B;
-  splits = std::max(1, std::min(splits, (ntiles + 1) / 2));
-  L.tiles_per_split = (ntiles + splits - 1) / splits;
-  L.splits = (ntiles + L.tiles_per_split - 1) / L.tiles_per_split;
+  L.units = std::max(1, std::min(256, B * std::max(1, ntiles / 2)));
+  L.slots = L.units + B;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes, 256); return o; };
   L.xn = take((size_t)B * a.hidden * 2);
   L.qa = take((size_t)B * a.q_lora * 2);
   L.q = take((size_t)B * a.heads * HD * 2);
   L.qbuf = take((size_t)B * a.heads * QKD * 2);
-  L.part_ml = take((size_t)B * L.splits * a.heads * 2 * 4);
-  L.part_o = take((size_t)B * L.splits * a.heads * LORA * 2);
+  L.part_ml = take((size_t)L.slots * a.heads * 2 * 4);
+  L.part_o = take((size_t)L.slots * a.heads * LORA * 2);
   L.attn = take((size_t)B * a.heads * a.v_dim * 2);
   L.lin = take(std::max(L.pa.part_bytes, std::max(L.pb.part_bytes, L.po.part_bytes)));  // K-part sums of the linears
   L.total = off;
@@ -973,7 +1076,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   //    caches, inference/ops.py:136-141; forward.py:92)
   mark(ev, 0, st);
   const uint16_t *xin = x;
-  if (a->input_gamma) {
+  if (a->input_gamma && !L.rs) {
     uint16_t *xn = reinterpret_cast<uint16_t *>(ws + L.xn);
     if ((rc = launch_rms_norm(x, B, a->hidden, a->hidden, reinterpret_cast<const uint16_t *>(a->input_gamma), a->eps,
                               xn, a->hidden, st)))
@@ -991,11 +1094,17 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pa.ckv_bstride = (int64_t)a->max_seq * LORA; pa.kpe_bstride = (int64_t)a->max_seq * ROPE;
   pa.kv_lora = LORA; pa.rope = ROPE; pa.pos = a->positions; pa.seq_len = 1; pa.max_rows = a->max_seq;
   pa.part = reinterpret_cast<float *>(ws + L.lin);
-  // 2. q_a_layernorm (inference/ops.py:130): fused into the K-part finish, or
-  //    a row norm in place when the GEMV needs no finishing pass
+  // 2. q_a_layernorm (inference/ops.py:130): in q_b's x staging (batch <= 16),
+  //    else fused into the K-part finish, or a row norm in place when the
+  //    GEMV needs no finishing pass
   mark(ev, 1, st);
   const uint16_t *gq = reinterpret_cast<const uint16_t *>(a->gamma_q);
-  if (L.pa.kparts > 1) {
+  if (L.rs) {
+    // one pass over [wq_a; wkv_a] with the input norm fused; q_a stays raw
+    // (bf16) for q_b, which normalises it in its own x staging
+    if ((rc = launch_gemv_rs(pa, GEMV_QKVA, L.pa, reinterpret_cast<const uint16_t *>(a->input_gamma), a->eps, st)))
+      return rc;
+  } else if (L.pa.kparts > 1) {
     if ((rc = launch_gemv(pa, GEMV_QKVA, L.pa, st, false))) return rc;
     if ((rc = launch_qkva_finish_norm(pa, L.pa.kparts, gq, a->eps, st))) return rc;
   } else {
@@ -1013,7 +1122,11 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pb.pos = a->positions; pb.seq_len = 1; pb.rope = ROPE; pb.rope_table = a->rope_table; pb.rope_rows = a->rope_rows;
   pb.head_dim = HD; pb.nope = a->qk_nope;
   pb.part = reinterpret_cast<float *>(ws + L.lin);
-  if ((rc = launch_gemv(pb, GEMV_QROPE, L.pb, st))) return rc;
+  if (L.rs) {
+    if ((rc = launch_gemv_rs(pb, GEMV_QROPE, L.pb, gq, a->eps, st))) return rc;
+  } else if ((rc = launch_gemv(pb, GEMV_QROPE, L.pb, st))) {
+    return rc;
+  }
 
   // 4. absorb W_UK into the query
   mark(ev, 3, st);
@@ -1030,12 +1143,12 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   ap.kpe = reinterpret_cast<const uint16_t *>(a->kpe_cache);
   ap.ckv_bstride = (int64_t)a->max_seq * LORA; ap.kpe_bstride = (int64_t)a->max_seq * ROPE;
   ap.rope_table = a->rope_table; ap.pos = a->positions; ap.tmax = mla_context_bound(*a);
-  ap.splits = L.splits; ap.tiles_per_split = L.tiles_per_split;
+  ap.units = L.units; ap.batch = B;
   ap.scale_log2 = a->softmax_scale * 1.4426950408889634f;
   ap.eps = a->eps;
   ap.part_o = reinterpret_cast<uint16_t *>(ws + L.part_o);
   ap.part_ml = reinterpret_cast<float *>(ws + L.part_ml);
-  attn_kernel<<<dim3(L.splits, B), 256, ATTN_LDS, st>>>(ap);
+  attn_kernel<<<dim3(L.slots), 256, ATTN_LDS, st>>>(ap);
   if ((rc = check_launch("mla attention"))) return rc;
 
   // 6. merge splits, W_UV
@@ -1056,7 +1169,8 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   po.res = reinterpret_cast<const uint16_t *>(a->residual); po.ldr = a->hidden;
   po.seq_len = 1;
   po.part = reinterpret_cast<float *>(ws + L.lin);
-  rc = launch_gemv(po, a->residual ? GEMV_RESID : GEMV_PLAIN, L.po, st);
+  rc = L.rs ? launch_gemv_rs(po, a->residual ? GEMV_RESID : GEMV_PLAIN, L.po, nullptr, 0.f, st)
+            : launch_gemv(po, a->residual ? GEMV_RESID : GEMV_PLAIN, L.po, st);
   mark(ev, NSTAGE, st);
   return rc;
 }
