@@ -366,6 +366,28 @@ def stream_extras(dev):
     return {"expert_stream_8_us": round(ms * 1000, 1), "expert_stream_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
 
 
+def prefill_extra(stack, dev, reps=8):
+    """Prefill of 4096 tokens from an empty cache, one layer per call (rotating over up to
+    4 layers' weights), mean of ``reps`` calls after two warm-up calls."""
+    S = 4096
+    hp = synth.randn((1, S, CFG.hidden_size), synth.seed_of("bench", "prefill"), 1.0, dev).to(torch.bfloat16)
+    cp = (torch.zeros(1, S, 512, dtype=torch.bfloat16, device=dev), torch.zeros(1, S, 64, dtype=torch.bfloat16, device=dev))
+    ropep = ops.precompute_rope_freqs(CFG, S, dev)
+    for i in range(2):
+        ops.mla_attention(hp, stack[i % len(stack)].attn_weights, cp, 0, ropep, CFG)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(reps):
+        ops.mla_attention(hp, stack[i % min(4, len(stack))].attn_weights, cp, 0, ropep, CFG)
+    e.record()
+    torch.cuda.synchronize()
+    pms = s.elapsed_time(e) / reps
+    tf = prefill_flops(S) / (pms * 1e-3) / 1e12
+    return {"prefill_4096_ms": round(pms, 3), "prefill_4096_tflops": round(tf, 1),
+            "prefill_frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -376,6 +398,9 @@ def main():
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--only-prefill", action="store_true",
+                    help="only time the 4096-token prefill (one JSON line) and exit: the profiling workload "
+                         "of the prefill kernels")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 launches) and exit: the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -396,6 +421,10 @@ def main():
         return
     torch.manual_seed(0)
     B, T, NL = args.batch, args.context, args.layers
+    if args.only_prefill:
+        res = prefill_extra(make_stack(min(NL, 4), B, T, dev), dev, reps=args.steps)
+        print(json.dumps(res), flush=True)
+        return
 
     stack = make_stack(NL, B, T, dev)
     caches = make_caches(NL, B, T, dev)
@@ -436,26 +465,7 @@ def main():
         extras["decode_ragged_b32_attention_us_at_b8_rate"] = round(
             sum(lengths) * ROW_BYTES / (achieved * 1e9) * 1e6, 2)
         extras["fp8_linear"] = linear_extras(stack, dev, args.steps, args.warmup)
-        # prefill 4096 tokens, one layer (rotating over up to 4 layers' weights)
-        S = 4096
-        hp = synth.randn((1, S, CFG.hidden_size), synth.seed_of("bench", "prefill"), 1.0, dev).to(torch.bfloat16)
-        cp = (torch.zeros(1, S, 512, dtype=torch.bfloat16, device=dev), torch.zeros(1, S, 64, dtype=torch.bfloat16, device=dev))
-        ropep = ops.precompute_rope_freqs(CFG, S, dev)
-        for i in range(2):
-            ops.mla_attention(hp, stack[i % len(stack)].attn_weights, cp, 0, ropep, CFG)
-        torch.cuda.synchronize()
-        reps = 8
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        for i in range(reps):
-            ops.mla_attention(hp, stack[i % min(4, len(stack))].attn_weights, cp, 0, ropep, CFG)
-        e.record()
-        torch.cuda.synchronize()
-        pms = s.elapsed_time(e) / reps
-        extras["prefill_4096_ms"] = round(pms, 3)
-        extras["prefill_4096_tflops"] = round(prefill_flops(S) / (pms * 1e-3) / 1e12, 1)
-        extras["prefill_frac_bf16_peak"] = round(extras["prefill_4096_tflops"] / BF16_PEAK_TFLOPS, 4)
-        del hp, cp
+        extras.update(prefill_extra(stack, dev))
         extras.update(ffn_extras(B, dev))
         extras.update(head_extras(B, dev))
         extras.update(stream_extras(dev))
