@@ -11,10 +11,12 @@ instructions in program order, modelling the two in-order counters:
   queue, every vector-memory load / store / LDS copy joins the VMEM queue;
 * ``s_waitcnt lgkmcnt(N)`` / ``vmcnt(N)`` retire all but the newest N entries of a queue;
 * any instruction whose sources or destinations meet the destination registers of a
-  queued (not yet retired) load is reported.
+  queued (not yet retired) load issued from inline asm is reported.
 
-Branches are followed in file order (the loop bodies that matter are straight-line
-after unrolling), which is conservative for loads issued before a branch.
+Loads the compiler emitted itself are waited for by the compiler; they take part in the
+counting but are not checked (the file-order walk would otherwise report uses on the
+other side of a branch).  Branches are followed in file order: the loop bodies with
+hand-counted waits are straight-line after unrolling.
 """
 from __future__ import annotations
 
@@ -42,8 +44,8 @@ def _all_regs(toks: Iterable[str]) -> set:
 
 
 def kernels(asm: str) -> dict:
-    """Kernel symbol -> list of instruction lines (comments and directives dropped)."""
-    out, cur = {}, None
+    """Kernel symbol -> list of (instruction, from inline asm) (comments and directives dropped)."""
+    out, cur, in_asm = {}, None, False
     for line in asm.splitlines():
         if re.match(r"^_Z\w+:", line):
             cur = line.split(":")[0]
@@ -54,16 +56,26 @@ def kernels(asm: str) -> dict:
         if line.startswith(".Lfunc_end"):
             cur = None
             continue
+        if ";;#ASMSTART" in line:
+            in_asm = True
+            continue
+        if ";;#ASMEND" in line:
+            in_asm = False
+            continue
         s = line.split(";")[0].strip()
         if s and not s.startswith(".") and not s.endswith(":"):
-            out[cur].append(s)
+            out[cur].append((s, in_asm))
     return out
 
 
 def inflight_uses(instrs: list) -> list:
-    """Instructions that touch registers of a load that may still be in flight."""
+    """Instructions that touch registers of an inline-asm load that may still be in flight.
+
+    ``instrs``: instruction strings (all treated as inline asm) or (instruction, from_asm) pairs.
+    """
     lds, vm, issues = [], [], []
-    for n, s in enumerate(instrs):
+    for n, item in enumerate(instrs):
+        s, tracked = (item, True) if isinstance(item, str) else item
         parts = s.split(None, 1)
         op = parts[0]
         args = [a.split()[0] for a in re.split(r",\s*", parts[1]) if a.strip()] if len(parts) > 1 else []
@@ -94,9 +106,9 @@ def inflight_uses(instrs: list) -> list:
             if hit:
                 issues.append(f"{s}  touches {sorted(hit)[:4]} of in-flight [{text}] (instr {at})")
         if op.startswith("ds_"):
-            lds.append((dst, n, s))
+            lds.append((dst if tracked else set(), n, s))
         elif op.startswith(("global_load", "buffer_load", "flat_load", "global_store", "buffer_store")):
-            vm.append((set() if is_lds_copy else dst, n, s))
+            vm.append((set() if is_lds_copy or not tracked else dst, n, s))
     return issues
 
 
