@@ -17,13 +17,26 @@ with events only:
 
 ``prefetch`` starts copies early (for example while the attention of the same
 layer runs); ``transfer_experts`` keeps the reference's call and return shape;
-``experts_for(layer)`` gives the mapping ``amla.ops.moe_block`` takes.
+``experts_for(layer)`` gives the mapping ``amla.ops.moe_block`` takes, and
+``amla.ops.moe_block`` also takes the streamer itself (it then streams the
+chosen experts in pool-sized waves, so any batch runs on any pool).
+
+Lifetime of the returned views: the slots handed out by ``transfer_experts`` /
+``experts_for`` are held (no ``prefetch`` may evict them) until ``release()`` or
+the next ``transfer_experts`` / ``experts_for`` call, which records the
+compute-stream event that later copies into those slots wait for.  Enqueue the
+work that reads the views before that call.
+
+The host side may be a callable ``(layer, e) -> weights`` (such as the reference's
+``weight_store.get_expert``) or an object with ``get_expert`` and optionally
+``note_copy(layer, e, event)`` (``amla.expert_store.ExpertStore``), which is told
+when the copy out of its pinned slot completes.
 """
 from __future__ import annotations
 
 import math
 from collections import OrderedDict
-from typing import Callable, Iterable
+from typing import Iterable
 
 import torch
 
@@ -38,10 +51,15 @@ class ExpertStreamer:
     weight store keeps them, gpu_transfer.py:12).
     """
 
-    def __init__(self, config, host_experts: Callable[[int, int], dict], device, slots: int | None = None,
-                 verbose: bool = False):
+    def __init__(self, config, host_experts, device, slots: int | None = None, verbose: bool = False):
         self.config = config
-        self.host_experts = host_experts
+        if hasattr(host_experts, "get_expert"):
+            self.host_experts = host_experts.get_expert
+            self._note_copy = getattr(host_experts, "note_copy", None)
+        else:
+            self.host_experts = host_experts
+            owner = getattr(host_experts, "__self__", None)
+            self._note_copy = getattr(owner, "note_copy", None)
         self.device = torch.device(device)
         self.verbose = verbose
         self.slots = int(slots or 4 * config.num_experts_per_tok)
@@ -57,6 +75,7 @@ class ExpertStreamer:
         self.lru: OrderedDict = OrderedDict()                           # (layer, e) -> slot
         self.ready: dict[int, torch.cuda.Event] = {}                    # slot -> copy done
         self.free = list(range(self.slots))
+        self.held: set = set()                                          # slots handed out, not yet released
         self.copies = 0                                                 # experts copied so far
 
     # -------------------------------------------------------------- slots
@@ -69,9 +88,10 @@ class ExpertStreamer:
         if self.free:
             slot = self.free.pop()
         else:
-            victim = next((k for k in self.lru if self.lru[k] not in pinned), None)
+            victim = next((k for k in self.lru if self.lru[k] not in pinned and self.lru[k] not in self.held), None)
             if victim is None:
-                raise RuntimeError("ExpertStreamer: every slot is in use by this call; raise `slots`")
+                raise RuntimeError("ExpertStreamer: every slot is in use by this call or held; raise `slots` "
+                                   "(amla.ops.moe_block streams larger sets in waves)")
             slot = self.lru.pop(victim)
             # compute already enqueued may still read the old expert
             done = torch.cuda.Event()
@@ -86,6 +106,8 @@ class ExpertStreamer:
             ev = torch.cuda.Event()
             ev.record(self.stream)
         self.ready[slot] = ev
+        if self._note_copy is not None:
+            self._note_copy(layer, e, ev)
         self.lru[key] = slot
         self.copies += 1
         if self.verbose:
@@ -108,17 +130,31 @@ class ExpertStreamer:
 
     # -------------------------------------------------------------- reference-shaped API
 
+    def release(self) -> None:
+        """Ends the hold on the slots handed out so far: work already enqueued on the current
+        stream may read them; later copies into them wait for it."""
+        if not self.held:
+            return
+        done = torch.cuda.Event()
+        done.record(torch.cuda.current_stream(self.device))
+        self.stream.wait_event(done)
+        self.held.clear()
+
     def transfer_experts(self, layer: int, expert_indices, verbose: bool = False) -> list[dict]:
         """gpu_transfer.py:50-89: the device weights of these experts, in the given order.
 
         The current stream waits for their copies on the device (no host synchronisation).
+        The slots of the previous call are released first; these are held until the next
+        call or ``release()``.
         """
         ids = [int(e) for e in (expert_indices.tolist() if isinstance(expert_indices, torch.Tensor)
                                 else expert_indices)]
+        self.release()
         slots = dict(zip(dict.fromkeys(ids), self.prefetch(layer, ids)))
         cur = torch.cuda.current_stream(self.device)
         for s in set(slots.values()):
             cur.wait_event(self.ready[s])
+        self.held.update(slots.values())
         return [self._views(slots[e]) for e in ids]
 
     def experts_for(self, layer: int, expert_ids) -> dict:

@@ -404,23 +404,39 @@ def _stacked_expert_tables(experts: dict, E: int, d: int, dev):
     return tabs, n_inter
 
 
-def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: dict, experts, config) -> torch.Tensor:
+def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: dict, experts, config, *,
+              layer: int | None = None, routing=None) -> torch.Tensor:
     """inference/forward.py:112-153 with the routed experts handed in.
 
-    ``experts`` maps an expert index to its weight dict (a Mapping, or a
-    callable taking the index) on the same device, or is one dict of stacked
-    weights ``{"gate_proj": (w (E, n, k), s (E, ceil(n/128), ceil(k/128))), ...}``
-    (all experts of the layer contiguous: no per-expert host work); the
-    reference's weight_store / gpu_transfer streaming is out of scope here.  As in the
-    reference, the chosen indices come to the host once (one synchronisation).
-    amla_moe_experts then runs each chosen expert once over all tokens that
-    chose it (the reference loops over (token, k) pairs), and the combine keeps
-    the reference's order and bf16 roundings: per token, k = 0.. accumulates
-    bf16(bf16(w_k) * expert_k(x)) into a bf16 sum, then shared + sum * 2.5.
+    ``experts`` is one of:
+
+    * a mapping (or a callable) from expert index to its weight dict on the same device;
+    * one dict of stacked weights ``{"gate_proj": (w (E, n, k), s (E, ceil(n/128),
+      ceil(k/128))), ...}`` (all experts of the layer contiguous: no per-expert host work);
+    * an ``amla.experts.ExpertStreamer`` (with ``layer=``): the chosen experts are streamed
+      from host memory in waves of at most the pool size, each wave computed before the
+      next one is copied, so any batch runs on any pool (gpu_transfer.py:50-89 plus
+      forward.py:140-151 without the per-token host synchronisation).
+
+    ``routing=(indices, weights)`` reuses a routing already computed (``route``), so a caller
+    that routed to prefetch experts does not route twice.  As in the reference, the chosen
+    indices come to the host once (one synchronisation).  amla_moe_experts then runs each
+    chosen expert once over all tokens that chose it (the reference loops over (token, k)
+    pairs), and the combine keeps the reference's order and bf16 roundings: per token,
+    k = 0.. accumulates bf16(bf16(w_k) * expert_k(x)) into a bf16 sum, then shared + sum * 2.5.
     """
-    stacked = isinstance(experts, dict) and "gate_proj" in experts and experts["gate_proj"][0].dim() == 3
-    get = None if stacked else (experts if callable(experts) else experts.__getitem__)
-    idx, w = route(hidden, gate_weight, config)
+    from .experts import ExpertStreamer
+
+    streamed = isinstance(experts, ExpertStreamer)
+    if streamed and layer is None:
+        raise ValueError("moe_block: an ExpertStreamer needs layer=")
+    stacked = not streamed and isinstance(experts, dict) and "gate_proj" in experts and \
+        experts["gate_proj"][0].dim() == 3
+    get = None if stacked or streamed else (experts if callable(experts) else experts.__getitem__)
+    if routing is not None:
+        idx, w = routing
+    else:
+        idx, w = route(hidden, gate_weight, config)
     shared_out = expert_ffn(hidden, shared_weights)
     d = hidden.shape[-1]
     top_k = config.num_experts_per_tok
@@ -434,6 +450,9 @@ def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: d
         return out
     idx_host = idx.reshape(m, top_k).cpu().contiguous()
     dev = hidden.device
+    if streamed:
+        eout = _moe_experts_streamed(h2, idx_host, experts, layer, config)
+        return _moe_combine(shared_out, eout, w, m, top_k, d, config, out, hidden)
     if stacked:
         tables, n_inter = _stacked_expert_tables(experts, E, d, dev)
         keep = []
@@ -463,17 +482,57 @@ def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: d
                 tuple(ew["down_proj"][0].shape) != (d, ni):
             raise ValueError(f"moe_block: expert {e} weights do not match hidden size {d}")
     eout = torch.empty(m, top_k, d, dtype=BF16, device=hidden.device)
-    ws = workspace(hidden.device, lib().amla_moe_experts_workspace_bytes(m, d, top_k, n_inter))
-    stream = _stream_ptr(hidden)
+    _moe_experts_call(h2, idx_host, tables, n_inter, E, eout)
+    del keep
+    return _moe_combine(shared_out, eout, w, m, top_k, d, config, out, hidden)
+
+
+def _moe_experts_call(h2, idx_host, tables, n_inter, E, eout) -> None:
+    """amla_moe_experts over the (token, k) slots whose index is >= 0."""
+    m, top_k = idx_host.shape
+    d = h2.shape[1]
+    ws = workspace(h2.device, lib().amla_moe_experts_workspace_bytes(m, d, top_k, n_inter))
     check(lib().amla_moe_experts(h2.data_ptr(), m, d, top_k, idx_host.data_ptr(), n_inter, E,
                                  *[ctypes.cast(t, ctypes.c_void_p) for t in tables], eout.data_ptr(),
-                                 ws.data_ptr(), ws.numel(), stream), "moe_experts")
+                                 ws.data_ptr(), ws.numel(), _stream_ptr(h2)), "moe_experts")
+
+
+def _moe_combine(shared_out, eout, w, m, top_k, d, config, out, hidden):
     sh = shared_out.reshape(m, d).contiguous()
     wc = w.reshape(m, top_k).contiguous()
     check(lib().amla_moe_combine(sh.data_ptr(), eout.data_ptr(), wc.data_ptr(), m, top_k, d,
-                                 float(config.routed_scaling_factor), out.data_ptr(), stream), "moe_combine")
-    del keep
+                                 float(config.routed_scaling_factor), out.data_ptr(), _stream_ptr(hidden)),
+          "moe_combine")
     return out
+
+
+def _moe_experts_streamed(h2, idx_host, streamer, layer, config) -> torch.Tensor:
+    """Routed experts streamed in waves of at most ``streamer.slots`` distinct experts: the
+    wave's copies (ordered on the device before its compute), then amla_moe_experts over the
+    slots of that wave only (the others carry index -1); the next wave's copies reuse slots
+    only after this wave's compute (``ExpertStreamer`` releases on the next call)."""
+    m, top_k = idx_host.shape
+    d = h2.shape[1]
+    E = config.n_routed_experts
+    chosen = torch.unique(idx_host).tolist()
+    eout = torch.empty(m, top_k, d, dtype=BF16, device=h2.device)
+    n_inter = None
+    for w0 in range(0, len(chosen), streamer.slots):
+        wave = chosen[w0:w0 + streamer.slots]
+        table = streamer.experts_for(layer, wave)
+        tables = [(ctypes.c_void_p * E)() for _ in range(6)]
+        for e, ew in table.items():
+            for j, key in enumerate(("gate_proj", "up_proj", "down_proj")):
+                wt, sc = ew[key]
+                tables[2 * j][e] = wt.data_ptr()
+                tables[2 * j + 1][e] = sc.data_ptr()
+            n_inter = ew["gate_proj"][0].shape[0]
+        in_wave = torch.zeros(E, dtype=torch.bool)
+        in_wave[wave] = True
+        idx_w = torch.where(in_wave[idx_host], idx_host, torch.full_like(idx_host, -1)).contiguous()
+        _moe_experts_call(h2, idx_w, tables, n_inter, E, eout)
+    streamer.release()
+    return eout
 
 
 # ------------------------------------------------------------------ output head

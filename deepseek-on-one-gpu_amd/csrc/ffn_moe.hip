@@ -481,7 +481,8 @@ int amla_moe_experts(const void *hidden, int64_t m, int64_t d, int top_k, const 
                 "moe_experts: needs hidden %% 128 == 0, intermediate %% 256 == 0 and 16-byte aligned rows");
   for (int64_t i = 0; i < m * top_k; ++i) {
     const int64_t e = indices[i];
-    if (e < 0 || e >= n_experts) return fail(AMLA_EINVAL, "moe_experts: expert index %lld out of range", (long long)e);
+    if (e < 0) continue;  // a slot left to another call (its expert_out row is not written)
+    if (e >= n_experts) return fail(AMLA_EINVAL, "moe_experts: expert index %lld out of range", (long long)e);
     if (!gate_w[e] || !gate_s[e] || !up_w[e] || !up_s[e] || !down_w[e] || !down_s[e] || !aligned16(gate_w[e]) ||
         !aligned16(up_w[e]) || !aligned16(down_w[e]))
       return fail(AMLA_EINVAL, "moe_experts: expert %lld has a null or misaligned weight", (long long)e);
@@ -502,11 +503,14 @@ int amla_moe_experts(const void *hidden, int64_t m, int64_t d, int top_k, const 
   std::vector<int32_t> order;
   for (int64_t t0 = 0; t0 < m; t0 += L.chunk_tokens) {
     const int nt = (int)std::min<int64_t>(L.chunk_tokens, m - t0);
-    const int ns = nt * top_k;
-    // slots of this chunk sorted by expert (stable: token-major within an expert)
-    order.resize(ns);
-    for (int i = 0; i < ns; ++i) order[i] = i;
+    // slots of this chunk with an expert (index >= 0), sorted by expert
+    // (stable: token-major within an expert)
     const int64_t *ix = indices + t0 * top_k;
+    order.clear();
+    for (int i = 0; i < nt * top_k; ++i)
+      if (ix[i] >= 0) order.push_back(i);
+    const int ns = (int)order.size();
+    if (ns == 0) continue;
     std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return ix[a] < ix[b]; });
     RowList gather, scatter;
     int32_t *dg = nullptr, *dsc = nullptr;

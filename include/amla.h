@@ -194,8 +194,11 @@ size_t amla_moe_route_workspace_bytes(int64_t m, int64_t n_experts);
  * (expert_ffn of every (token, k) pair), with the experts already on the device:
  *   expert_out[t, k] = swiglu(hidden[t], expert indices[t, k])
  * indices (m, top_k) int64 in HOST memory (the reference also brings them to
- * the host); gate_w .. down_s: HOST arrays of n_experts device pointers (only
- * the chosen experts' entries are read; others may be NULL), the weights of
+ * the host); an index < 0 skips its (token, k) slot, whose expert_out row is
+ * then left as it was (a caller that holds only some experts on the device
+ * runs them in several calls); gate_w .. down_s: HOST arrays of n_experts
+ * device pointers (only the chosen experts' entries are read; others may be
+ * NULL), the weights of
  * expert e laid out as for amla_swiglu with intermediate size n_inter.  Each
  * chosen expert runs once over all of its tokens (gather, [gate | up] in one
  * skinny GEMM, silu * up, down, scatter).  hidden (m, d) bf16, expert_out
