@@ -346,9 +346,11 @@ AMLA_DEV float max_lane_groups(float v) {
 //     stays fixed, so O^T is only ever touched by MFMA (no rescaling); a head
 //     whose sum of p reaches 2^64 (a later score far above m_ref) is flagged
 //     instead and recomputed exactly by the combine;
-//   P^T (p * r_t as bf16) of the wave's heads goes to LDS; after a barrier
+//   P^T (p * r_t as bf16) of the wave's heads goes to LDS;
 //   O^T (128 latent x 128 heads, fp32) += C^T (128 x t) . P^T (t x 128), C^T
-//     by transpose reads of the wave's 128 columns of the raw tile.
+//     by transpose reads of the wave's 128 columns of the raw tile: first the
+//     wave's own 32 heads (P from registers), then, after a barrier, the other
+//     waves' 96 heads from LDS.
 // Registers: O^T takes 256 accumulators, the query fragments 144; the loop
 // must not spill (a scratch reload would wait for every copy in flight),
 // which is why the copies use scalar bases and there is no rescaling path.
@@ -618,62 +620,96 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       }
       have_ref = true;
 
-      // ---- P^T to LDS: row = head, bf16 slot 8*lg + j holds t = 4*lg + j
-      // (j < 4) or 16 + 4*lg + j - 4: exactly this lane's eight scores, and the
-      // k order of the transpose reads below
+      // ---- P^T of this wave's heads to LDS, for the other waves: row = head,
+      // bf16 slot 8*lg + j holds t = 4*lg + j (j < 4) or 16 + 4*lg + j - 4:
+      // exactly this lane's eight scores, and the k order of the transpose
+      // reads below (so pk[nt] is also this wave's own B fragment)
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
-        *reinterpret_cast<u32x4 *>(smem + P_OFF + (head0 + nt * 16 + li) * PROW + lg * 16) = pk[nt];
-      asm volatile("" ::: "memory");  // the P^T stores stay before the reads counted below
+        asm volatile("ds_write_b128 %0, %1" ::"v"(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+                         (__attribute__((address_space(3))) uint8_t *)(smem + P_OFF + (head0 + nt * 16 + li) * PROW +
+                                                                       lg * 16)))),
+                     "v"(pk[nt])
+                     : "memory");
 
       // ---- O^T (latent x head) += C^T (latent x t) . P^T (t x head).  C^T by
       // transpose reads: within a 16-lane group, lane s addresses row
       // t0 + s/4, columns c0 + 4(s%4) .. +3 and lane L receives
       // C[t0 .. t0+3][c0 + L]; t0 = 4*lg and 16 + 4*lg match P^T's k order.
-      // Outputs are early-clobber (two reads share one address).  PV_DEPTH
-      // column blocks are in flight; the first ones are issued before the
-      // barrier that publishes P^T.
-      constexpr int PV_DEPTH = 3;
+      // All eight column blocks of this wave's 128 latent columns are read
+      // once and kept for both passes (outputs early-clobber: two reads share
+      // one address).  Accumulator block j holds head block (2*wave + j) & 7,
+      // so blocks 0 and 1 are this wave's own heads: their MFMAs run on P
+      // straight from registers while the other waves' P^T is written, and
+      // only the other six blocks wait for the barrier.
       const int s16 = lane & 15;
       const uint32_t a0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
           (__attribute__((address_space(3))) const uint16_t *)(K + (4 * lg + (s16 >> 2)) * KROW + wave * 128 +
                                                                 4 * (s16 & 3))));
-      u32x2 t0[PV_DEPTH], t1[PV_DEPTH];
-#define AMLA_TR(dst0, dst1, MT)                                                                            \
+      u32x2 ta[8], tb[8];
+#define AMLA_TR(MT)                                                                                        \
   asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"               \
-               : "=&v"(dst0), "=&v"(dst1)                                                                \
+               : "=&v"(ta[MT]), "=&v"(tb[MT])                                                            \
                : "v"(a0), "i"((MT) * 32), "i"((MT) * 32 + 16 * KROW * 2))
-#pragma unroll
-      for (int d = 0; d < PV_DEPTH; ++d) AMLA_TR(t0[d], t1[d], d);
-      // P^T writes done (the 2*PV_DEPTH reads after them may stay in flight)
-      asm volatile("s_waitcnt lgkmcnt(6)" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      const uint32_t paddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-          (__attribute__((address_space(3))) const uint8_t *)(smem + P_OFF + li * PROW + lg * 16)));
-      u32x4 pb[8];
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt)
-        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(pb[nt]) : "v"(paddr), "i"(nt * 16 * PROW));
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(pb[0]), "+v"(pb[1]), "+v"(pb[2]), "+v"(pb[3]), "+v"(pb[4]), "+v"(pb[5]), "+v"(pb[6]),
-                     "+v"(pb[7]), "+v"(t0[0]), "+v"(t1[0])::"memory");
+      AMLA_TR(0); AMLA_TR(1); AMLA_TR(2); AMLA_TR(3); AMLA_TR(4); AMLA_TR(5); AMLA_TR(6); AMLA_TR(7);
+#undef AMLA_TR
+      // wait for column block MT's reads (LDS operations complete in order:
+      // 2 * (7 - MT) reads were issued after them); the P^T writes before them
+      // are then complete too
+#define AMLA_WTR(MT, N) \
+  asm volatile("s_waitcnt lgkmcnt(" #N ")" : "+v"(ta[MT]), "+v"(tb[MT])::"memory")
+      // the own-head MFMAs read pk, written by VALU (the cvt/pack above): cover
+      // the VALU write -> MFMA read wait states the compiler does not see
+      asm volatile("s_nop 4" : "+v"(pk[0]), "+v"(pk[1])::"memory");
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) {
-        const int c = mt % PV_DEPTH;
-        const int ahead = (7 - mt) < (PV_DEPTH - 1) ? (7 - mt) : (PV_DEPTH - 1);
-        if (mt > 0) {
-          if (ahead == 2) asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
-          else if (ahead == 1) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
-          else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(t0[c]), "+v"(t1[c])::"memory");
+        switch (mt) {
+          case 0: AMLA_WTR(0, 14); break;
+          case 1: AMLA_WTR(1, 12); break;
+          case 2: AMLA_WTR(2, 10); break;
+          case 3: AMLA_WTR(3, 8); break;
+          case 4: AMLA_WTR(4, 6); break;
+          case 5: AMLA_WTR(5, 4); break;
+          case 6: AMLA_WTR(6, 2); break;
+          default: AMLA_WTR(7, 0); break;
         }
-        const bf16x8 a = as_bf16x8(u32x4{t0[c].x, t0[c].y, t1[c].x, t1[c].y});
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt)  // accumulators pinned to AGPRs (only these MFMAs touch them in the loop)
-          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(o[mt][nt]) : "v"(a), "v"(pb[nt]));
-        if (mt + PV_DEPTH < 8) AMLA_TR(t0[c], t1[c], mt + PV_DEPTH);
+        const bf16x8 a = as_bf16x8(u32x4{ta[mt].x, ta[mt].y, tb[mt].x, tb[mt].y});
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(o[mt][0]) : "v"(a), "v"(pk[0]));
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(o[mt][1]) : "v"(a), "v"(pk[1]));
       }
-#undef AMLA_TR
+#undef AMLA_WTR
+      // every LDS operation of this wave is complete (lgkmcnt(0) above): after
+      // the barrier all waves' P^T is visible
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      u32x4 pb[6];
+      {
+        const uint32_t paddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+            (__attribute__((address_space(3))) const uint8_t *)(smem + P_OFF + li * PROW + lg * 16)));
+#pragma unroll
+        for (int j = 0; j < 6; ++j) {
+          const uint32_t off = static_cast<uint32_t>((((2 * wave + 2 + j) & 7) * 16) * PROW);  // wave-uniform
+          asm volatile("ds_read_b128 %0, %1" : "=v"(pb[j]) : "v"(paddr + off));
+        }
+      }
+#define AMLA_WPB(J, N) asm volatile("s_waitcnt lgkmcnt(" #N ")" : "+v"(pb[J])::"memory")
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        switch (j) {
+          case 0: AMLA_WPB(0, 5); break;
+          case 1: AMLA_WPB(1, 4); break;
+          case 2: AMLA_WPB(2, 3); break;
+          case 3: AMLA_WPB(3, 2); break;
+          case 4: AMLA_WPB(4, 1); break;
+          default: AMLA_WPB(5, 0); break;
+        }
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) {  // accumulators pinned to AGPRs (only these MFMAs touch them in the loop)
+          const bf16x8 a = as_bf16x8(u32x4{ta[mt].x, ta[mt].y, tb[mt].x, tb[mt].y});
+          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(o[mt][2 + j]) : "v"(a), "v"(pb[j]));
+        }
+      }
+#undef AMLA_WPB
       __builtin_amdgcn_sched_barrier(0);
 
       // barrier without a memory fence: a fence would also wait for the copy
@@ -714,7 +750,8 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt)
-      *reinterpret_cast<u32x2 *>(smem + (nt * 16 + li) * OROW + (wave * 128 + mt * 16 + 4 * lg) * 2) =
+      *reinterpret_cast<u32x2 *>(smem + ((((2 * wave + nt) & 7) * 16) + li) * OROW +
+                                 (wave * 128 + mt * 16 + 4 * lg) * 2) =
           u32x2{pack_bf16(o[mt][nt].x, o[mt][nt].y), pack_bf16(o[mt][nt].z, o[mt][nt].w)};
   __syncthreads();
   uint8_t *const dst = reinterpret_cast<uint8_t *>(p.part_o + (size_t)slot * HEADS * LORA);
