@@ -362,10 +362,17 @@ constexpr int F_NW = 8;                            // waves per workgroup (two p
 constexpr int F_QB = F_NW * F_QW;                  // queries per workgroup
 constexpr int F_RPW = F_KT / F_NW;                 // key rows each wave copies per tile
 constexpr int F_NST = 3;                           // LDS stages (copies run two tiles ahead)
-// one stage: k_nope rows (256 B), rope-key rows (128 B), value rows (256 B);
-// 16-byte chunks swizzled per row so that the fragment reads hit distinct banks
-constexpr int F_NOPE = 0, F_RPE = F_KT * 256, F_VAL = F_RPE + F_KT * 128;
-constexpr int F_STAGE = F_VAL + F_KT * 256;        // 40 KB
+// one stage: k_nope as two arrays of 128 B half-rows (dims 0-63 of every key,
+// then dims 64-127), rope-key rows (128 B), values as two arrays of 128 B
+// half-rows.  LDS has 128 banks of 4 B (a 512 B window = four half-rows): a
+// 16-byte read serves 32 lanes per pass and a transpose read 64 lanes, so the
+// chunks are swizzled per row (chunk c of a k_nope / rope half-row r at
+// c ^ ((r >> 2) & 7), 64-byte segment g of a value half-row at g ^ ((r >> 2) & 1))
+// and the 32 key rows of a fragment read, and the 8 x 64 B of a transpose
+// read, each cover the window once.
+constexpr int F_HALF = F_KT * 128;                 // one array of half-rows
+constexpr int F_NOPE = 0, F_RPE = 2 * F_HALF, F_VAL = 3 * F_HALF;
+constexpr int F_STAGE = F_VAL + 2 * F_HALF;        // 40 KB
 constexpr int F_LDS = F_NST * F_STAGE;
 constexpr int F_DMA = 5 * F_RPW / 8;               // copies per wave per tile
 
@@ -380,90 +387,81 @@ struct FlashParams {
   float scale_log2;
 };
 
-// Wave w copies key rows F_RPW w .. +F_RPW-1 of the tile (k_nope, value and rope key)
-// straight into LDS: each global_load_lds writes 64 lanes x 16 B contiguously,
-// so the swizzle is applied to the source chunk each lane fetches.  Slot
-// (row, c) holds chunk c ^ (row & 7) of a k_nope or rope-key row and chunk
-// c ^ 2(row & 3) of a value row.  Inside the keys in use the row bases are
-// scalar and each lane adds a fixed offset; the tile that crosses Tlim
+// Wave w copies key rows F_RPW w .. +F_RPW-1 of the tile (both k_nope halves,
+// both value halves and the rope key) straight into LDS: each global_load_lds
+// writes 64 lanes x 16 B contiguously (8 half-rows), so the swizzle is applied
+// to the source chunk each lane fetches.  Inside the keys in use the row bases
+// are scalar and each lane adds a fixed offset; the tile that crosses Tlim
 // clamps rows to Tlim - 1 per lane (in bounds; their scores are masked).
 struct FlashLane {
-  uint32_t nope[2];  // lane offset of k_nope copies j even / odd (row r16 of 4, swizzled chunk)
-  uint32_t val;      // lane offset of value copies
-  uint32_t rope;     // lane offset of rope-key copies (row r8 of 8)
+  uint32_t nope;  // lane offset of k_nope copies (row r8 of 8, swizzled chunk; + 128 B for the second half)
+  uint32_t val;   // lane offset of value copies (+ 128 B for the second half)
+  uint32_t rope;  // lane offset of rope-key copies
 };
 
-AMLA_DEV FlashLane flash_lane(int lane) {
-  const int r16 = lane >> 4, c16 = lane & 15, r8 = lane >> 3, c8 = lane & 7;
+// chunk of a k_nope / rope half-row slot c8 of copy row r8 (key row 8 w + r8) holds
+AMLA_DEV int flash_kchunk(int wave, int lane) { return (lane & 7) ^ ((2 * wave + (lane >> 5)) & 7); }
+// chunk of a value half-row slot c8 holds (the 64-byte segment moves with bit 2 of the row)
+AMLA_DEV int flash_vchunk(int lane) { return (lane & 7) ^ (4 * ((lane >> 5) & 1)); }
+
+AMLA_DEV FlashLane flash_lane(int wave, int lane) {
+  const int r8 = lane >> 3;
   FlashLane fl;
-  fl.nope[0] = r16 * P_KVROW + 16 * (c16 ^ r16);
-  fl.nope[1] = r16 * P_KVROW + 16 * (c16 ^ (4 + r16));
-  fl.val = r16 * P_KVROW + P_NOPE * 2 + 16 * (c16 ^ (2 * r16));
-  fl.rope = r8 * (P_ROPE * 2) + 16 * (c8 ^ r8);
+  fl.nope = r8 * P_KVROW + 16 * flash_kchunk(wave, lane);
+  fl.val = r8 * P_KVROW + P_NOPE * 2 + 16 * flash_vchunk(lane);
+  fl.rope = r8 * (P_ROPE * 2) + 16 * flash_kchunk(wave, lane);
   return fl;
 }
 
 AMLA_DEV void flash_dma(const FlashParams &p, int h, int t0, int Tlim, uint8_t *stage, int wave, int lane,
                         const FlashLane &fl) {
+  static_assert(F_RPW == 8, "one copy covers the 8 rows of a wave");
   const char *kv = reinterpret_cast<const char *>(p.kvb) + h * ((P_NOPE + P_V) * 2);
   const char *kr = reinterpret_cast<const char *>(p.kpe);
+  const int row = F_RPW * wave;
   if (t0 + F_KT <= Tlim) {
-    const char *kvw = kv + (size_t)(t0 + F_RPW * wave) * P_KVROW;
-    const char *krw = kr + (size_t)(t0 + F_RPW * wave) * (P_ROPE * 2);
+    const char *kvw = kv + (size_t)(t0 + row) * P_KVROW;
+    const char *krw = kr + (size_t)(t0 + row) * (P_ROPE * 2);
 #pragma unroll
-    for (int j = 0; j < F_RPW / 4; ++j) {
-      const int row = F_RPW * wave + 4 * j;
-      __builtin_amdgcn_global_load_lds(kvw + (size_t)(4 * j) * P_KVROW + fl.nope[j & 1],
-                                       LDS_PTR(stage + F_NOPE + row * 256), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(kvw + (size_t)(4 * j) * P_KVROW + fl.val, LDS_PTR(stage + F_VAL + row * 256),
+    for (int half = 0; half < 2; ++half) {
+      __builtin_amdgcn_global_load_lds(kvw + 128 * half + fl.nope, LDS_PTR(stage + F_NOPE + half * F_HALF + row * 128),
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds(kvw + 128 * half + fl.val, LDS_PTR(stage + F_VAL + half * F_HALF + row * 128),
                                        16, 0, 0);
     }
-#pragma unroll
-    for (int j = 0; j < F_RPW / 8; ++j)
-      __builtin_amdgcn_global_load_lds(krw + 8 * j * (P_ROPE * 2) + fl.rope,
-                                       LDS_PTR(stage + F_RPE + (F_RPW * wave + 8 * j) * 128), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(krw + fl.rope, LDS_PTR(stage + F_RPE + row * 128), 16, 0, 0);
     return;
   }
-  const int r16 = lane >> 4, c16 = lane & 15, r8 = lane >> 3, c8 = lane & 7;
-  const int last = Tlim - 1;
+  const int t = min(t0 + row + (lane >> 3), Tlim - 1);
+  const char *src = kv + (size_t)t * P_KVROW;
+  const int kc = flash_kchunk(wave, lane), vc = flash_vchunk(lane);
 #pragma unroll
-  for (int j = 0; j < F_RPW / 4; ++j) {
-    const int row = F_RPW * wave + 4 * j;
-    const int t = min(t0 + row + r16, last);
-    const char *src = kv + (size_t)t * P_KVROW;
-    __builtin_amdgcn_global_load_lds(src + 16 * (c16 ^ (4 * (j & 1) + r16)), LDS_PTR(stage + F_NOPE + row * 256), 16,
-                                     0, 0);
-    __builtin_amdgcn_global_load_lds(src + P_NOPE * 2 + 16 * (c16 ^ (2 * r16)), LDS_PTR(stage + F_VAL + row * 256),
+  for (int half = 0; half < 2; ++half) {
+    __builtin_amdgcn_global_load_lds(src + 128 * half + 16 * kc, LDS_PTR(stage + F_NOPE + half * F_HALF + row * 128),
                                      16, 0, 0);
+    __builtin_amdgcn_global_load_lds(src + P_NOPE * 2 + 128 * half + 16 * vc,
+                                     LDS_PTR(stage + F_VAL + half * F_HALF + row * 128), 16, 0, 0);
   }
-#pragma unroll
-  for (int j = 0; j < F_RPW / 8; ++j) {
-    const int row = F_RPW * wave + 8 * j;
-    const int t = min(t0 + row + r8, last);
-    __builtin_amdgcn_global_load_lds(kr + (size_t)t * (P_ROPE * 2) + 16 * (c8 ^ r8), LDS_PTR(stage + F_RPE + row * 128),
-                                     16, 0, 0);
-  }
+  __builtin_amdgcn_global_load_lds(kr + (size_t)t * (P_ROPE * 2) + 16 * kc, LDS_PTR(stage + F_RPE + row * 128), 16,
+                                   0, 0);
 }
 
 // Copy PIECE (0 .. F_DMA-1) of a tile wholly inside the keys in use: k_nope
-// copies, then value copies, then rope-key copies (the order of flash_dma).
+// halves, value halves, then the rope keys.
 AMLA_DEV void flash_dma_piece(const FlashParams &p, int h, int t0, uint8_t *stage, int wave, const FlashLane &fl,
                               int piece) {
-  constexpr int NJ = F_RPW / 4;
-  const char *kvw = reinterpret_cast<const char *>(p.kvb) + h * ((P_NOPE + P_V) * 2) + (size_t)(t0 + F_RPW * wave) * P_KVROW;
-  if (piece < NJ) {
-    const int j = piece;
-    __builtin_amdgcn_global_load_lds(kvw + (size_t)(4 * j) * P_KVROW + fl.nope[j & 1],
-                                     LDS_PTR(stage + F_NOPE + (F_RPW * wave + 4 * j) * 256), 16, 0, 0);
-  } else if (piece < 2 * NJ) {
-    const int j = piece - NJ;
-    __builtin_amdgcn_global_load_lds(kvw + (size_t)(4 * j) * P_KVROW + fl.val,
-                                     LDS_PTR(stage + F_VAL + (F_RPW * wave + 4 * j) * 256), 16, 0, 0);
+  const int row = F_RPW * wave;
+  const char *kvw = reinterpret_cast<const char *>(p.kvb) + h * ((P_NOPE + P_V) * 2) + (size_t)(t0 + row) * P_KVROW;
+  if (piece < 2) {
+    __builtin_amdgcn_global_load_lds(kvw + 128 * piece + fl.nope, LDS_PTR(stage + F_NOPE + piece * F_HALF + row * 128),
+                                     16, 0, 0);
+  } else if (piece < 4) {
+    const int half = piece - 2;
+    __builtin_amdgcn_global_load_lds(kvw + 128 * half + fl.val, LDS_PTR(stage + F_VAL + half * F_HALF + row * 128),
+                                     16, 0, 0);
   } else {
-    const int j = piece - 2 * NJ;
-    const char *krw = reinterpret_cast<const char *>(p.kpe) + (size_t)(t0 + F_RPW * wave) * (P_ROPE * 2);
-    __builtin_amdgcn_global_load_lds(krw + 8 * j * (P_ROPE * 2) + fl.rope,
-                                     LDS_PTR(stage + F_RPE + (F_RPW * wave + 8 * j) * 128), 16, 0, 0);
+    const char *krw = reinterpret_cast<const char *>(p.kpe) + (size_t)(t0 + row) * (P_ROPE * 2);
+    __builtin_amdgcn_global_load_lds(krw + fl.rope, LDS_PTR(stage + F_RPE + row * 128), 16, 0, 0);
   }
 }
 
@@ -500,7 +498,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
   const int wave_last_pos = pos0 + min(s_wave + F_QW, p.S) - 1;
   const float sl2 = p.scale_log2;
 
-  const FlashLane fl = flash_lane(lane);
+  const FlashLane fl = flash_lane(wave, lane);
   flash_dma(p, h, 0, Tlim, fsm, wave, lane, fl);
 
   // Q^T fragments: column = query s_wave + 32 qg + j32, dims 16 ks + 8 hh .. +7
@@ -526,24 +524,20 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
   }
 
   // per-lane LDS offsets.  K fragment (A of S^T): key row 32 kg + j32, chunk
-  // (2 ks + hh) ^ (j32 & 7).  V^T by ds_read_b64_tr_b16: in a 16-lane group g,
-  // lane L addresses value row t + L/4 and columns c0 + 4 (L%4) .. +3 with
-  // c0 = 32 vt + 16 (g & 1), and receives column c0 + L of rows t .. t+3.
-  const int x7 = j32 & 7;
+  // 2 ks + hh of half-row array ks / 4 (arrays 0, 1: k_nope; 2: rope), at slot
+  // (2 ks + hh) ^ ((j32 >> 2) & 7).  V^T by ds_read_b64_tr_b16: in a 16-lane
+  // group g, lane L addresses value row t + L/4 and columns c0 + 4 (L%4) .. +3
+  // with c0 = 32 vt + 16 (g & 1), and receives column c0 + L of rows t .. t+3;
+  // rows t = 8i + 4 hh, so the segment of column block vt sits at (vt & 1) ^ hh.
   const int L16 = lane & 15, g16 = lane >> 4;
   const int vrow = L16 >> 2;
-  int koff[4], roff[4];
+  int koff[4];
 #pragma unroll
-  for (int k4 = 0; k4 < 4; ++k4) {
-    koff[k4] = F_NOPE + j32 * 256 + 16 * ((2 * k4 + hh) ^ x7);
-    roff[k4] = F_RPE + j32 * 128 + 16 * ((2 * k4 + hh) ^ x7);
-  }
-  int voff[2];  // vt even / odd (bit 2 of the chunk index meets the swizzle)
+  for (int k4 = 0; k4 < 4; ++k4) koff[k4] = F_NOPE + j32 * 128 + 16 * ((2 * k4 + hh) ^ ((j32 >> 2) & 7));
+  int voff[2];  // vt even / odd
 #pragma unroll
-  for (int par = 0; par < 2; ++par) {
-    const int chunk = 4 * par + 2 * (g16 & 1) + ((L16 & 3) >> 1);
-    voff[par] = F_VAL + (4 * hh + vrow) * 256 + 16 * (chunk ^ (2 * vrow)) + 8 * (L16 & 1);
-  }
+  for (int par = 0; par < 2; ++par)
+    voff[par] = F_VAL + (4 * hh + vrow) * 128 + 64 * (par ^ hh) + 32 * (g16 & 1) + 8 * (L16 & 3);
 
   // ---- software pipeline over 32-key groups g (tile g/2, half g%2).  Step
   // A of g computes S_{g+1} while exponentiating group g; step B accumulates
@@ -552,7 +546,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
   // runs all groups of the block; groups past its queries are fully masked.
   const uint32_t lds0 = static_cast<uint32_t>(
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t *)fsm));
-  uint32_t kb[4], rb[4], vb0, vb1;
+  uint32_t kb[4], vb0, vb1;
   f32x16 scA[F_NQG], scB[F_NQG];
   u32x4 pb[F_NQG][2];  // [qg][16-key step]: bf16 P of the group being accumulated
   float nm[F_NQG];     // -running max (scaled) per query group
@@ -565,10 +559,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
 #define FL_KBASE(STG)                                      \
   {                                                        \
     const uint32_t sb_ = lds0 + (STG) * F_STAGE;           \
-    _Pragma("unroll") for (int k4 = 0; k4 < 4; ++k4) {     \
-      kb[k4] = sb_ + koff[k4];                             \
-      rb[k4] = sb_ + roff[k4];                             \
-    }                                                      \
+    _Pragma("unroll") for (int k4 = 0; k4 < 4; ++k4) kb[k4] = sb_ + koff[k4]; \
   }
 #define FL_VBASE(STG)                                      \
   {                                                        \
@@ -579,8 +570,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
 #define FL_RDK(D, KS, KG)                                                                      \
   asm volatile("ds_read_b128 %0, %1 offset:%2"                                                \
                : "=v"(D)                                                                      \
-               : "v"((KS) < 8 ? kb[(KS) & 3] : rb[(KS) & 3]),                                 \
-                 "i"((KS) < 8 ? ((KS) >> 2) * 128 + (KG) * 8192 : (KG) * 4096)                \
+               : "v"(kb[(KS) & 3]), "i"(((KS) >> 2) * F_HALF + (KG) * 32 * 128)             \
                : "memory")
   // exp slice q4 of query group QG of SCE (rows 4 q4 .. +3) -> pb, l.  The
   // empty asm statements pin each slice between the MFMAs it is meant to
@@ -653,7 +643,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
       "ds_read_b64_tr_b16 %0, %4 offset:%5\n\tds_read_b64_tr_b16 %1, %4 offset:%6\n\t"              \
       "ds_read_b64_tr_b16 %2, %4 offset:%7\n\tds_read_b64_tr_b16 %3, %4 offset:%8"                  \
       : "=&v"(D[0]), "=&v"(D[1]), "=&v"(D[2]), "=&v"(D[3])                                          \
-      : "v"(BASE), "i"(OFS), "i"(OFS + 2048), "i"(OFS + 4096), "i"(OFS + 6144)                      \
+      : "v"(BASE), "i"(OFS), "i"(OFS + 1024), "i"(OFS + 2048), "i"(OFS + 3072)                      \
       : "memory")
 #define FL_WAIT(N, D) \
   asm volatile("s_waitcnt lgkmcnt(" #N ")" : "+v"(D[0]), "+v"(D[1]), "+v"(D[2]), "+v"(D[3])::"memory")
@@ -673,13 +663,13 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
   {                                                                                                  \
     if (DOMAX) _Pragma("unroll") for (int qg = 0; qg < F_NQG; ++qg) mx[qg] = -INFINITY;              \
     u32x2 tv[3][4];                                                                                  \
-    FL_TR(tv[0], vb0, (KG) * 8192);                                                                  \
-    FL_TR(tv[1], vb1, (KG) * 8192);                                                                  \
-    FL_TR(tv[2], vb0, (KG) * 8192 + 128);                                                            \
+    FL_TR(tv[0], vb0, (KG) * 4096);                                                                  \
+    FL_TR(tv[1], vb1, (KG) * 4096);                                                                  \
+    FL_TR(tv[2], vb0, (KG) * 4096 + F_HALF);                                                         \
     FL_WAIT(8, tv[0]);                                                                               \
     FL_PVSTEP(0, tv[0], 0, SCN, GI, DOMAX, MASKED);                                                  \
     FL_PVSTEP(0, tv[0], 1, SCN, GI, DOMAX, MASKED);                                                  \
-    FL_TR(tv[0], vb1, (KG) * 8192 + 128);                                                            \
+    FL_TR(tv[0], vb1, (KG) * 4096 + F_HALF);                                                         \
     FL_WAIT(8, tv[1]);                                                                               \
     FL_PVSTEP(1, tv[1], 0, SCN, GI, DOMAX, MASKED);                                                  \
     FL_PVSTEP(1, tv[1], 1, SCN, GI, DOMAX, MASKED);                                                  \
