@@ -320,7 +320,16 @@ def ffn_extras(B, dev):
     out["moe_block_b8_experts"] = n_used
     moved = (n_used + 1) * 3 * mi * d + E * d * 2
     out["moe_block_b8_hbm_gbs"] = round(moved / (ms * 1e-3) / 1e9, 1)
-    del experts, shared
+    # the same block with the indices brought to the host for the grouping (one synchronisation)
+    ms = _time_eager(lambda: ops.moe_block(x, gw, shared, experts, CFG, device_grouping=False), 10)
+    out["moe_block_b8_host_grouping_us"] = round(ms * 1000, 2)
+    # grouped on the device: the whole block captured in one HIP graph and replayed
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.moe_block(x, gw, shared, experts, CFG)
+    ms = _time_eager(graph.replay, 10)
+    out["moe_block_b8_graph_us"] = round(ms * 1000, 2)
+    del graph, experts, shared
     torch.cuda.empty_cache()
     return out
 

@@ -65,6 +65,9 @@ SIGNATURES = [
     ("amla_moe_experts", c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     ("amla_moe_experts_workspace_bytes", c_size_t, [c_int64, c_int64, c_int, c_int64]),
+    ("amla_moe_experts_dev", c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_int64, c_int64, c_void_p,
+                                     c_void_p, c_void_p, c_size_t, c_void_p]),
+    ("amla_moe_experts_dev_workspace_bytes", c_size_t, [c_int64, c_int64, c_int, c_int64, c_int64]),
     ("amla_bf16_logits", c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     ("amla_argmax", c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     ("amla_sample_top_p", c_int, [c_void_p, c_int64, c_int64, c_int64, c_float, c_float, ctypes.c_uint64, c_void_p,

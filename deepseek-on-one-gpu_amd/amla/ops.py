@@ -404,8 +404,26 @@ def _stacked_expert_tables(experts: dict, E: int, d: int, dev):
     return tabs, n_inter
 
 
+_device_table_cache: dict = {}
+
+
+def _stacked_device_table(experts: dict, E: int, d: int, dev):
+    """Device pointer table [gate_w | gate_s | up_w | up_s | down_w | down_s] x E of stacked
+    expert weights (amla_moe_experts_dev), made once per set of tensors."""
+    tabs, n_inter = _stacked_expert_tables(experts, E, d, dev)
+    key = tuple(t[0] for t in tabs) + (E, str(dev))
+    hit = _device_table_cache.get(key)
+    if hit is None:
+        flat = [int(t[e] or 0) for t in tabs for e in range(E)]
+        hit = torch.tensor(flat, dtype=torch.int64).to(dev)
+        if len(_device_table_cache) > 64:
+            _device_table_cache.clear()
+        _device_table_cache[key] = hit
+    return hit, n_inter
+
+
 def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: dict, experts, config, *,
-              layer: int | None = None, routing=None) -> torch.Tensor:
+              layer: int | None = None, routing=None, device_grouping: bool = True) -> torch.Tensor:
     """inference/forward.py:112-153 with the routed experts handed in.
 
     ``experts`` is one of:
@@ -419,9 +437,12 @@ def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: d
       forward.py:140-151 without the per-token host synchronisation).
 
     ``routing=(indices, weights)`` reuses a routing already computed (``route``), so a caller
-    that routed to prefetch experts does not route twice.  As in the reference, the chosen
-    indices come to the host once (one synchronisation).  amla_moe_experts then runs each
-    chosen expert once over all tokens that chose it (the reference loops over (token, k)
+    that routed to prefetch experts does not route twice.  With stacked weights (and
+    ``device_grouping``, the default) the slots are grouped by expert on the device
+    (amla_moe_experts_dev): no host copy of the indices and no synchronisation, so the whole
+    block can be captured in a HIP graph.  Otherwise, as in the reference, the chosen indices
+    come to the host once (one synchronisation) for amla_moe_experts.  Either way each chosen
+    expert runs once over all tokens that chose it (the reference loops over (token, k)
     pairs), and the combine keeps the reference's order and bf16 roundings: per token,
     k = 0.. accumulates bf16(bf16(w_k) * expert_k(x)) into a bf16 sum, then shared + sum * 2.5.
     """
@@ -448,8 +469,13 @@ def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: d
     out = torch.empty_like(hidden)
     if m == 0:
         return out
-    idx_host = idx.reshape(m, top_k).cpu().contiguous()
     dev = hidden.device
+    if stacked and device_grouping and E <= MOE_DEV_MAX_EXPERTS:
+        table, n_inter = _stacked_device_table(experts, E, d, dev)
+        eout = torch.empty(m, top_k, d, dtype=BF16, device=dev)
+        _moe_experts_dev_call(h2, idx.reshape(m, top_k).contiguous(), table, n_inter, E, eout)
+        return _moe_combine(shared_out, eout, w, m, top_k, d, config, out, hidden)
+    idx_host = idx.reshape(m, top_k).cpu().contiguous()
     if streamed:
         eout = _moe_experts_streamed(h2, idx_host, experts, layer, config)
         return _moe_combine(shared_out, eout, w, m, top_k, d, config, out, hidden)
@@ -495,6 +521,23 @@ def _moe_experts_call(h2, idx_host, tables, n_inter, E, eout) -> None:
     check(lib().amla_moe_experts(h2.data_ptr(), m, d, top_k, idx_host.data_ptr(), n_inter, E,
                                  *[ctypes.cast(t, ctypes.c_void_p) for t in tables], eout.data_ptr(),
                                  ws.data_ptr(), ws.numel(), _stream_ptr(h2)), "moe_experts")
+
+
+MOE_DEV_MAX_EXPERTS = 512
+MOE_DEV_MAX_SLOTS = 65536
+
+
+def _moe_experts_dev_call(h2, idx_dev, table, n_inter, E, eout) -> None:
+    """amla_moe_experts_dev over token chunks of at most 65536 (token, k) slots each."""
+    m, top_k = idx_dev.shape
+    d = h2.shape[1]
+    tpc = max(1, MOE_DEV_MAX_SLOTS // top_k)
+    for t0 in range(0, m, tpc):
+        mc = min(tpc, m - t0)
+        ws = workspace(h2.device, lib().amla_moe_experts_dev_workspace_bytes(mc, d, top_k, n_inter, E))
+        check(lib().amla_moe_experts_dev(h2[t0:t0 + mc].data_ptr(), mc, d, top_k, idx_dev[t0:t0 + mc].data_ptr(),
+                                         n_inter, E, table.data_ptr(), eout[t0:t0 + mc].data_ptr(), ws.data_ptr(),
+                                         ws.numel(), _stream_ptr(h2)), "moe_experts_dev")
 
 
 def _moe_combine(shared_out, eout, w, m, top_k, d, config, out, hidden):

@@ -92,6 +92,33 @@ struct GemvGroups {
 // plan: plan_gemv_grouped(max M of the groups, N, K) (or plan_gemv).
 GemvPlan plan_gemv_grouped(int M, int N, int K);
 int launch_gemv_grouped(const GemvParams &p, GemvGroups groups, const GemvPlan &plan, hipStream_t stream);
+// Routed-expert work scheduled on the device (amla_moe_experts_dev): entries
+// of (expert, first row, rows, unused) int32, their count in device memory,
+// and the device table of expert weights [6][E]: gate_w, gate_s, up_w, up_s,
+// down_w, down_s.  Row r of an entry's x / y is row (first row + r) of the
+// gathered buffers.
+struct MoeSched {
+  const void *const *wtab;
+  const int32_t *ent;
+  const int32_t *count;
+  int E;
+  int down;  // 0: [gate | up] as two weight segments (n_split = gate rows), 1: down
+};
+AMLA_DEV void moe_sched_weights(GemvParams &p, const MoeSched &s, int e) {
+  const void *const *t = s.wtab + (s.down ? 4 : 0) * s.E;
+  p.w0 = static_cast<const uint8_t *>(t[e]);
+  p.s0 = static_cast<const float *>(t[s.E + e]);
+  p.w1 = s.down ? nullptr : static_cast<const uint8_t *>(t[2 * s.E + e]);
+  p.s1 = s.down ? nullptr : static_cast<const float *>(t[3 * s.E + e]);
+}
+// Skinny GEMMs (GEMV_PLAIN) of the scheduled entries, each with at most max_m
+// rows; grid max_entries x plan.groups.  plan: plan_gemv_grouped(max_m, N, K);
+// p.part holds plan.kparts * (rows of all entries) * N fp32 when kparts > 1
+// (entry at first row r0 uses part + kparts * r0 * N).
+int launch_gemv_sched(const GemvParams &p, const MoeSched &s, int max_entries, int max_m, const GemvPlan &plan,
+                      hipStream_t stream);
+// Large-M fp8 GEMM tiles of the scheduled entries (rows <= 256 each).
+int launch_gemm_sched(const GemvParams &p, const MoeSched &s, int max_entries, hipStream_t stream);
 // Register-streaming skinny GEMM for M <= 16 (weights HBM -> VGPRs, x in
 // LDS).  Blocks per wave per tile: at most RS_NARROW_NB with three tiles in
 // flight, or RS_WIDE_NB (one part of up to 4 * RS_WIDE_NB blocks) with one.

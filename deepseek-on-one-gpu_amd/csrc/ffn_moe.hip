@@ -4,6 +4,9 @@
 //   amla_swiglu       <- swiglu / dense_ffn / expert_ffn, inference/ops.py:186-206
 //   amla_moe_route    <- route, inference/ops.py:209-257
 //   amla_moe_experts  <- the routed-expert loop of moe_block, inference/forward.py:139-151
+//   amla_moe_experts_dev <- the same loop with the slots grouped by expert on the
+//                        device (the reference's host read of the indices,
+//                        gpu_transfer.py:60, has no counterpart)
 //   amla_moe_combine  <- the combine of moe_block, inference/forward.py:138-153
 //
 // swiglu runs gate and up as one skinny (M <= 64) or large fp8 GEMM over the
@@ -55,8 +58,11 @@ static int launch_silu_mul(const uint16_t *g, const uint16_t *u, int64_t n, uint
 }
 
 // h[r, j] = bf16( bf16(silu(gu[r, j])) * gu[r, n + j] ) for rows r of [gate | up]
+// (drows: the row count in device memory, else rows)
 __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const uint16_t *__restrict__ gu, int rows, int n,
-                                                            uint16_t *__restrict__ h) {
+                                                            uint16_t *__restrict__ h,
+                                                            const int32_t *__restrict__ drows = nullptr) {
+  if (drows) rows = *drows;
   for (int r = blockIdx.y; r < rows; r += gridDim.y) {
     const uint16_t *g = gu + (size_t)r * 2 * n, *u = g + n;
     for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < n / 8; c += gridDim.x * blockDim.x) {
@@ -408,12 +414,14 @@ struct RowList {
 
 // dst row i (of `rows`) = src row L[i]  (gather), or dst row L[i] = src row i
 // (scatter); L = dlist when given (device memory), else the by-value list
+// (drows: the row count in device memory, else rows)
 template <bool SCATTER>
 __global__ __launch_bounds__(256) void move_rows_kernel(const uint16_t *__restrict__ src, int64_t d, int rows,
                                                         RowList list, const int32_t *__restrict__ dlist,
-                                                        uint16_t *__restrict__ dst) {
+                                                        uint16_t *__restrict__ dst,
+                                                        const int32_t *__restrict__ drows = nullptr) {
   const int i = blockIdx.x;
-  if (i >= rows) return;
+  if (i >= (drows ? *drows : rows)) return;
   const int li = dlist ? dlist[i] : list.row[i];
   const uint16_t *s = src + (size_t)(SCATTER ? i : li) * d;
   uint16_t *t = dst + (size_t)(SCATTER ? li : i) * d;
@@ -639,6 +647,239 @@ int amla_moe_experts(const void *hidden, int64_t m, int64_t d, int top_k, const 
     if ((rc = check_launch("moe_experts scatter"))) return rc;
   }
   return AMLA_OK;
+}
+
+}  // extern "C"
+
+namespace amla {
+
+// ---------------------------------------------------------------- routed experts, device schedule
+
+// amla_moe_experts_dev: the (token, k) slots are grouped by expert on the
+// device, so the call needs no host copy of the indices and no stream
+// synchronisation (a HIP graph can hold it).  moe_sort_kernel (one workgroup)
+// makes the schedule; every later launch has a grid for the worst case and
+// its workgroups past the device counts return at once.
+constexpr int MSORT_WAVES = 16;     // 1024 threads
+constexpr int MSORT_MAXE = 512;     // experts per layer
+constexpr int MSORT_EBITS = 9;      // bits of an expert index
+constexpr int MOE_DEV_MAX_SLOTS = 65536;
+constexpr int MOE_TILE_ROWS = 256;  // rows of a GEMM tile entry
+
+struct MoeDevLayout {
+  int sb;                      // largest group on the skinny path
+  int max_small, max_tiles;    // schedule entries (worst case)
+  size_t hdr, gather, scatter, small, tiles, xs, ys, gu, h, part, total;
+};
+
+static MoeDevLayout moe_dev_layout(int64_t m, int64_t d, int top_k, int64_t n, int64_t E) {
+  MoeDevLayout L;
+  const int64_t S = m * top_k;
+  // a token names an expert once in a routing, so a group has at most m rows;
+  // larger groups (repeated indices) and groups over 64 rows take the GEMM
+  L.sb = (int)std::min<int64_t>(std::min<int64_t>(m, 64), S);
+  L.max_small = (int)std::min<int64_t>(E, S);
+  L.max_tiles = (int)((S + MOE_TILE_ROWS - 1) / MOE_TILE_ROWS + std::min<int64_t>(E, S / (L.sb + 1)));
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
+  L.hdr = take(16);
+  L.gather = take((size_t)S * 4);
+  L.scatter = take((size_t)S * 4);
+  L.small = take((size_t)L.max_small * 16);
+  L.tiles = take((size_t)std::max(L.max_tiles, 1) * 16);
+  L.xs = take((size_t)S * d * 2);
+  L.ys = take((size_t)S * d * 2);
+  L.gu = take((size_t)S * 2 * n * 2);
+  L.h = take((size_t)S * n * 2);
+  const GemvPlan a = plan_gemv_grouped(L.sb, (int)(2 * n), (int)d), b = plan_gemv_grouped(L.sb, (int)d, (int)n);
+  const size_t pa = a.kparts > 1 ? (size_t)a.kparts * S * 2 * n * 4 : 0;
+  const size_t pb = b.kparts > 1 ? (size_t)b.kparts * S * d * 4 : 0;
+  L.part = take(std::max<size_t>(std::max(pa, pb), 16));
+  L.total = off;
+  return L;
+}
+
+AMLA_DEV int block_scan_incl(int v, int *wsum, int lane, int wave) {
+  // inclusive prefix sum over the first MSORT_WAVES * 64 threads (all take part)
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  if (lane == 63) wsum[wave] = v;
+  __syncthreads();
+  for (int w = 0; w < wave; ++w) v += wsum[w];
+  __syncthreads();
+  return v;
+}
+
+// Schedule of the routed slots.  Wave w walks slots [w S/16, (w+1) S/16) in
+// order: first counting them per expert (its own row of counts), then, with
+// every expert's start known, placing each slot at its expert's next free
+// position (rank among equal experts of the 64-slot step by ballots), so the
+// order is slot order within each expert whatever the timing.  Outputs:
+//   gather[p] = token of position p, scatter[p] = slot of position p;
+//   small[]   = (expert, first position, rows) of experts with 1..sb slots;
+//   tiles[]   = (expert, first position, rows <= 256) of the larger ones;
+//   hdr       = {routed slots, small entries, tile entries, skipped slots}.
+// Slots with a negative index are left out; an index >= E, or an expert with a
+// null or misaligned weight, is left out and counted as skipped.
+__global__ __launch_bounds__(1024) void moe_sort_kernel(const int64_t *__restrict__ idx, int S, int top_k, int E,
+                                                        int sb, const void *const *__restrict__ wtab,
+                                                        int32_t *__restrict__ hdr, int32_t *__restrict__ gather,
+                                                        int32_t *__restrict__ scatter, int32_t *__restrict__ small,
+                                                        int32_t *__restrict__ tiles) {
+  __shared__ int32_t cur[MSORT_WAVES][MSORT_MAXE];  // per-wave counts, then per-wave next positions
+  __shared__ int32_t eok[MSORT_MAXE];
+  __shared__ int32_t wsum[3][MSORT_WAVES];
+  __shared__ int32_t skipped;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < MSORT_WAVES * MSORT_MAXE; i += 1024) (&cur[0][0])[i] = 0;
+  for (int e = tid; e < E; e += 1024) {
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < 6; ++j) {
+      const uintptr_t a = reinterpret_cast<uintptr_t>(wtab[j * E + e]);
+      ok = ok && a != 0 && (a & ((j & 1) ? 3 : 15)) == 0;
+    }
+    eok[e] = ok;
+  }
+  if (tid == 0) skipped = 0;
+  __syncthreads();
+  const int b0 = (int)((int64_t)S * wave / MSORT_WAVES), b1 = (int)((int64_t)S * (wave + 1) / MSORT_WAVES);
+  auto expert_of = [&](int i) -> int {  // -1: left out, -2: skipped
+    if (i >= b1) return -1;
+    const int64_t v = idx[i];
+    if (v < 0) return -1;
+    if (v >= E || !eok[(int)v]) return -2;
+    return (int)v;
+  };
+  for (int base = b0; base < b1; base += 64) {
+    const int e = expert_of(base + lane);
+    if (e >= 0) atomicAdd(&cur[wave][e], 1);
+    else if (e == -2) atomicAdd(&skipped, 1);
+  }
+  __syncthreads();
+  // per expert: waves' counts -> offsets inside the expert; schedule sizes
+  int tot = 0;
+  if (tid < E) {
+#pragma unroll
+    for (int w = 0; w < MSORT_WAVES; ++w) {
+      const int c = cur[w][tid];
+      cur[w][tid] = tot;
+      tot += c;
+    }
+  }
+  const int is_small = tot >= 1 && tot <= sb;
+  const int ntile = tot > sb ? (tot + MOE_TILE_ROWS - 1) / MOE_TILE_ROWS : 0;
+  const int pos_incl = block_scan_incl(tot, wsum[0], lane, wave);
+  const int small_incl = block_scan_incl(is_small, wsum[1], lane, wave);
+  const int tile_incl = block_scan_incl(ntile, wsum[2], lane, wave);
+  const int first = pos_incl - tot;
+  if (tid < E) {
+#pragma unroll
+    for (int w = 0; w < MSORT_WAVES; ++w) cur[w][tid] += first;
+    if (is_small) {
+      int32_t *en = small + 4 * (small_incl - 1);
+      en[0] = tid; en[1] = first; en[2] = tot; en[3] = 0;
+    }
+    for (int j = 0; j < ntile; ++j) {
+      int32_t *en = tiles + 4 * (tile_incl - ntile + j);
+      en[0] = tid; en[1] = first + j * MOE_TILE_ROWS; en[2] = min(MOE_TILE_ROWS, tot - j * MOE_TILE_ROWS); en[3] = 0;
+    }
+  }
+  if (tid == 1023) {
+    hdr[0] = pos_incl;
+    hdr[1] = small_incl;
+    hdr[2] = tile_incl;
+  }
+  __syncthreads();
+  if (tid == 0) hdr[3] = skipped;
+  // placement, in slot order per wave
+  for (int base = b0; base < b1; base += 64) {
+    const int i = base + lane;
+    const int e = expert_of(i);
+    const bool act = e >= 0;
+    uint64_t peers = __ballot(act);
+#pragma unroll
+    for (int bit = 0; bit < MSORT_EBITS; ++bit) {
+      const bool on = act && ((e >> bit) & 1);
+      const uint64_t bm = __ballot(on);
+      peers &= on ? bm : ~bm;
+    }
+    const uint64_t lower = peers & ((1ull << lane) - 1);
+    if (act) {
+      const int p = cur[wave][e] + __popcll(lower);
+      gather[p] = i / top_k;
+      scatter[p] = i;
+    }
+    // every lane of the wave has read its position: the lowest lane of each
+    // expert advances that expert's next position
+    if (act && lower == 0) cur[wave][e] += __popcll(peers);
+  }
+}
+
+}  // namespace amla
+
+extern "C" {
+
+size_t amla_moe_experts_dev_workspace_bytes(int64_t m, int64_t d, int top_k, int64_t n_inter, int64_t n_experts) {
+  if (m <= 0 || d <= 0 || top_k <= 0 || top_k > 64 || n_inter <= 0 || n_experts <= 0 ||
+      n_experts > MSORT_MAXE || m * top_k > MOE_DEV_MAX_SLOTS)
+    return 0;
+  return moe_dev_layout(m, d, top_k, n_inter, n_experts).total;
+}
+
+int amla_moe_experts_dev(const void *hidden, int64_t m, int64_t d, int top_k, const int64_t *indices,
+                         int64_t n_inter, int64_t n_experts, const void *const *weight_table, void *expert_out,
+                         void *workspace, size_t workspace_bytes, void *stream) {
+  if (!hidden || !indices || !weight_table || !expert_out) return fail(AMLA_EINVAL, "moe_experts_dev: null pointer");
+  if (m < 0 || d <= 0 || top_k <= 0 || n_inter <= 0 || n_experts <= 0)
+    return fail(AMLA_EINVAL, "moe_experts_dev: bad sizes");
+  if (m == 0) return AMLA_OK;
+  if (top_k > 64 || n_experts > MSORT_MAXE || m * top_k > MOE_DEV_MAX_SLOTS)
+    return fail(AMLA_EUNSUPPORTED, "moe_experts_dev: needs top_k <= 64, at most %d experts and %d slots per call",
+                MSORT_MAXE, MOE_DEV_MAX_SLOTS);
+  if (d % 128 || n_inter % 256 || d > INT32_MAX || n_inter > INT32_MAX / 2 || !aligned16(hidden) ||
+      !aligned16(expert_out))
+    return fail(AMLA_EUNSUPPORTED,
+                "moe_experts_dev: needs hidden %% 128 == 0, intermediate %% 256 == 0 and 16-byte aligned rows");
+  const MoeDevLayout L = moe_dev_layout(m, d, top_k, n_inter, n_experts);
+  if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
+    return fail(AMLA_EWORKSPACE, "moe_experts_dev: needs %zu bytes of 16-byte aligned workspace (got %zu)", L.total,
+                workspace ? workspace_bytes : (size_t)0);
+  uint8_t *ws = static_cast<uint8_t *>(workspace);
+  int32_t *hdr = reinterpret_cast<int32_t *>(ws + L.hdr);
+  int32_t *gather = reinterpret_cast<int32_t *>(ws + L.gather), *scatter = reinterpret_cast<int32_t *>(ws + L.scatter);
+  int32_t *small = reinterpret_cast<int32_t *>(ws + L.small), *tiles = reinterpret_cast<int32_t *>(ws + L.tiles);
+  uint16_t *xs = reinterpret_cast<uint16_t *>(ws + L.xs), *ys = reinterpret_cast<uint16_t *>(ws + L.ys);
+  uint16_t *gu = reinterpret_cast<uint16_t *>(ws + L.gu), *hb = reinterpret_cast<uint16_t *>(ws + L.h);
+  float *part = reinterpret_cast<float *>(ws + L.part);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int S = (int)(m * top_k), n = (int)n_inter, D = (int)d, E = (int)n_experts;
+  int rc;
+  moe_sort_kernel<<<1, 1024, 0, st>>>(indices, S, top_k, E, L.sb, weight_table, hdr, gather, scatter, small, tiles);
+  if ((rc = check_launch("moe_experts_dev schedule"))) return rc;
+  RowList none = {};
+  move_rows_kernel<false><<<S, 256, 0, st>>>(static_cast<const uint16_t *>(hidden), d, S, none, gather, xs, hdr);
+  if ((rc = check_launch("moe_experts_dev gather"))) return rc;
+  const MoeSched small_gu = {weight_table, small, hdr + 1, E, 0}, tiles_gu = {weight_table, tiles, hdr + 2, E, 0};
+  const MoeSched small_dn = {weight_table, small, hdr + 1, E, 1}, tiles_dn = {weight_table, tiles, hdr + 2, E, 1};
+  GemvParams pg = {};  // [gate | up] x (rows, D) -> gu (rows, 2n)
+  pg.x = xs; pg.ldx = D; pg.N = 2 * n; pg.K = D; pg.n_split = n; pg.y = gu; pg.ldy = 2 * n; pg.seq_len = 1;
+  pg.part = part;
+  GemvParams pd = {};  // down h (rows, n) -> ys (rows, D)
+  pd.x = hb; pd.ldx = n; pd.N = D; pd.K = n; pd.n_split = D; pd.y = ys; pd.ldy = D; pd.seq_len = 1;
+  pd.part = part;
+  if ((rc = launch_gemm_sched(pg, tiles_gu, L.max_tiles, st))) return rc;
+  if ((rc = launch_gemv_sched(pg, small_gu, L.max_small, L.sb, plan_gemv_grouped(L.sb, 2 * n, D), st))) return rc;
+  silu_mul_rows_kernel<<<dim3((unsigned)std::max(1, std::min(n / 8 / 256, 16)), (unsigned)std::min(S, 65535)), 256,
+                         0, st>>>(gu, S, n, hb, hdr);
+  if ((rc = check_launch("moe_experts_dev silu_mul"))) return rc;
+  if ((rc = launch_gemm_sched(pd, tiles_dn, L.max_tiles, st))) return rc;
+  if ((rc = launch_gemv_sched(pd, small_dn, L.max_small, L.sb, plan_gemv_grouped(L.sb, D, n), st))) return rc;
+  move_rows_kernel<true><<<S, 256, 0, st>>>(ys, d, S, none, scatter, static_cast<uint16_t *>(expert_out), hdr);
+  return check_launch("moe_experts_dev scatter");
 }
 
 }  // extern "C"

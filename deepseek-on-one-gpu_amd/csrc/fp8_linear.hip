@@ -416,6 +416,35 @@ __global__ __launch_bounds__(64) void gemv_finish_grouped(GemvParams p, GemvGrou
   gemv_finish_body<GEMV_PLAIN>(q, (int64_t)(blockIdx.x % gr.units) * 64 + threadIdx.x, kparts);
 }
 
+// Skinny GEMMs of a device schedule (routed experts): entry g = blockIdx.x /
+// units; entries past the device count return at once (uniform per workgroup).
+template <int MT>
+__global__ __launch_bounds__(256) void gemv_sched_kernel(GemvParams p, MoeSched s, int units, int rg, int kparts,
+                                                         int kpb) {
+  const int g = blockIdx.x / units;
+  if (g >= *s.count) return;
+  const int32_t *en = s.ent + 4 * g;
+  const int e = en[0], r0 = en[1];
+  p.M = en[2];
+  p.x += (size_t)r0 * p.ldx;
+  p.y += (size_t)r0 * p.ldy;
+  p.part += (size_t)kparts * r0 * p.N;
+  moe_sched_weights(p, s, e);
+  gemv_body<MT, GEMV_PLAIN>(p, blockIdx.x % units, rg, kparts, kpb);
+}
+
+// gemv_finish for the entries of gemv_sched_kernel: units blocks of 64 per entry.
+__global__ __launch_bounds__(64) void gemv_finish_sched(GemvParams p, MoeSched s, int units, int kparts) {
+  const int g = blockIdx.x / units;
+  if (g >= *s.count) return;
+  const int32_t *en = s.ent + 4 * g;
+  const int r0 = en[1];
+  p.M = en[2];
+  p.y += (size_t)r0 * p.ldy;
+  p.part += (size_t)kparts * r0 * p.N;
+  gemv_finish_body<GEMV_PLAIN>(p, (int64_t)(blockIdx.x % units) * 64 + threadIdx.x, kparts);
+}
+
 // ---------------------------------------------------------------- register-streaming skinny GEMM
 
 // Skinny GEMM for M <= 16 with the weights streamed HBM -> VGPRs (no LDS on
@@ -897,6 +926,40 @@ int launch_gemv_grouped(const GemvParams &p, GemvGroups gr, const GemvPlan &pl, 
     gemv_finish_grouped<<<dim3((unsigned)(fr.n * fr.units)), 64, 0, st>>>(p, fr, pl.kparts);
   }
   return check_launch("grouped fp8 skinny GEMM");
+}
+
+template <int MT>
+static void launch_sched_mt(const GemvParams &p, const MoeSched &s, int max_entries, const GemvPlan &pl,
+                            hipStream_t st) {
+  static bool attr_set = false;  // raise the dynamic LDS limit once per process
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void *)gemv_sched_kernel<MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    attr_set = true;
+  }
+  gemv_sched_kernel<MT><<<dim3((unsigned)(max_entries * pl.groups)), 256, pl.lds, st>>>(p, s, pl.groups, pl.rg,
+                                                                                      pl.kparts, pl.kpb);
+}
+
+int launch_gemv_sched(const GemvParams &p, const MoeSched &s, int max_entries, int max_m, const GemvPlan &pl,
+                      hipStream_t st) {
+  if (max_entries <= 0) return AMLA_OK;
+  if (max_m < 1 || max_m > 64) return fail(AMLA_EINVAL, "scheduled skinny GEMM: max rows %d", max_m);
+  if (p.N % 16 || p.K % 128 || pl.kparts > GEMV_MAX_PARTS || (!s.down && p.n_split % 128))
+    return fail(AMLA_EUNSUPPORTED, "scheduled skinny GEMM: unsupported shape N=%d K=%d", p.N, p.K);
+  if (pl.kparts > 1 && !p.part) return fail(AMLA_EWORKSPACE, "scheduled skinny GEMM: missing partial sums");
+  const int MT = max_m <= 16 ? 1 : (max_m <= 32 ? 2 : 4);
+  if (gemv_lds_bytes(max_m, MT, pl.kpb, pl.rg) > pl.lds)
+    return fail(AMLA_EINVAL, "scheduled skinny GEMM: plan for a smaller M");
+  if ((int64_t)max_entries * pl.groups > INT32_MAX) return fail(AMLA_EUNSUPPORTED, "scheduled skinny GEMM: grid");
+  if (MT == 1) launch_sched_mt<1>(p, s, max_entries, pl, st);
+  else if (MT == 2) launch_sched_mt<2>(p, s, max_entries, pl, st);
+  else launch_sched_mt<4>(p, s, max_entries, pl, st);
+  if (pl.kparts > 1) {
+    const int units = (int)(((int64_t)max_m * (p.N / 4) + 63) / 64);
+    gemv_finish_sched<<<dim3((unsigned)(max_entries * units)), 64, 0, st>>>(p, s, units, pl.kparts);
+  }
+  return check_launch("scheduled fp8 skinny GEMM");
 }
 
 // ---------------------------------------------------------------- rms_norm

@@ -136,14 +136,14 @@ constexpr int G_DMA = G_STAGE / 1024 / G_NW;     // copies per wave per stage
 constexpr int G_EPITCH = 128 * 2 + 8;           // LDS row pitch of the staged output block
 static_assert(G_NW * 64 * G_EPITCH <= G_LDS, "staged output block exceeds LDS");
 
+// One 256 x 256 output tile at (n0, m0).
 template <int MODE>
-__global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p, bool staged_out) {
+AMLA_DEV void gemm_body(const GemvParams &p, bool staged_out, const int n0, const int m0) {
   extern __shared__ __align__(16) uint8_t gsm[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave & 1, wm = wave >> 1;
   const int j32 = lane & 31, hh = lane >> 5;
-  const int n0 = blockIdx.x * G_BN, m0 = blockIdx.y * G_BM;
   const bool seg1 = (MODE == GEMV_QKVA || p.w1) && n0 >= p.n_split;
   const uint8_t *W = seg1 ? p.w1 : p.w0;
   const float *S = seg1 ? p.s1 : p.s0;
@@ -315,6 +315,26 @@ __global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p, bool s
   }
 }
 
+template <int MODE>
+__global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p, bool staged_out) {
+  gemm_body<MODE>(p, staged_out, blockIdx.x * G_BN, blockIdx.y * G_BM);
+}
+
+// Tiles of the routed experts from a device schedule: workgroup (x, y) takes
+// output columns 256 x of entry y (expert e, rows r0 .. r0 + rows - 1 of x and
+// y, rows <= 256); entries past the count return at once.
+__global__ __launch_bounds__(G_NW * 64, 1) void gemm_sched_kernel(GemvParams p, MoeSched s) {
+  const int t = blockIdx.y;
+  if (t >= *s.count) return;
+  const int32_t *en = s.ent + 4 * t;
+  const int e = en[0], r0 = en[1];
+  p.M = en[2];
+  p.x += (size_t)r0 * p.ldx;
+  p.y += (size_t)r0 * p.ldy;
+  moe_sched_weights(p, s, e);
+  gemm_body<GEMV_PLAIN>(p, true, blockIdx.x * G_BN, 0);
+}
+
 size_t gemm_ws_bytes(int, int, int) { return 0; }
 
 int launch_gemm(const GemvParams &p, int mode, hipStream_t st) {
@@ -349,6 +369,22 @@ int launch_gemm(const GemvParams &p, int mode, hipStream_t st) {
     default: gemm_kernel<GEMV_QROPE><<<grid, G_NW * 64, G_LDS, st>>>(p, staged); break;
   }
   return check_launch("fp8 GEMM");
+}
+
+int launch_gemm_sched(const GemvParams &p, const MoeSched &s, int max_entries, hipStream_t st) {
+  if (max_entries <= 0) return AMLA_OK;
+  if (p.K % 128 || p.N % 8 || p.ldx % 8 || p.ldy % 8 || !aligned16(p.x) || !aligned16(p.y))
+    return fail(AMLA_EUNSUPPORTED, "scheduled fp8 GEMM needs K %% 128 == 0, N %% 8 == 0 and 16-byte aligned rows");
+  if (!s.down && p.n_split % G_BN)
+    return fail(AMLA_EUNSUPPORTED, "scheduled fp8 GEMM: the first weight segment must be a multiple of 256 rows");
+  if (max_entries > 65535) return fail(AMLA_EUNSUPPORTED, "scheduled fp8 GEMM: %d entries", max_entries);
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void *)gemm_sched_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS);
+    attr_set = true;
+  }
+  gemm_sched_kernel<<<dim3((p.N + G_BN - 1) / G_BN, max_entries), G_NW * 64, G_LDS, st>>>(p, s);
+  return check_launch("scheduled fp8 GEMM");
 }
 
 // ---------------------------------------------------------------- K10 causal flash attention

@@ -214,6 +214,31 @@ int amla_moe_experts(const void *hidden, int64_t m, int64_t d, int top_k, const 
                      void *stream);
 size_t amla_moe_experts_workspace_bytes(int64_t m, int64_t d, int top_k, int64_t n_inter);
 
+/* amla_moe_experts with the indices left on the device: the same computation
+ * (forward.py:139-151, each chosen expert once over all of its tokens), with
+ * the (token, k) slots grouped by expert on the device, so the call copies
+ * nothing from the host, never waits for the stream and can be captured in a
+ * HIP graph.  The reference brings the indices to the host (gpu_transfer.py:60,
+ * `.tolist()`) before its expert loop; this entry point has no counterpart
+ * there.  It is for callers that hold every expert of the layer on the device.
+ *   indices (m, top_k) int64 in DEVICE memory; an index < 0 skips its slot
+ *     (expert_out row left as it was);
+ *   weight_table: DEVICE array of 6 * n_experts pointers, [gate_w | gate_s |
+ *     up_w | up_s | down_w | down_s] x n_experts (weights 16-byte aligned,
+ *     scales 4-byte aligned), laid out per expert as for amla_swiglu;
+ *   m * top_k <= 65536, n_experts <= 512, top_k <= 64, d % 128 == 0,
+ *   n_inter % 256 == 0.
+ * A slot whose index is >= n_experts, or whose expert has a NULL or misaligned
+ * pointer in the table, is skipped like a negative one and counted: after the
+ * call the first 16 bytes of the workspace hold int32 {routed slots, skinny
+ * groups, GEMM tiles, skipped slots}.  Workspace of
+ * amla_moe_experts_dev_workspace_bytes(m, d, top_k, n_inter, n_experts) bytes
+ * (0 for unsupported sizes); calls that share a workspace must not overlap. */
+int amla_moe_experts_dev(const void *hidden, int64_t m, int64_t d, int top_k, const int64_t *indices,
+                         int64_t n_inter, int64_t n_experts, const void *const *weight_table, void *expert_out,
+                         void *workspace, size_t workspace_bytes, void *stream);
+size_t amla_moe_experts_dev_workspace_bytes(int64_t m, int64_t d, int top_k, int64_t n_inter, int64_t n_experts);
+
 /* The combine of moe_block, inference/forward.py:138-153, for m tokens:
  *   acc = 0;  for k in 0..top_k-1:  acc = bf16( acc + bf16( bf16(w[t, k]) * expert_out[t, k] ) )
  *   out[t] = bf16( shared_out[t] + bf16( acc * routed_scaling_factor ) )

@@ -153,3 +153,24 @@ def test_moe_experts_checks_indices_and_tables_on_the_host():
                               *[ctypes.cast(t, ctypes.c_void_p) for t in tables], p, p, 1 << 30, None) == -3
     need = L.amla_moe_experts_workspace_bytes(m, d, top_k, n)
     assert need >= 2 * m * top_k * d * 2
+
+
+def test_moe_experts_dev_checks_sizes_on_the_host():
+    """The device-grouped entry point rejects what its schedule cannot hold before any launch
+    (it reads neither the indices nor the weight table on the host)."""
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(256)
+    p0 = ctypes.cast(buf, ctypes.c_void_p).value
+    p = p0 + 16 - p0 % 16 if p0 % 16 else p0
+    m, d, top_k, n, E = 8, 256, 8, 256, 256
+    need = L.amla_moe_experts_dev_workspace_bytes(m, d, top_k, n, E)
+    assert need >= 2 * m * top_k * d * 2 + 3 * m * top_k * n * 2
+    assert L.amla_moe_experts_dev_workspace_bytes(m, d, top_k, n, 513) == 0      # more than 512 experts
+    assert L.amla_moe_experts_dev_workspace_bytes(8193, d, 8, n, E) == 0          # 65544 slots
+    assert L.amla_moe_experts_dev(None, m, d, top_k, p, n, E, p, p, p, need, None) == -1
+    assert L.amla_moe_experts_dev(p, m, d, top_k, p, n, 513, p, p, p, need, None) == -3
+    assert L.amla_moe_experts_dev(p, 8193, d, 8, p, n, E, p, p, p, need, None) == -3
+    assert L.amla_moe_experts_dev(p, m, 200, top_k, p, n, E, p, p, p, need, None) == -3
+    assert L.amla_moe_experts_dev(p, m, d, top_k, p, n, E, p, p, p, 64, None) == -2
+    assert b"workspace" in L.amla_last_error()
+    assert L.amla_moe_experts_dev(p, 0, d, top_k, p, n, E, p, p, p, 0, None) == 0  # nothing to do
