@@ -130,9 +130,23 @@ size_t gemv_rs_lds_bytes(int M, int kpb, int rg);
 // (needs plan.kparts == 1).
 int launch_gemv_rs(const GemvParams &p, int mode, const GemvPlan &plan, const uint16_t *xgamma, float eps,
                    hipStream_t stream, bool finish = true);
-// Large-M fp8 GEMM with the same modes (M > 64).
+// Large-M fp8 GEMM with the same modes (M > 64).  With split_ws of at least
+// gemm_ws_bytes(M, N, K) bytes, tiles past the last full round of 256
+// workgroups are cut into K parts (fp32 partial sums in split_ws, summed in
+// part order by a finishing kernel); without it every tile takes the whole K.
+constexpr int GEMM_MAX_PARTS = 8;
+struct GemmSplit {
+  int full;        // tiles with the whole K
+  int parts;       // K parts of each later tile
+  int n_tiles;     // 256-column tiles
+  int items;       // workgroups
+  float *partial;  // [split tile][part][256 x 256] fp32 in the workgroup's lane order
+  size_t bytes;    // of partial
+};
+GemmSplit plan_gemm_split(int M, int N, int K);
 size_t gemm_ws_bytes(int M, int N, int K);
-int launch_gemm(const GemvParams &p, int mode, hipStream_t stream);
+int launch_gemm(const GemvParams &p, int mode, hipStream_t stream, float *split_ws = nullptr,
+                size_t split_ws_bytes = 0);
 
 int launch_rms_norm(const uint16_t *x, int64_t rows, int64_t dim, int64_t ldx, const uint16_t *gamma,
                     float eps, uint16_t *y, int64_t ldy, hipStream_t stream);

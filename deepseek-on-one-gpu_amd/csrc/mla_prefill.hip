@@ -134,11 +134,17 @@ constexpr int G_STAGE = G_BN * G_BK + G_BM * G_BK * 2;
 constexpr int G_LDS = G_NST * G_STAGE;           // 144 KB
 constexpr int G_DMA = G_STAGE / 1024 / G_NW;     // copies per wave per stage
 constexpr int G_EPITCH = 128 * 2 + 8;           // LDS row pitch of the staged output block
+constexpr int G_WAVE_F4 = 4 * 2 * 4 * 64;        // f32x4 partial sums of one wave's 128 x 64 block
+constexpr int G_TILE_F4 = G_NW * G_WAVE_F4;      // ... of one 256 x 256 tile (256 KB)
 static_assert(G_NW * 64 * G_EPITCH <= G_LDS, "staged output block exceeds LDS");
 
-// One 256 x 256 output tile at (n0, m0).
+// One 256 x 256 output tile at (n0, m0) over the 128-wide K blocks
+// [kb_begin, kb_end).  partial != nullptr: the tile's fp32 sums (scaled) go to
+// partial in the lanes' own order (gemm_finish_kernel sums the K parts),
+// else through the epilogue.
 template <int MODE>
-AMLA_DEV void gemm_body(const GemvParams &p, bool staged_out, const int n0, const int m0) {
+AMLA_DEV void gemm_body(const GemvParams &p, bool staged_out, const int n0, const int m0, const int kb_begin,
+                        const int kb_end, float *partial) {
   extern __shared__ __align__(16) uint8_t gsm[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -210,11 +216,11 @@ AMLA_DEV void gemm_body(const GemvParams &p, bool staged_out, const int n0, cons
   float s_run = 0.f;
   bool skip = false;
 
-  const int iters = p.K / G_BK;
-  dma(0, gsm);
-  if (iters > 1) dma(1, gsm + G_STAGE);
+  const int iters = 2 * kb_end;  // 64-wide K stages, two per scale block
+  dma(2 * kb_begin, gsm);
+  if (2 * kb_begin + 1 < iters) dma(2 * kb_begin + 1, gsm + G_STAGE);
   int stg = 0;
-  for (int it = 0; it < iters; ++it) {
+  for (int it = 2 * kb_begin; it < iters; ++it) {
     if (it + 1 < iters) wait_vmcnt<G_DMA>();
     else wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
@@ -266,6 +272,19 @@ AMLA_DEV void gemm_body(const GemvParams &p, bool staged_out, const int n0, cons
   }
 
   // C[n][m]: lane holds m = 32 j + j32 of its rows, n = 32 g + 8 q + 4 hh .. +3.
+  if (partial) {
+    // [wave][g][j][q][lane] f32x4: every store is 1 KB contiguous per wave
+    f32x4 *dst = reinterpret_cast<f32x4 *>(partial) + (size_t)wave * G_WAVE_F4;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          dst[((g * 2 + j) * 4 + q) * 64 + lane] =
+              f32x4{acc[g][j][4 * q], acc[g][j][4 * q + 1], acc[g][j][4 * q + 2], acc[g][j][4 * q + 3]} * s_run;
+    return;
+  }
   if (!staged_out) {
     // outputs without 16-byte aligned rows: 8-byte stores straight from the accumulators
     if (wave_rows) {
@@ -315,9 +334,66 @@ AMLA_DEV void gemm_body(const GemvParams &p, bool staged_out, const int n0, cons
   }
 }
 
+// Workgroup i: tile i (t = m_tile * n_tiles + n_tile) with the whole K while
+// i < sp.full, else K part (i - full) % parts of tile full + (i - full) / parts.
 template <int MODE>
-__global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p, bool staged_out) {
-  gemm_body<MODE>(p, staged_out, blockIdx.x * G_BN, blockIdx.y * G_BM);
+__global__ __launch_bounds__(G_NW * 64, 1) void gemm_kernel(GemvParams p, bool staged_out, GemmSplit sp) {
+  const int i = blockIdx.x, KB = p.K >> 7;
+  int t = i, kb0 = 0, kb1 = KB;
+  float *partial = nullptr;
+  if (i >= sp.full) {
+    const int st = (i - sp.full) / sp.parts, q = (i - sp.full) % sp.parts;
+    t = sp.full + st;
+    kb0 = q * KB / sp.parts;
+    kb1 = (q + 1) * KB / sp.parts;
+    partial = sp.partial + (size_t)(st * sp.parts + q) * G_TILE_F4 * 4;
+  }
+  gemm_body<MODE>(p, staged_out, (t % sp.n_tiles) * G_BN, (t / sp.n_tiles) * G_BM, kb0, kb1, partial);
+}
+
+// Sums the K parts of the split tiles in part order and applies the epilogue.
+// Workgroup = one wave block (64 rows x 128 columns) of one split tile: the
+// parts are read in the lane order they were written (coalesced), summed in
+// part order, staged in LDS as rows, and stored 8 outputs per thread through
+// the same epilogue as the staged tiles (16-byte row stores).
+template <int MODE>
+__global__ __launch_bounds__(256) void gemm_finish_kernel(GemvParams p, GemmSplit sp) {
+  __shared__ float rows[64][128 + 4];
+  const int tid = threadIdx.x;
+  const int st = blockIdx.x / G_NW, wave = blockIdx.x % G_NW;
+  const f32x4 *src = reinterpret_cast<const f32x4 *>(sp.partial) + (size_t)st * sp.parts * G_TILE_F4 +
+                     (size_t)wave * G_WAVE_F4;
+  constexpr int PER = G_WAVE_F4 / 256;  // f32x4 per thread
+  f32x4 sum[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) sum[k] = src[k * 256 + tid];
+  for (int q = 1; q < sp.parts; ++q) {
+    f32x4 v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) v[k] = src[(size_t)q * G_TILE_F4 + k * 256 + tid];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) sum[k] += v[k];
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int rr = k * 256 + tid;  // ((g * 2 + j) * 4 + q) * 64 + lane
+    const int gjq = rr >> 6, lane = rr & 63;
+    const int g = gjq >> 3, j = (gjq >> 2) & 1, q = gjq & 3;
+    *reinterpret_cast<f32x4 *>(&rows[32 * j + (lane & 31)][32 * g + 8 * q + 4 * (lane >> 5)]) = sum[k];
+  }
+  __syncthreads();
+  const int t = sp.full + st;
+  const int m0 = (t / sp.n_tiles) * G_BM + (wave >> 1) * 64, n0 = (t % sp.n_tiles) * G_BN + (wave & 1) * 128;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int e = k * 256 + tid, r = e >> 4, c = (e & 15) * 8;
+    const int m = m0 + r, n = n0 + c;
+    if (m < p.M && n < p.N) {
+      const float *v = &rows[r][c];
+      pstore8<MODE>(p, m, n, u32x4{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]),
+                                   pack_bf16(v[6], v[7])});
+    }
+  }
 }
 
 // Tiles of the routed experts from a device schedule: workgroup (x, y) takes
@@ -332,12 +408,40 @@ __global__ __launch_bounds__(G_NW * 64, 1) void gemm_sched_kernel(GemvParams p, 
   p.x += (size_t)r0 * p.ldx;
   p.y += (size_t)r0 * p.ldy;
   moe_sched_weights(p, s, e);
-  gemm_body<GEMV_PLAIN>(p, true, blockIdx.x * G_BN, 0);
+  gemm_body<GEMV_PLAIN>(p, true, blockIdx.x * G_BN, 0, 0, p.K >> 7, nullptr);
 }
 
-size_t gemm_ws_bytes(int, int, int) { return 0; }
+// Tiles past the last full round of 256 workgroups are cut into K parts so
+// that the launch ends with the machine full: time ~ (rounds of 256 work
+// items) x (tile time / parts) + the partial sums written and read back (256
+// KB per part); a tile's time is taken as proportional to K (~500 us at
+// K = 16384 on MI355X), the partial traffic at ~5 TB/s.
+GemmSplit plan_gemm_split(int M, int N, int K) {
+  GemmSplit sp = {};
+  sp.n_tiles = (N + G_BN - 1) / G_BN;
+  const int tiles = sp.n_tiles * ((M + G_BM - 1) / G_BM);
+  const int KB = K / 128;
+  const int full = tiles / 256 * 256, rest = tiles - full;
+  const double t_tile = 500.0 * K / 16384.0;  // us
+  int best = 1;
+  double best_cost = rest ? t_tile : 0.0;
+  for (int s = 2; s <= std::min(GEMM_MAX_PARTS, KB) && rest; ++s) {
+    const double cost = (double)((rest * s + 255) / 256) * t_tile / s + rest * s * (0.25 * 2 / 5e6 * 1e6);
+    if (cost < best_cost * 0.95) {
+      best_cost = cost;
+      best = s;
+    }
+  }
+  sp.full = best > 1 ? full : tiles;
+  sp.parts = best;
+  sp.items = sp.full + (tiles - sp.full) * best;
+  sp.bytes = best > 1 ? (size_t)(tiles - sp.full) * best * G_TILE_F4 * 16 : 0;
+  return sp;
+}
 
-int launch_gemm(const GemvParams &p, int mode, hipStream_t st) {
+size_t gemm_ws_bytes(int M, int N, int K) { return plan_gemm_split(M, N, K).bytes; }
+
+int launch_gemm(const GemvParams &p, int mode, hipStream_t st, float *split_ws, size_t split_ws_bytes) {
   if (p.K % 128 || p.N % 4) return fail(AMLA_EUNSUPPORTED, "fp8 GEMM needs K %% 128 == 0 and N %% 4 == 0");
   if (p.ldx % 8) return fail(AMLA_EUNSUPPORTED, "fp8 GEMM needs 16-byte aligned activation rows");
   if ((mode == GEMV_QKVA && p.max_rows <= 0) || (mode == GEMV_QROPE && p.rope_rows <= 0))
@@ -361,14 +465,30 @@ int launch_gemm(const GemvParams &p, int mode, hipStream_t st) {
     staged = staged && aligned16(p.ckv) && aligned16(p.kpe) && p.kv_lora % 8 == 0 && p.rope % 8 == 0 &&
              p.ckv_bstride % 8 == 0 && p.kpe_bstride % 8 == 0;
   if (mode == GEMV_QROPE) staged = staged && p.head_dim % 8 == 0 && p.nope % 8 == 0;
-  dim3 grid((p.N + G_BN - 1) / G_BN, (p.M + G_BM - 1) / G_BM);
-  switch (mode) {
-    case GEMV_PLAIN: gemm_kernel<GEMV_PLAIN><<<grid, G_NW * 64, G_LDS, st>>>(p, staged); break;
-    case GEMV_RESID: gemm_kernel<GEMV_RESID><<<grid, G_NW * 64, G_LDS, st>>>(p, staged); break;
-    case GEMV_QKVA: gemm_kernel<GEMV_QKVA><<<grid, G_NW * 64, G_LDS, st>>>(p, staged); break;
-    default: gemm_kernel<GEMV_QROPE><<<grid, G_NW * 64, G_LDS, st>>>(p, staged); break;
+  GemmSplit sp = plan_gemm_split(p.M, p.N, p.K);
+  if (sp.parts > 1 && (!staged || !split_ws || split_ws_bytes < sp.bytes || !aligned16(split_ws))) {
+    // no room for the partial sums (or outputs without 16-byte stores): whole tiles
+    sp.full = sp.items = sp.n_tiles * ((p.M + G_BM - 1) / G_BM);
+    sp.parts = 1;
   }
-  return check_launch("fp8 GEMM");
+  sp.partial = split_ws;
+  const dim3 grid(sp.items);
+  switch (mode) {
+    case GEMV_PLAIN: gemm_kernel<GEMV_PLAIN><<<grid, G_NW * 64, G_LDS, st>>>(p, staged, sp); break;
+    case GEMV_RESID: gemm_kernel<GEMV_RESID><<<grid, G_NW * 64, G_LDS, st>>>(p, staged, sp); break;
+    case GEMV_QKVA: gemm_kernel<GEMV_QKVA><<<grid, G_NW * 64, G_LDS, st>>>(p, staged, sp); break;
+    default: gemm_kernel<GEMV_QROPE><<<grid, G_NW * 64, G_LDS, st>>>(p, staged, sp); break;
+  }
+  int rc = check_launch("fp8 GEMM");
+  if (rc || sp.parts == 1) return rc;
+  const dim3 fgrid((unsigned)((sp.items - sp.full) / sp.parts * G_NW));
+  switch (mode) {
+    case GEMV_PLAIN: gemm_finish_kernel<GEMV_PLAIN><<<fgrid, 256, 0, st>>>(p, sp); break;
+    case GEMV_RESID: gemm_finish_kernel<GEMV_RESID><<<fgrid, 256, 0, st>>>(p, sp); break;
+    case GEMV_QKVA: gemm_finish_kernel<GEMV_QKVA><<<fgrid, 256, 0, st>>>(p, sp); break;
+    default: gemm_finish_kernel<GEMV_QROPE><<<fgrid, 256, 0, st>>>(p, sp); break;
+  }
+  return check_launch("fp8 GEMM K-part finish");
 }
 
 int launch_gemm_sched(const GemvParams &p, const MoeSched &s, int max_entries, hipStream_t st) {
@@ -828,14 +948,15 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
 
 // ---------------------------------------------------------------- orchestration
 
-// p.part must hold the K-part sums of the skinny plan (PrefillLayout::lin)
-static int run_linear(const GemvParams &p, int mode, hipStream_t st) {
+// p.part (lin_bytes) holds the K-part sums of the skinny plan or the split
+// GEMM's partial sums (PrefillLayout::lin)
+static int run_linear(const GemvParams &p, int mode, hipStream_t st, size_t lin_bytes) {
   if (p.M <= 64) return launch_gemv(p, mode, plan_gemv(p.M, p.N, p.K), st);
-  return launch_gemm(p, mode, st);
+  return launch_gemm(p, mode, st, p.part, lin_bytes);
 }
 
 struct PrefillLayout {
-  size_t xn, qa, qan, q, kvn, kpe, kvb, attn, lin, total;
+  size_t xn, qa, qan, q, kvn, kpe, kvb, attn, lin, lin_bytes, total;
   int Tmax;
 };
 
@@ -854,17 +975,19 @@ static PrefillLayout prefill_layout(const amla_mla_args &a) {
   L.kpe = take((size_t)L.Tmax * a.qk_rope * 2);
   L.kvb = take((size_t)L.Tmax * a.heads * (a.qk_nope + a.v_dim) * 2);
   L.attn = take(M * a.heads * a.v_dim * 2);
-  // K-part sums of the skinny linears (M <= 64)
+  // K-part sums of the skinny linears (M <= 64), or the K-split partial sums
+  // of the large-M GEMMs
   size_t lin = 0;
   const int HDv = a.qk_nope + a.v_dim;
   auto need = [&](int m, int n, int k) {
-    if (m <= 64) lin = std::max(lin, plan_gemv(m, n, k).part_bytes);
+    lin = std::max(lin, m <= 64 ? plan_gemv(m, n, k).part_bytes : gemm_ws_bytes(m, n, k));
   };
   need((int)M, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
   need((int)M, a.heads * HD, a.q_lora);
   need(L.Tmax, a.heads * HDv, a.kv_lora);
   need((int)M, a.hidden, a.heads * a.v_dim);
   L.lin = take(lin);
+  L.lin_bytes = lin;
   L.total = off;
   return L;
 }
@@ -925,7 +1048,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   pa.kpe = reinterpret_cast<uint16_t *>(a->kpe_cache);
   pa.ckv_bstride = (int64_t)a->max_seq * a->kv_lora; pa.kpe_bstride = (int64_t)a->max_seq * a->qk_rope;
   pa.kv_lora = a->kv_lora; pa.rope = a->qk_rope; pa.pos = a->positions; pa.seq_len = S; pa.max_rows = a->max_seq;
-  if ((rc = run_linear(pa, GEMV_QKVA, st))) return rc;
+  if ((rc = run_linear(pa, GEMV_QKVA, st, L.lin_bytes))) return rc;
 
   if ((rc = launch_rms_norm(qa, M, a->q_lora, a->q_lora, reinterpret_cast<const uint16_t *>(a->gamma_q), a->eps,
                             qan, a->q_lora, st)))
@@ -940,7 +1063,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   pb.pos = a->positions; pb.seq_len = S; pb.rope = a->qk_rope; pb.rope_table = a->rope_table;
   pb.rope_rows = a->rope_rows;
   pb.head_dim = HD; pb.nope = a->qk_nope;
-  if ((rc = run_linear(pb, GEMV_QROPE, st))) return rc;
+  if ((rc = run_linear(pb, GEMV_QROPE, st, L.lin_bytes))) return rc;
 
   const int T = L.Tmax;
   FlashParams fp = {};
@@ -961,7 +1084,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
     pk.w0 = reinterpret_cast<const uint8_t *>(a->w_kv_b); pk.s0 = a->s_kv_b;
     pk.N = a->heads * (a->qk_nope + a->v_dim); pk.K = a->kv_lora; pk.n_split = pk.N;
     pk.y = kvb; pk.ldy = pk.N; pk.seq_len = 1;
-    if ((rc = run_linear(pk, GEMV_PLAIN, st))) return rc;
+    if ((rc = run_linear(pk, GEMV_PLAIN, st, L.lin_bytes))) return rc;
     fp.b = b;
     static bool flash_attr = false;  // dynamic LDS above 64 KB
     if (!flash_attr) {
@@ -980,7 +1103,7 @@ int prefill_impl(const amla_mla_args *a, hipStream_t st) {
   po.N = a->hidden; po.K = a->heads * a->v_dim; po.n_split = po.N;
   po.y = reinterpret_cast<uint16_t *>(a->out); po.ldy = a->hidden;
   po.res = reinterpret_cast<const uint16_t *>(a->residual); po.ldr = a->hidden; po.seq_len = 1;
-  return run_linear(po, a->residual ? GEMV_RESID : GEMV_PLAIN, st);
+  return run_linear(po, a->residual ? GEMV_RESID : GEMV_PLAIN, st, L.lin_bytes);
 }
 
 }  // namespace amla
