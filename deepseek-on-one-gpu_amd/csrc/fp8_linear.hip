@@ -144,7 +144,7 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
 // 128-wide blocks; a workgroup (4 waves) owns one unit.
 //   * x[:, part] is staged in LDS once per workgroup (bf16, 16 B padded rows);
 //   * weight tiles stream HBM -> LDS with LDS-DMA (global_load_lds, no
-//     registers), NBUF-1 tiles ahead; one copy moves 512 contiguous bytes of
+//     registers), nbuf - 1 tiles ahead; one copy moves 512 contiguous bytes of
 //     two rows, so every row is read in long runs;
 //   * the 4 waves split the part's blocks of a tile (block b -> wave b % 4),
 //     read the MFMA fragments from LDS, convert fp8 -> bf16 in registers and
@@ -164,12 +164,15 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
 constexpr int GEMV_MAX_PARTS = 32;  // K parts summed by gemv_finish
 constexpr int GEMV_MAX_RG = 16;     // 16-row tiles per workgroup
 constexpr int GEMV_KPB = 16;        // max 128-wide blocks per K part (2 KB of a row)
-// Weight tiles resident (current + NBUF-1 in flight).  With M <= 16 (MT 1)
-// the x fragments live in registers instead of LDS, which leaves room for one
-// more tile in flight.
-__host__ __device__ constexpr int gemv_nbuf(int MT) { return MT == 1 ? 4 : 3; }
+// Weight tiles resident: nbuf (current + nbuf - 1 in flight).  Measured on
+// MI355X (decode shapes at M = 8, the FFN and MoE blocks): keeping about
+// 32 KB of copies in flight per workgroup is fastest, deeper rings are
+// slower (o_proj 32 KB tiles: ring 3 31.1 us, 4 32.2; q_b 24 KB tiles: ring 2
+// 14.2, 3 15.0, 4 15.5; q_a | kv_a 16 KB tiles: 15.6 / 16.6 / 16.9; the MoE
+// block 16 % faster with 2 or 3 than with 4).
+__host__ __device__ inline int gemv_nbuf(int tile_bytes) { return tile_bytes >= 32 * 1024 ? 3 : 2; }
 
-// LDS: [NBUF][16 rows][ceil4(kpb) * 128] weights | [M][kpb * 256 + 16] x (MT > 1) |
+// LDS: [nbuf][16 rows][ceil4(kpb) * 128] weights | [M][kpb * 256 + 16] x (MT > 1) |
 //      [2][4 waves][MT][64] f32x4 partial tiles | [rg][MT][64] f32x4 results
 __host__ __device__ inline int gemv_kpb4(int kpb) { return (kpb + 3) & ~3; }
 __host__ __device__ inline int gemv_xrow(int kpb) { return kpb * 256 + 16; }
@@ -177,7 +180,6 @@ __host__ __device__ inline int gemv_xrow(int kpb) { return kpb * 256 + 16; }
 template <int MT, int MODE>
 AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int kpb) {
   constexpr bool XREG = MT == 1;
-  constexpr int NBUF = gemv_nbuf(MT);
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
@@ -191,10 +193,11 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
   const int nseg = (nbp + 3) >> 2;          // 512 B segments per row
   const int XROW = gemv_xrow(kpb);
   const int TILE_BYTES = 16 * gemv_kpb4(kpb) * 128;
+  const int nbuf = gemv_nbuf(TILE_BYTES);
 
   extern __shared__ __align__(16) uint8_t gsm[];
   uint8_t *const wbuf = gsm;
-  uint8_t *const xs = gsm + NBUF * TILE_BYTES;
+  uint8_t *const xs = gsm + nbuf * TILE_BYTES;
   f32x4 *const red = reinterpret_cast<f32x4 *>(xs + (XREG ? 0 : p.M * XROW));
   f32x4 *const done = red + 2 * 4 * MT * 64;
 
@@ -228,7 +231,7 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
   // the first weight tiles are in flight while x is read
   if (tile_begin < tile_end) {
 #pragma unroll
-    for (int b = 0; b < NBUF - 1; ++b) dma_tile(tile_begin + b, b);
+    for (int b = 0; b < nbuf - 1; ++b) dma_tile(tile_begin + b, b);
   }
 
   // MT 1: this wave's x fragments (blocks wave + 4j of the part, row li; rows
@@ -254,8 +257,7 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
     }
   }
 
-  for (int tile = tile_begin, it = 0; tile < tile_end; ++tile, ++it) {
-    const int buf = it % NBUF;
+  for (int tile = tile_begin, it = 0, buf = 0; tile < tile_end; ++tile, ++it, buf = buf == nbuf - 1 ? 0 : buf + 1) {
     const int nt = tile * 16;
     // block scales of this wave's blocks through the scalar cache (constant
     // address space: the scales are never written here), so waiting for them
@@ -267,21 +269,18 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
     float scw[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) scw[j] = srow[min(wave + 4 * j, nbp - 1)];
-    // this tile's copies landed (the later tiles' may stay in flight: 2*nseg
-    // copies per wave per tile), then every wave's part of it is visible
-    if constexpr (NBUF == 4) {
-      if (nseg == 4) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-      else if (nseg == 3) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-      else if (nseg == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    } else {
+    // this tile's copies landed (the next nbuf - 2 tiles' may stay in flight:
+    // 2 * nseg copies per wave per tile), then every wave's part of it is visible
+    if (nbuf == 3) {
       if (nseg == 4) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
       else if (nseg == 3) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
       else if (nseg == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
       else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     lds_barrier();
-    dma_tile(tile + NBUF - 1, (it + NBUF - 1) % NBUF);  // into the buffer read last trip
+    dma_tile(tile + nbuf - 1, buf == 0 ? nbuf - 1 : buf - 1);  // into the buffer read last trip
 
     const uint8_t *tb = wbuf + buf * TILE_BYTES;
     f32x4 acc[MT];
@@ -378,8 +377,9 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(GemvParams p, GemvGro
 }
 
 size_t gemv_lds_bytes(int M, int MT, int kpb, int rg) {
-  return (size_t)gemv_nbuf(MT) * 16 * gemv_kpb4(kpb) * 128 + (MT == 1 ? 0 : (size_t)M * gemv_xrow(kpb)) +
-         2 * 4 * MT * 64 * 16 + (size_t)rg * MT * 64 * 16;
+  const int tile = 16 * gemv_kpb4(kpb) * 128;
+  return (size_t)gemv_nbuf(tile) * tile + (MT == 1 ? 0 : (size_t)M * gemv_xrow(kpb)) + 2 * 4 * MT * 64 * 16 +
+         (size_t)rg * MT * 64 * 16;
 }
 
 // Sums the K parts of gemv_kernel in part order and applies the epilogue.
