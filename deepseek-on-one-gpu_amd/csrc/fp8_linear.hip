@@ -804,15 +804,18 @@ GemvPlan plan_gemv(int M, int N, int K) {
   }
   pl.kpb = kpb;
   pl.kparts = (KB + kpb - 1) / kpb;
-  // tiles per unit: fewest rounds of 256 workgroups x (tiles per unit + one
-  // tile's worth of per-workgroup start-up), then the largest unit (fewer x
-  // stagings), within the LDS budget
+  // tiles per unit: fewest rounds of the workgroups the machine holds (256,
+  // or 512 when two fit one CU's LDS: measured faster for q_a | kv_a and q_b,
+  // whose units then run two per CU) x (tiles per unit + one tile's worth of
+  // per-workgroup start-up), then the largest unit (fewer x stagings), within
+  // the LDS budget
   int best_rg = 1;
   int64_t best_cost = INT64_MAX;
   for (int rg = 1; rg <= GEMV_MAX_RG; ++rg) {
     if (gemv_lds_bytes(M, MT, kpb, rg) > LDS_MAX) break;
     const int64_t units = (int64_t)((tiles + rg - 1) / rg) * pl.kparts;
-    const int64_t cost = ((units + 255) / 256) * (rg + 1);
+    const int64_t slots = 256 * std::min<int64_t>(2, LDS_MAX / gemv_lds_bytes(M, MT, kpb, rg));
+    const int64_t cost = ((units + slots - 1) / slots) * (rg + 1);
     if (cost <= best_cost) {
       best_cost = cost;
       best_rg = rg;
