@@ -794,9 +794,9 @@ GemvPlan plan_gemv(int M, int N, int K) {
   // count <= GEMV_KPB (multiple of 4) that splits K into equal parts; both
   // within the LDS budget with one tile per unit
   constexpr size_t LDS_MAX = 160 * 1024;
-  // long rows (K >= 16384: o_proj, the dense FFN's down) take 16 KB tiles
-  // (more K parts, two workgroups per CU): measured faster than 32 KB tiles
-  int kmax = K >= 16384 ? 8 : GEMV_KPB;
+  // rows of K >= 2048 (o_proj, the FFN and expert projections) take 16 KB
+  // tiles (more K parts, two workgroups per CU): measured faster than 32 KB
+  int kmax = K >= 2048 ? 8 : GEMV_KPB;
   while (kmax > 4 && gemv_lds_bytes(M, MT, kmax, 1) > LDS_MAX) kmax -= 4;
   int kpb = KB <= kmax ? KB : 0;
   if (!kpb) {
