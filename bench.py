@@ -347,6 +347,11 @@ def head_extras(B, dev):
     logits = ops.final_logits(x, g, w, CFG).reshape(B, V)
     out["sample_top_p_b8_us"] = round(_time_eager(lambda: ops.sample(logits, 0.7, 0.9, seed=1), 20) * 1000, 2)
     out["sample_greedy_b8_us"] = round(_time_eager(lambda: ops.sample(logits, 0.0, 0.9), 20) * 1000, 2)
+    # the same draws by the one-workgroup-per-row entry points
+    res = torch.empty(B, dtype=torch.int64, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    one_wg = lambda: ops.lib().amla_sample_top_p(logits.data_ptr(), B, V, V, 0.7, 0.9, 1, res.data_ptr(), st)
+    out["sample_top_p_b8_one_workgroup_per_row_us"] = round(_time_eager(one_wg, 20) * 1000, 2)
     del w
     torch.cuda.empty_cache()
     return out

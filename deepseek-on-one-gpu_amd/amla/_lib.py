@@ -72,6 +72,9 @@ SIGNATURES = [
     ("amla_argmax", c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     ("amla_sample_top_p", c_int, [c_void_p, c_int64, c_int64, c_int64, c_float, c_float, ctypes.c_uint64, c_void_p,
                                   c_void_p]),
+    ("amla_sample", c_int, [c_void_p, c_int64, c_int64, c_int64, c_float, c_float, ctypes.c_uint64, c_void_p,
+                            c_void_p, c_size_t, c_void_p]),
+    ("amla_sample_workspace_bytes", c_size_t, [c_int64, c_int64]),
     ("amla_moe_combine", c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int64, c_float, c_void_p,
                                  c_void_p]),
 ]

@@ -614,7 +614,8 @@ def sample(logits: torch.Tensor, temperature: float, top_p: float, *, seed: int 
     mass strictly before it exceeds top_p, renormalise, draw one); the draw uses
     a counter-based generator keyed by ``seed`` (default: drawn from torch's CPU
     generator), so it follows the same distribution as torch.multinomial but not
-    its random stream.
+    its random stream.  Each row is cut into chunks (rows x chunks workgroups); the
+    result equals the one-workgroup-per-row kernels' (amla_argmax, amla_sample_top_p).
     """
     _need_cuda(logits, "logits")
     if logits.dtype != torch.float32 or logits.dim() != 2:
@@ -624,11 +625,11 @@ def sample(logits: torch.Tensor, temperature: float, top_p: float, *, seed: int 
     out = torch.empty(B, dtype=torch.int64, device=logits.device)
     if B == 0:
         return out
-    if temperature == 0:
-        check(lib().amla_argmax(lg.data_ptr(), B, n, lg.stride(0), out.data_ptr(), _stream_ptr(logits)), "sample")
-        return out
-    if seed is None:
+    if temperature != 0 and seed is None:
         seed = int(torch.randint(0, 2 ** 62, (1,)).item())
-    check(lib().amla_sample_top_p(lg.data_ptr(), B, n, lg.stride(0), float(temperature), float(top_p),
-                                  int(seed) & (2 ** 64 - 1), out.data_ptr(), _stream_ptr(logits)), "sample")
+    ws_bytes = lib().amla_sample_workspace_bytes(B, n)
+    ws = workspace(logits.device, ws_bytes)
+    check(lib().amla_sample(lg.data_ptr(), B, n, lg.stride(0), float(temperature), float(top_p),
+                            int(seed or 0) & (2 ** 64 - 1), out.data_ptr(), ws.data_ptr(), ws_bytes,
+                            _stream_ptr(logits)), "sample")
     return out

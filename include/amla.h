@@ -260,12 +260,25 @@ int amla_argmax(const float *logits, int64_t rows, int64_t n, int64_t ld, int64_
 
 /* sample(logits, temperature, top_p) of engine.py:166-186 for temperature > 0:
  * p = softmax(logits / temperature); sorted by p descending, a token is dropped when the
- * mass strictly before it exceeds top_p (tokens tied with the last kept one are all kept);
+ * mass strictly before it exceeds top_p (equal probabilities in vocabulary order, the order of
+ * a stable sort: of the tokens tied at the threshold, the first ones are kept);
  * one token is drawn from the renormalised kept p with a counter-based generator keyed
  * by (seed, row).  Same distribution as the reference's torch.multinomial, not the same
- * random stream. */
+ * random stream: the masses are summed in 2^-40 fixed point (integer sums, independent of
+ * the order of the additions), u = floor(K * r / 2^64) for the kept mass K and a 64-bit
+ * random r, and the token is the first kept one in vocabulary order whose running kept
+ * mass exceeds u.  One workgroup per row. */
 int amla_sample_top_p(const float *logits, int64_t rows, int64_t n, int64_t ld, float temperature, float top_p,
                       uint64_t seed, int64_t *out, void *stream);
+
+/* sample(logits, temperature, top_p) of engine.py:166-186 with each row cut into chunks
+ * (rows x chunks workgroups fill the device): temperature 0 gives amla_argmax's result,
+ * temperature > 0 amla_sample_top_p's result for the same seed (the same token).
+ * Workspace of amla_sample_workspace_bytes(rows, n) bytes, 256-byte aligned; scratch only,
+ * nothing needs clearing; calls that share a workspace must be ordered on one stream. */
+int amla_sample(const float *logits, int64_t rows, int64_t n, int64_t ld, float temperature, float top_p,
+                uint64_t seed, int64_t *out, void *workspace, size_t workspace_bytes, void *stream);
+size_t amla_sample_workspace_bytes(int64_t rows, int64_t n);
 
 #ifdef __cplusplus
 }

@@ -8,8 +8,9 @@ the oracle restates what the draw is taken from (``nucleus``: the kept tokens an
 their renormalised probabilities) and the greedy path (temperature 0 -> argmax).
 
 Pinning (tests/test_oracle_head.py): top_p = 0 keeps only the maximum, top_p >= 1
-keeps every token, a hand-worked four-token example, and the kept set equals the
-"mass strictly before the token <= top_p" rule computed in float64 on random rows.
+keeps every token, hand-worked four- and five-token examples (the second with tied
+probabilities), and the kept set equals the "mass strictly before the token <= top_p"
+rule computed in float64 on random rows, with and without ties.
 """
 from __future__ import annotations
 
@@ -32,7 +33,10 @@ def greedy(logits: torch.Tensor) -> torch.Tensor:
 def nucleus(logits: torch.Tensor, temperature: float, top_p: float) -> tuple[torch.Tensor, torch.Tensor]:
     """engine.py:175-182: (kept mask in vocabulary order, renormalised probabilities in vocabulary order)."""
     probs = torch.softmax(logits / temperature, dim=-1)                     # :175
-    sorted_probs, sorted_indices = probs.sort(dim=-1, descending=True)      # :178
+    # :178 calls sort without stable=True, which leaves the order of equal probabilities open
+    # (torch's CPU sort does not keep them in vocabulary order); the oracle fixes it as the
+    # vocabulary order, so that ties at the threshold keep a definite set of tokens
+    sorted_probs, sorted_indices = probs.sort(dim=-1, descending=True, stable=True)
     cumulative = sorted_probs.cumsum(dim=-1)                                # :179
     mask = cumulative - sorted_probs > top_p                                # :180
     sorted_probs[mask] = 0.0                                                # :181

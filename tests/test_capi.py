@@ -174,3 +174,28 @@ def test_moe_experts_dev_checks_sizes_on_the_host():
     assert L.amla_moe_experts_dev(p, m, d, top_k, p, n, E, p, p, p, 64, None) == -2
     assert b"workspace" in L.amla_last_error()
     assert L.amla_moe_experts_dev(p, 0, d, top_k, p, n, E, p, p, p, 0, None) == 0  # nothing to do
+
+
+def test_sample_checks_sizes_on_the_host():
+    """amla_sample: the workspace it asks for (three level histograms per row, chunk maxima and
+    kept masses), and the arguments it rejects before any launch."""
+    L = _lib.lib()
+    # 8 rows of the R1 vocabulary: 64 chunks of 2048 per row (512 workgroups)
+    need = L.amla_sample_workspace_bytes(8, 129280)
+    assert need == 8 * 64 * 8 + 8 * 3 * 2048 * 8 + 8 * 3 * 32 + 8 * 64 * 16
+    assert L.amla_sample_workspace_bytes(1, 129280) >= 3 * 2048 * 8 + 127 * 16     # 127 chunks of 1024
+    assert L.amla_sample_workspace_bytes(0, 100) == 0
+    assert L.amla_sample_workspace_bytes(4, 0) == 0
+    buf = ctypes.create_string_buffer(1024)
+    p0 = ctypes.cast(buf, ctypes.c_void_p).value
+    p = p0 + 256 - p0 % 256 if p0 % 256 else p0       # 256-byte aligned host address, never dereferenced
+    assert L.amla_sample(None, 8, 129280, 129280, 1.0, 0.9, 1, p, p, need, None) == -1
+    assert L.amla_sample(p, 8, 129280, 100, 1.0, 0.9, 1, p, p, need, None) == -1          # ld < n
+    assert L.amla_sample(p, 8, 129280, 129280, -1.0, 0.9, 1, p, p, need, None) == -1      # temperature < 0
+    assert L.amla_sample(p, 8, 129280, 129280, 1.0, float("nan"), 1, p, p, need, None) == -1
+    assert L.amla_sample(p, 8, 129280, 129280, 1.0, 0.9, 1, p, p, need - 1, None) == -2
+    assert b"workspace" in L.amla_last_error()
+    assert L.amla_sample(p, 8, 129280, 129280, 0.0, 0.9, 1, p, None, 0, None) == -2
+    assert L.amla_sample(p, 8, 129280, 129280, 1.0, 0.9, 1, p, p + 16, need, None) == -1  # alignment
+    assert b"aligned" in L.amla_last_error()
+    assert L.amla_sample(p, 0, 129280, 129280, 1.0, 0.9, 1, p, None, 0, None) == 0        # nothing to do

@@ -80,3 +80,64 @@ def test_empty_inputs():
     lg = torch.zeros(0, 48, device=DEV)
     assert ops.sample(lg, 0.0, 0.9).shape == (0,)
     assert ops.sample(lg, 1.0, 0.9).shape == (0,)
+
+
+def _one_workgroup_per_row(lg, temp, top_p, seed):
+    """amla_argmax / amla_sample_top_p (one workgroup per row) through the C-ABI."""
+    B, n = lg.shape
+    out = torch.empty(B, dtype=torch.int64, device=DEV)
+    L, st = ops.lib(), ops._stream_ptr(lg)
+    if temp == 0:
+        rc = L.amla_argmax(lg.data_ptr(), B, n, lg.stride(0), out.data_ptr(), st)
+    else:
+        rc = L.amla_sample_top_p(lg.data_ptr(), B, n, lg.stride(0), temp, top_p, seed, out.data_ptr(), st)
+    ops.check(rc, "one workgroup per row")
+    return out
+
+
+@pytest.mark.parametrize("rows,n,ld", [(8, 129280, 129280), (1, 129280, 129280), (3, 5000, 5008), (64, 1000, 1000),
+                                       (2, 1, 1), (5, 70000, 70001), (600, 3000, 3000)])
+def test_chunked_sample_equals_one_workgroup_per_row(rows, n, ld):
+    """amla_sample (rows cut into chunks, histograms merged with integer atomics) returns the same
+    token as the one-workgroup kernels for every (temperature, top_p, seed), each inside the
+    oracle's nucleus.  Half the rows hold logits on a grid of 1/4, so many tokens tie, also at the
+    threshold."""
+    print(f"[case] chunked sample rows={rows} n={n} ld={ld}", flush=True)
+    g = torch.Generator().manual_seed(rows * 1009 + n)
+    buf = torch.randn(rows, ld, generator=g) * 2.5
+    buf[::2] = torch.round(buf[::2] * 4) / 4
+    lg_cpu = buf[:, :n]
+    lg = buf.to(DEV)[:, :n]
+    got = ops.sample(lg, 0.0, 0.9)
+    assert torch.equal(got, _one_workgroup_per_row(lg, 0.0, 0.9, 0)), "temperature 0"
+    assert got.cpu().tolist() == H.greedy(lg_cpu).tolist()
+    for temp, top_p, seed in ((1.0, 0.9, 11), (0.7, 0.5, 12), (1.3, 0.99, 13), (1.0, 0.0, 14), (1.0, 1.0, 15),
+                              (0.9, 5.0, 16), (1.0, 0.9, 2 ** 63 + 17)):
+        got = ops.sample(lg, temp, top_p, seed=seed)
+        want = _one_workgroup_per_row(lg, temp, top_p, seed)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (temp, top_p, seed)
+        kept, _ = H.nucleus(lg_cpu, temp, top_p)
+        assert kept[torch.arange(rows), got.cpu()].all(), (temp, top_p, seed)
+
+
+def test_sample_in_a_hip_graph():
+    """ops.sample captured once (workspace from the graph's pool), replayed on new logits with
+    eager work between replays: every replay equals the eager call."""
+    print("[case] sample graph capture B=8 V=129280", flush=True)
+    g = torch.Generator().manual_seed(21)
+    inputs = [torch.randn(8, 129280, generator=g) * 2 for _ in range(3)]
+    static = inputs[0].to(DEV)
+    for temp in (0.0, 0.8):
+        ops.sample(static, temp, 0.9, seed=5)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_out = ops.sample(static, temp, 0.9, seed=5)
+        for r, x in enumerate(inputs):
+            static.copy_(x.to(DEV))
+            eager = ops.sample(x.to(DEV), temp, 0.9, seed=5)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static_out, eager), (temp, r)

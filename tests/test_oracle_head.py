@@ -26,10 +26,27 @@ def test_nucleus_hand_example():
     torch.testing.assert_close(q, torch.tensor([[0.0, 0.625, 0.0, 0.375]]))
 
 
+def test_nucleus_ties_in_vocabulary_order():
+    # probabilities proportional to 1, e, e, e, 1: p_e = e / (3e + 2), p_1 = 1 / (3e + 2).
+    # Sorted with ties in vocabulary order: 1, 2, 3 (mass before 0, p_e, 2 p_e), then 0, 4.
+    logits = torch.tensor([[0.0, 1.0, 1.0, 1.0, 0.0]])
+    e = float(np.e)
+    p_e, p_1 = e / (3 * e + 2), 1 / (3 * e + 2)
+    kept, _ = H.nucleus(logits, 1.0, 0.0)
+    assert kept.tolist() == [[False, True, False, False, False]]        # only the first maximum
+    kept, q = H.nucleus(logits, 1.0, 1.5 * p_e)                          # 2 p_e > 1.5 p_e: token 3 dropped
+    assert kept.tolist() == [[False, True, True, False, False]]
+    torch.testing.assert_close(q, torch.tensor([[0.0, 0.5, 0.5, 0.0, 0.0]]))
+    kept, _ = H.nucleus(logits, 1.0, 3 * p_e + 0.5 * p_1)                # token 0 at 3 p_e, token 4 at 3 p_e + p_1
+    assert kept.tolist() == [[True, True, True, True, False]]
+
+
 def test_nucleus_rule_float64():
     g = torch.Generator().manual_seed(1)
-    for top_p in (0.1, 0.5, 0.9, 0.99):
+    for top_p, tied in ((0.1, False), (0.5, False), (0.9, False), (0.99, False), (0.5, True), (0.9, True)):
         logits = torch.randn(4, 300, generator=g) * 3
+        if tied:
+            logits = torch.round(logits * 2) / 2          # many equal probabilities
         kept, _ = H.nucleus(logits, 0.8, top_p)
         pr = torch.softmax(logits.double() / 0.8, -1).numpy()
         for r in range(4):
