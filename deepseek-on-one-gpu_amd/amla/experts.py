@@ -3,7 +3,7 @@ inference/gpu_transfer.py:7-89 (GPUTransfer).
 
 The reference copies the 8 experts of one token into 8 fixed device buffers on
 a side stream, then waits for that stream on the host (``transfer_stream.
-synchronize()``, gpu_transfer.py:82) before every token's expert compute.
+synchronize()``, gpu_transfer.py:79) before every token's expert compute.
 Here the device side is a pool of expert slots kept as stacked tensors
 ``(slots, rows, cols)`` with an LRU map (layer, expert) -> slot, so experts
 that stay hot are not copied again; copies run on a side stream and are ordered

@@ -119,17 +119,6 @@ int launch_gemv_sched(const GemvParams &p, const MoeSched &s, int max_entries, i
                       hipStream_t stream);
 // Large-M fp8 GEMM tiles of the scheduled entries (rows <= 256 each).
 int launch_gemm_sched(const GemvParams &p, const MoeSched &s, int max_entries, hipStream_t stream);
-// Register-streaming skinny GEMM for M <= 16 (weights HBM -> VGPRs, x in
-// LDS).  Blocks per wave per tile: at most RS_NARROW_NB with three tiles in
-// flight, or RS_WIDE_NB (one part of up to 4 * RS_WIDE_NB blocks) with one.
-constexpr int RS_NARROW_NB = 4;
-constexpr int RS_WIDE_NB = 16;
-GemvPlan plan_gemv_rs(int M, int N, int K);
-size_t gemv_rs_lds_bytes(int M, int kpb, int rg);
-// xgamma != nullptr: x rows are replaced by rms_norm(x, xgamma, eps) first
-// (needs plan.kparts == 1).
-int launch_gemv_rs(const GemvParams &p, int mode, const GemvPlan &plan, const uint16_t *xgamma, float eps,
-                   hipStream_t stream, bool finish = true);
 // Large-M fp8 GEMM with the same modes (M > 64).  With split_ws of at least
 // gemm_ws_bytes(M, N, K) bytes, tiles past the last full round of 256
 // workgroups are cut into K parts (fp32 partial sums in split_ws, summed in

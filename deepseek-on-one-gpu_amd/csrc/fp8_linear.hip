@@ -6,17 +6,19 @@
 //   amla_apply_rope         <- inference/ops.py:86-97
 //
 // Skinny GEMM (M <= 64, the decode projections): HBM-bound on the fp8 weight
-// stream.  Each wave owns RT tiles of 16 weight rows and walks 128-wide K
-// blocks; per block a lane loads 32 contiguous fp8 bytes of one row (4 lanes
-// cover the block's 128 bytes), converts them exactly to bf16 and issues four
-// v_mfma_f32_16x16x32_bf16 against x^T (batch rows as the MFMA N dimension).
-// The block's partial product is scaled by its fp32 scale_inv (wave-uniform:
-// a 16-row tile never straddles a 128-row scale block) and added to an fp32
-// accumulator, so the weight is never materialised.  The 4-16 waves of a
-// workgroup split the K blocks and reduce through LDS in a fixed order, so
-// results are deterministic and no workgroup waits on another (a split of K
-// across workgroups would need device-scope release fences, which write back
-// the per-XCD L2s and cost more than they save).
+// stream.  Weight tiles of 16 rows stream HBM -> LDS by LDS-DMA; the 4 waves
+// of a workgroup split a tile's 128-wide K blocks, convert the fp8 bytes
+// exactly to bf16 and issue v_mfma_f32_16x16x32_bf16 against x^T (batch rows
+// as the MFMA N dimension).  A block's partial product is scaled by its fp32
+// scale_inv (wave-uniform: a 16-row tile never straddles a 128-row scale
+// block) and added to an fp32 accumulator, so the weight is never
+// materialised; the waves' partial tiles are summed through LDS in wave
+// order.  A long K is split into K parts over workgroups: their fp32 sums go
+// to the workspace and a finishing pass (gemv_finish, or the consumer's own
+// finish) adds them in part order.  Results are deterministic, and no
+// workgroup waits on another: an in-kernel finish would need device-scope
+// release fences, which write back the per-XCD L2s and cost more than the
+// separate pass.  M > 64 takes the tiled GEMM (gemm_kernel, mla_prefill.hip).
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -445,275 +447,6 @@ __global__ __launch_bounds__(64) void gemv_finish_sched(GemvParams p, MoeSched s
   gemv_finish_body<GEMV_PLAIN>(p, (int64_t)(blockIdx.x % units) * 64 + threadIdx.x, kparts);
 }
 
-// ---------------------------------------------------------------- register-streaming skinny GEMM
-
-// Skinny GEMM for M <= 16 with the weights streamed HBM -> VGPRs (no LDS on
-// the weight path) and x staged once per workgroup in LDS as bf16.  A
-// workgroup (4 waves) owns rg consecutive 16-row tiles of one K part; wave w
-// owns blocks w, w + 4, .. of the part (NBMAX per wave at most).  Lane
-// (row l%16, group g = l/16) loads bytes 16g.. and 64 + 16g.. of each 128-byte
-// block of its row: the same K order as gemv_body, so the x fragments are the
-// same.  Tiles are loaded PD ahead in a register ring; loads of tiles past the
-// workgroup's last re-read its last tile (in bounds, an L2 hit, unused).  Per
-// tile each wave writes its 16 x 16 partial to LDS; after the last tile one
-// barrier and the waves' partials are summed in wave order (deterministic)
-// into the epilogue or the fp32 K-part sums.
-//
-// x (the K part of every row) is copied into LDS by LDS-DMA, all copies in
-// flight at once.  XNORM: the rows are then replaced in LDS by
-// rms_norm(x, xgamma, eps) (both roundings of inference/ops.py:10-12),
-// computed in every workgroup from the whole row (read once per workgroup,
-// from L2 after the first); needs the whole K in one part.
-template <int NBMAX, int PD, int MODE, bool XNORM>
-__global__ __launch_bounds__(256) void gemv_rs_kernel(GemvParams p, int rg, int kparts, int kpb,
-                                                      const uint16_t *__restrict__ xgamma, float eps) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int li = lane & 15, lg = lane >> 4;
-  const int KB = p.K >> 7;
-  const int ntiles = p.N >> 4;
-  const int unit = blockIdx.x;
-  const int part = unit % kparts;
-  const int tile_begin = (unit / kparts) * rg;
-  const int tile_end = min(tile_begin + rg, ntiles);
-  const int nt_here = tile_end - tile_begin;
-  const int kb_begin = part * kpb;
-  const int nbp = min(kpb, KB - kb_begin);         // blocks of this part
-  const int nbw = (nbp - wave + 3) >> 2;            // blocks of this wave (<= NBMAX)
-  const int XROW = nbp * 256 + 16;                  // bytes per x row in LDS (16 B pad)
-
-  extern __shared__ __align__(16) uint8_t rsm[];
-  uint8_t *const xs = rsm;                                      // [M][XROW]
-  f32x4 *const red = reinterpret_cast<f32x4 *>(rsm + p.M * XROW);  // [rg][4 waves][64]
-
-  // weight loads of one tile into a ring slot (row li, this wave's blocks)
-  auto load_tile = [&](int tile, u32x4 (&wv)[NBMAX][2]) {
-    const int nt = min(tile, tile_end - 1) * 16;
-    const bool seg1 = (MODE == GEMV_QKVA || p.w1) && nt >= p.n_split;
-    const uint8_t *wb = (seg1 ? p.w1 : p.w0) + (size_t)(seg1 ? nt - p.n_split : nt) * p.K + (size_t)li * p.K +
-                        (size_t)kb_begin * 128 + lg * 16;
-#pragma unroll
-    for (int j = 0; j < NBMAX; ++j) {
-      const int bl = min(wave + 4 * j, nbp - 1);  // blocks past this wave's share re-read one in bounds
-      wv[j][0] = ldg16(wb + bl * 128);
-      wv[j][1] = ldg16(wb + bl * 128 + 64);
-    }
-  };
-
-  // ---- x part -> LDS by LDS-DMA, every copy in flight at once: a copy moves
-  // 64 16-byte chunks (1 KB) of one row; row m's chunk c lands at
-  // xs + m * XROW + c * 16.  The copies go out before the weight loads, so
-  // waiting until only the weight loads are outstanding (loads complete in
-  // order) means x has landed.
-  {
-    const int cpr = nbp * 16;                      // 16-byte chunks of x per row in this part
-    const int spr = (cpr + 63) >> 6;               // copies per row
-    for (int q = wave; q < p.M * spr; q += 4) {
-      const int m = q / spr, sgm = q % spr;
-      const int c = sgm * 64 + lane;
-      if (c < cpr)
-        __builtin_amdgcn_global_load_lds(p.x + (size_t)m * p.ldx + (size_t)kb_begin * 128 + c * 8,
-                                         LDS_PTR(xs + m * XROW + sgm * 1024), 16, 0, 0);
-    }
-  }
-  u32x4 ring[PD][NBMAX][2];
-#pragma unroll
-  for (int s = 0; s < PD; ++s) load_tile(tile_begin + s, ring[s]);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(PD * NBMAX * 2) : "memory");
-  __syncthreads();
-
-  if constexpr (XNORM) {
-    // rms_norm of each row in place (the part is the whole row): wave w takes
-    // rows w, w + 4, ..; every chunk of the row is read before the sum (up to
-    // 16 per lane), then written back normalised: y = bf16(bf16(x * r) * g)
-    constexpr int RCH = 16;  // chunks per lane: K <= 64 * 16 * 8
-    const int cpr = p.K / 8;
-    for (int m = wave; m < p.M; m += 4) {
-      uint8_t *xr = xs + m * XROW;
-      u32x4 v[RCH];
-#pragma unroll
-      for (int i = 0; i < RCH; ++i) {
-        const int c = i * 64 + lane;
-        v[i] = c < cpr ? *reinterpret_cast<const u32x4 *>(xr + c * 16) : u32x4{0, 0, 0, 0};
-      }
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < RCH; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ss += lo_bf(v[i][e]) * lo_bf(v[i][e]) + hi_bf(v[i][e]) * hi_bf(v[i][e]);
-      ss = wave_sum(ss);
-      const float r = rsqrtf(ss / (float)p.K + eps);
-#pragma unroll
-      for (int i = 0; i < RCH; ++i) {
-        const int c = i * 64 + lane;
-        if (c < cpr) {
-          const u32x4 g = ldg16(xgamma + c * 8);
-          u32x4 o;
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            o[e] = pack_bf16(round_bf16(lo_bf(v[i][e]) * r) * lo_bf(g[e]), round_bf16(hi_bf(v[i][e]) * r) * hi_bf(g[e]));
-          *reinterpret_cast<u32x4 *>(xr + c * 16) = o;
-        }
-      }
-    }
-    __syncthreads();
-  }
-
-  // this wave's block scales per tile come through the scalar cache (the
-  // scales are never written here)
-  const bool xrow_ok = li < p.M;
-  const uint8_t *xl = xs + (xrow_ok ? li : 0) * XROW + lg * 32;
-  for (int base = 0; base < nt_here; base += PD) {
-#pragma unroll
-    for (int s = 0; s < PD; ++s) {
-      const int it = base + s;
-      if (it < nt_here) {
-        const int nt = (tile_begin + it) * 16;
-        const bool seg1 = (MODE == GEMV_QKVA || p.w1) && nt >= p.n_split;
-        const __attribute__((address_space(4))) float *srow = (const __attribute__((address_space(4))) float *)(
-            (seg1 ? p.s1 : p.s0) + (size_t)((seg1 ? nt - p.n_split : nt) >> 7) * KB + kb_begin);
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < NBMAX; ++j) {
-          if (j < nbw) {
-            const int bl = wave + 4 * j;
-            bf16x8 a0, a1, a2, a3;
-            fp8x16_to_bf16x16(ring[s][j][0], a0, a1);
-            fp8x16_to_bf16x16(ring[s][j][1], a2, a3);
-            const uint8_t *xp = xl + bl * 256;
-            const u32x4 z = {0, 0, 0, 0};
-            const bf16x8 x0 = as_bf16x8(xrow_ok ? *reinterpret_cast<const u32x4 *>(xp) : z);
-            const bf16x8 x1 = as_bf16x8(xrow_ok ? *reinterpret_cast<const u32x4 *>(xp + 16) : z);
-            const bf16x8 x2 = as_bf16x8(xrow_ok ? *reinterpret_cast<const u32x4 *>(xp + 128) : z);
-            const bf16x8 x3 = as_bf16x8(xrow_ok ? *reinterpret_cast<const u32x4 *>(xp + 144) : z);
-            f32x4 c = {0.f, 0.f, 0.f, 0.f};
-            c = mfma16(a0, x0, c);
-            c = mfma16(a1, x1, c);
-            c = mfma16(a2, x2, c);
-            c = mfma16(a3, x3, c);
-            acc += srow[bl] * c;
-          }
-        }
-        red[(it * 4 + wave) * 64 + lane] = acc;
-        load_tile(tile_begin + it + PD, ring[s]);  // the slot is free again
-      }
-    }
-  }
-  __syncthreads();
-  // partials of the unit: waves summed in order, then the epilogue or the K-part sums
-  for (int idx = tid; idx < nt_here * 64; idx += 256) {
-    const int tl = idx >> 6, ln = idx & 63;
-    const int m = ln & 15;
-    const int n = (tile_begin + tl) * 16 + 4 * (ln >> 4);
-    if (m >= p.M) continue;
-    f32x4 v = red[(tl * 4 + 0) * 64 + ln];
-    v += red[(tl * 4 + 1) * 64 + ln];
-    v += red[(tl * 4 + 2) * 64 + ln];
-    v += red[(tl * 4 + 3) * 64 + ln];
-    if (kparts == 1) store4<MODE>(p, m, n, v);
-    else *reinterpret_cast<f32x4 *>(p.part + ((size_t)part * p.M + m) * p.N + n) = v;
-  }
-}
-
-size_t gemv_rs_lds_bytes(int M, int kpb, int rg) {
-  return (size_t)M * (kpb * 256 + 16) + (size_t)rg * 4 * 64 * 16;
-}
-
-// Plan of gemv_rs_kernel for M <= 16: one K part (no finishing pass) when the
-// row tiles alone fill half the machine and K fits one workgroup's LDS, else
-// K parts of <= 16 blocks; tiles per workgroup as plan_gemv (fewest rounds of
-// 256 workgroups, then the longest run).
-GemvPlan plan_gemv_rs(int M, int N, int K) {
-  GemvPlan pl = {};
-  const int tiles = N / 16;
-  const int KB = K / 128;
-  constexpr size_t LDS_MAX = 160 * 1024;
-  if (tiles >= 128 && KB <= 4 * RS_WIDE_NB && gemv_rs_lds_bytes(M, KB, 1) <= LDS_MAX) {
-    pl.kpb = KB;
-  } else {
-    int kpb = 0;
-    for (int c = 4 * RS_NARROW_NB; c >= 4; --c)
-      if (KB % c == 0) { kpb = c; break; }
-    pl.kpb = kpb ? kpb : std::min(KB, 4 * RS_NARROW_NB);
-  }
-  pl.kparts = (KB + pl.kpb - 1) / pl.kpb;
-  int best_rg = 1;
-  int64_t best_cost = INT64_MAX;
-  for (int rg = 1; rg <= GEMV_MAX_RG; ++rg) {
-    if (gemv_rs_lds_bytes(M, pl.kpb, rg) > LDS_MAX) break;
-    const int64_t units = (int64_t)((tiles + rg - 1) / rg) * pl.kparts;
-    const int64_t cost = ((units + 255) / 256) * (rg + 1);
-    if (cost <= best_cost) {
-      best_cost = cost;
-      best_rg = rg;
-    }
-  }
-  pl.rg = best_rg;
-  pl.groups = ((tiles + pl.rg - 1) / pl.rg) * pl.kparts;
-  pl.lds = gemv_rs_lds_bytes(M, pl.kpb, pl.rg);
-  pl.part_bytes = pl.kparts > 1 ? (size_t)pl.kparts * M * N * 4 : 0;
-  return pl;
-}
-
-template <int NBMAX, int PD, int MODE, bool XNORM>
-static void launch_rs_cfg(const GemvParams &p, const GemvPlan &pl, const uint16_t *xgamma, float eps,
-                          hipStream_t st) {
-  static bool attr_set = false;  // raise the dynamic LDS limit once per process
-  if (!attr_set) {
-    (void)hipFuncSetAttribute((const void *)gemv_rs_kernel<NBMAX, PD, MODE, XNORM>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    attr_set = true;
-  }
-  gemv_rs_kernel<NBMAX, PD, MODE, XNORM><<<dim3(pl.groups), 256, pl.lds, st>>>(p, pl.rg, pl.kparts, pl.kpb, xgamma,
-                                                                                eps);
-}
-
-template <int MODE, bool XNORM>
-static void launch_rs_mode(const GemvParams &p, const GemvPlan &pl, const uint16_t *xgamma, float eps,
-                           hipStream_t st) {
-  if ((pl.kpb + 3) / 4 <= RS_NARROW_NB) launch_rs_cfg<RS_NARROW_NB, 3, MODE, XNORM>(p, pl, xgamma, eps, st);
-  else launch_rs_cfg<RS_WIDE_NB, 1, MODE, XNORM>(p, pl, xgamma, eps, st);
-}
-
-int launch_gemv_rs(const GemvParams &p0, int mode, const GemvPlan &pl, const uint16_t *xgamma, float eps,
-                   hipStream_t st, bool finish) {
-  if (p0.M < 1 || p0.M > 16) return fail(AMLA_EINVAL, "register-streaming fp8 GEMM needs 1 <= M <= 16 (got %d)", p0.M);
-  if (p0.N % 16 || p0.K % 128)
-    return fail(AMLA_EUNSUPPORTED, "fp8 GEMM needs N %% 16 == 0 and K %% 128 == 0 (N=%d K=%d)", p0.N, p0.K);
-  if ((pl.kpb + 3) / 4 > RS_WIDE_NB || pl.kparts > GEMV_MAX_PARTS)
-    return fail(AMLA_EUNSUPPORTED, "register-streaming fp8 GEMM: plan out of range (kpb=%d, kparts=%d)", pl.kpb,
-                pl.kparts);
-  if (xgamma && pl.kparts != 1) return fail(AMLA_EINVAL, "fp8 GEMM: a fused input norm needs the whole K in one part");
-  if (pl.kparts > 1 && !p0.part) return fail(AMLA_EWORKSPACE, "fp8 GEMM: missing partial-sum workspace");
-  if ((mode == GEMV_QKVA && p0.max_rows <= 0) || (mode == GEMV_QROPE && p0.rope_rows <= 0))
-    return fail(AMLA_EINVAL, "fp8 GEMM: cache rows / rope rows of the epilogue not set");
-  if (p0.w1 && p0.n_split % 128)
-    return fail(AMLA_EUNSUPPORTED, "fp8 GEMM: the first weight segment must be a multiple of 128 rows");
-  if (p0.ldx % 8 || !aligned16(p0.x)) return fail(AMLA_EUNSUPPORTED, "fp8 GEMM: x rows must be 16-byte aligned");
-  const bool xn = xgamma != nullptr;
-  switch (mode) {
-    case GEMV_PLAIN: xn ? launch_rs_mode<GEMV_PLAIN, true>(p0, pl, xgamma, eps, st)
-                        : launch_rs_mode<GEMV_PLAIN, false>(p0, pl, xgamma, eps, st); break;
-    case GEMV_RESID: xn ? launch_rs_mode<GEMV_RESID, true>(p0, pl, xgamma, eps, st)
-                        : launch_rs_mode<GEMV_RESID, false>(p0, pl, xgamma, eps, st); break;
-    case GEMV_QKVA: xn ? launch_rs_mode<GEMV_QKVA, true>(p0, pl, xgamma, eps, st)
-                       : launch_rs_mode<GEMV_QKVA, false>(p0, pl, xgamma, eps, st); break;
-    default: xn ? launch_rs_mode<GEMV_QROPE, true>(p0, pl, xgamma, eps, st)
-                : launch_rs_mode<GEMV_QROPE, false>(p0, pl, xgamma, eps, st); break;
-  }
-  if (pl.kparts > 1 && finish) {
-    const int64_t total = (int64_t)p0.M * (p0.N / 4);
-    const unsigned blocks = (unsigned)((total + 63) / 64);
-    switch (mode) {
-      case GEMV_PLAIN: gemv_finish<GEMV_PLAIN><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
-      case GEMV_RESID: gemv_finish<GEMV_RESID><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
-      case GEMV_QKVA: gemv_finish<GEMV_QKVA><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
-      default: gemv_finish<GEMV_QROPE><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
-    }
-  }
-  return check_launch("register-streaming fp8 GEMM");
-}
-
 // One workgroup per row m: sums the K parts of every output of the row in
 // part order, stores the kv_a columns (n >= n_split) into the caches, and
 // normalises the bf16 q_a columns: r = rsqrt(mean(q_a^2) + eps),
@@ -1119,15 +852,14 @@ int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void
   p.seq_len = 1;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (m > 64) return launch_gemm(p, GEMV_PLAIN, st);
-  const bool rs = false;  // the register-streaming kernel is not dispatched (see mla_decode.hip)
-  const GemvPlan pl = rs ? plan_gemv_rs((int)m, (int)n, (int)k) : plan_gemv((int)m, (int)n, (int)k);
+  const GemvPlan pl = plan_gemv((int)m, (int)n, (int)k);
   if (pl.part_bytes) {
     if (!workspace || workspace_bytes < pl.part_bytes || !aligned16(workspace))
       return fail(AMLA_EWORKSPACE, "fp8_linear: needs %zu bytes of 16-byte aligned workspace (got %zu)", pl.part_bytes,
                   workspace ? workspace_bytes : (size_t)0);
     p.part = reinterpret_cast<float *>(workspace);
   }
-  return rs ? launch_gemv_rs(p, GEMV_PLAIN, pl, nullptr, 0.f, st) : launch_gemv(p, GEMV_PLAIN, pl, st);
+  return launch_gemv(p, GEMV_PLAIN, pl, st);
 }
 
 int amla_rms_norm(const void *x, int64_t rows, int64_t dim, int64_t ldx, const void *gamma, float eps,

@@ -1005,15 +1005,9 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
 
 // ---------------------------------------------------------------- orchestration
 
-// The register-streaming decode GEMVs with fused norms are built but not
-// dispatched: in their present form they are slower than the LDS-streaming
-// GEMVs (their weight prefetch is cut short by conservative waits).
-constexpr bool kDecodeFusedNorms = false;
-
 struct DecodeLayout {
   size_t xn, qa, q, qbuf, part_ml, part_o, attn, lin, total;
   GemvPlan pa, pb, po;
-  bool rs;  // register-streaming skinny GEMMs with fused norms (batch <= 16)
   int units, slots;  // split plan size (device side: seq_splits) and partial slots
 };
 
@@ -1021,20 +1015,9 @@ static DecodeLayout decode_layout(const amla_mla_args &a) {
   DecodeLayout L = {};
   const int B = a.batch;
   const int HD = a.qk_nope + a.qk_rope;
-  // batch <= 16: q_a | kv_a reads the whole K in one pass (the input RMSNorm
-  // fused into its x staging, no finishing pass), q_b fuses q_a_layernorm the
-  // same way; larger batches take the LDS-streaming GEMM with K-part finishes
-  L.rs = kDecodeFusedNorms && B <= 16 && plan_gemv_rs(B, a.q_lora + a.kv_lora + a.qk_rope, a.hidden).kparts == 1 &&
-         plan_gemv_rs(B, a.heads * HD, a.q_lora).kparts == 1;
-  if (L.rs) {
-    L.pa = plan_gemv_rs(B, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
-    L.pb = plan_gemv_rs(B, a.heads * HD, a.q_lora);
-    L.po = plan_gemv_rs(B, a.hidden, a.heads * a.v_dim);
-  } else {
-    L.pa = plan_gemv(B, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
-    L.pb = plan_gemv(B, a.heads * HD, a.q_lora);
-    L.po = plan_gemv(B, a.hidden, a.heads * a.v_dim);
-  }
+  L.pa = plan_gemv(B, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
+  L.pb = plan_gemv(B, a.heads * HD, a.q_lora);
+  L.po = plan_gemv(B, a.hidden, a.heads * a.v_dim);
   // splits over the batch: one per CU, at least two tiles each for the
   // longest possible context; the plan itself is made on the device from the
   // positions (seq_splits), so a ragged batch is balanced by its total tokens
@@ -1113,7 +1096,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   //    caches, inference/ops.py:136-141; forward.py:92)
   mark(ev, 0, st);
   const uint16_t *xin = x;
-  if (a->input_gamma && !L.rs) {
+  if (a->input_gamma) {
     uint16_t *xn = reinterpret_cast<uint16_t *>(ws + L.xn);
     if ((rc = launch_rms_norm(x, B, a->hidden, a->hidden, reinterpret_cast<const uint16_t *>(a->input_gamma), a->eps,
                               xn, a->hidden, st)))
@@ -1131,17 +1114,11 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pa.ckv_bstride = (int64_t)a->max_seq * LORA; pa.kpe_bstride = (int64_t)a->max_seq * ROPE;
   pa.kv_lora = LORA; pa.rope = ROPE; pa.pos = a->positions; pa.seq_len = 1; pa.max_rows = a->max_seq;
   pa.part = reinterpret_cast<float *>(ws + L.lin);
-  // 2. q_a_layernorm (inference/ops.py:130): in q_b's x staging (batch <= 16),
-  //    else fused into the K-part finish, or a row norm in place when the
-  //    GEMV needs no finishing pass
+  // 2. q_a_layernorm (inference/ops.py:130): fused into the K-part finish, or
+  //    a row norm in place when the GEMV needs no finishing pass
   mark(ev, 1, st);
   const uint16_t *gq = reinterpret_cast<const uint16_t *>(a->gamma_q);
-  if (L.rs) {
-    // one pass over [wq_a; wkv_a] with the input norm fused; q_a stays raw
-    // (bf16) for q_b, which normalises it in its own x staging
-    if ((rc = launch_gemv_rs(pa, GEMV_QKVA, L.pa, reinterpret_cast<const uint16_t *>(a->input_gamma), a->eps, st)))
-      return rc;
-  } else if (L.pa.kparts > 1) {
+  if (L.pa.kparts > 1) {
     if ((rc = launch_gemv(pa, GEMV_QKVA, L.pa, st, false))) return rc;
     if ((rc = launch_qkva_finish_norm(pa, L.pa.kparts, gq, a->eps, st))) return rc;
   } else {
@@ -1159,11 +1136,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pb.pos = a->positions; pb.seq_len = 1; pb.rope = ROPE; pb.rope_table = a->rope_table; pb.rope_rows = a->rope_rows;
   pb.head_dim = HD; pb.nope = a->qk_nope;
   pb.part = reinterpret_cast<float *>(ws + L.lin);
-  if (L.rs) {
-    if ((rc = launch_gemv_rs(pb, GEMV_QROPE, L.pb, gq, a->eps, st))) return rc;
-  } else if ((rc = launch_gemv(pb, GEMV_QROPE, L.pb, st))) {
-    return rc;
-  }
+  if ((rc = launch_gemv(pb, GEMV_QROPE, L.pb, st))) return rc;
 
   // 4. absorb W_UK into the query
   mark(ev, 3, st);
@@ -1206,8 +1179,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   po.res = reinterpret_cast<const uint16_t *>(a->residual); po.ldr = a->hidden;
   po.seq_len = 1;
   po.part = reinterpret_cast<float *>(ws + L.lin);
-  rc = L.rs ? launch_gemv_rs(po, a->residual ? GEMV_RESID : GEMV_PLAIN, L.po, nullptr, 0.f, st)
-            : launch_gemv(po, a->residual ? GEMV_RESID : GEMV_PLAIN, L.po, st);
+  rc = launch_gemv(po, a->residual ? GEMV_RESID : GEMV_PLAIN, L.po, st);
   mark(ev, NSTAGE, st);
   return rc;
 }

@@ -64,3 +64,27 @@ def test_nucleus_rule_float64():
 def test_greedy_ties_to_first():
     logits = torch.tensor([[1.0, 3.0, 3.0, 2.0], [5.0, 5.0, 5.0, 5.0]])
     assert H.greedy(logits).tolist() == [1, 0]
+
+
+def test_lm_head_logits_one_hot_and_float64():
+    """forward.py:67-72 restated: one-hot vocabulary rows select single normed hidden entries
+    exactly; a weight of powers of two scales the logits exactly; random weights agree with a
+    float64 product of the same bf16 operands to fp32 summation accuracy."""
+    from oracle.ref_ops import rms_norm
+    g = torch.Generator().manual_seed(5)
+    h = torch.randn(3, 1, 256, generator=g).to(torch.bfloat16)
+    gamma = (1 + 0.1 * torch.randn(256, generator=g)).to(torch.bfloat16)
+    hn = rms_norm(h, gamma, 1e-6).float().reshape(3, 256)
+    sel = torch.tensor([0, 17, 255, 128, 3])
+    w = torch.zeros(5, 256, dtype=torch.bfloat16)
+    w[torch.arange(5), sel] = 1.0
+    got = H.lm_head_logits(h, gamma, w, 1e-6).reshape(3, 5)
+    assert torch.equal(got, hn[:, sel])
+    w2 = torch.zeros(5, 256, dtype=torch.bfloat16)
+    w2[torch.arange(5), sel] = torch.tensor([2.0, -4.0, 0.5, 8.0, -0.25], dtype=torch.bfloat16)
+    got2 = H.lm_head_logits(h, gamma, w2, 1e-6).reshape(3, 5)
+    assert torch.equal(got2, hn[:, sel] * torch.tensor([2.0, -4.0, 0.5, 8.0, -0.25]))
+    wr = (torch.randn(64, 256, generator=g) * 0.05).to(torch.bfloat16)
+    got3 = H.lm_head_logits(h, gamma, wr, 1e-6).reshape(3, 64).double()
+    want = hn.double() @ wr.double().T
+    assert (got3 - want).abs().max() < 1e-5
