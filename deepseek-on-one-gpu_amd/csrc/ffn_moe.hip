@@ -249,72 +249,93 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t *__res
   }
 }
 
-constexpr int ROUTE_MAX_E = 1024;  // experts per token handled by one wave (16 per lane)
+constexpr int ROUTE_MAX_E = 1024;           // experts per token handled by one wave
+constexpr int ROUTE_EPL = ROUTE_MAX_E / 64;  // experts per lane (lane l: l, l + 64, ..)
+constexpr int ROUTE_MAX_Z = 8;               // K splits of the logits (route_ksplit)
 
 // One wave per token: scores = sigmoid(logits); rank the n_group groups by
 // their maximum score and keep topk_group of them; take the top_k experts of
 // the kept groups by score (ties to the lower index); weights are the scores,
-// divided by (sum + 1e-9) when norm is set.
+// divided by (sum + 1e-9) when norm is set.  The scores stay in registers:
+// every split's partial logit is loaded at once and the splits are added in
+// order; a group is kept when fewer than topk_group groups rank above it (a
+// larger maximum, or an equal one at a lower index: the order of picking the
+// best remaining group topk_group times); the top_k rounds are wave
+// reductions.
 __global__ __launch_bounds__(64) void route_select_kernel(const float *__restrict__ part, int M, int ksplit, int E,
                                                           int n_group, int topk_group, int top_k, int norm,
                                                           int64_t *__restrict__ idx_out, float *__restrict__ w_out) {
-  __shared__ float sc[ROUTE_MAX_E];
-  __shared__ float gmax[64];
-  __shared__ int keep[64];
+  __shared__ int gmax[64];  // group maxima as the bits of non-negative floats (ordered like the values)
   const int lane = threadIdx.x, m = blockIdx.x;
-  for (int e = lane; e < E; e += 64) {
-    float l = part[(size_t)m * E + e];
-    for (int z = 1; z < ksplit; ++z) l += part[((size_t)z * M + m) * E + e];
-    sc[e] = 1.f / (1.f + expf(-l));
-  }
-  __syncthreads();
   const int gs = E / n_group;
+  float sc[ROUTE_EPL];
+#pragma unroll
+  for (int i = 0; i < ROUTE_EPL; ++i) {
+    const int e = lane + 64 * i;
+    float v[ROUTE_MAX_Z];
+#pragma unroll
+    for (int z = 0; z < ROUTE_MAX_Z; ++z) v[z] = e < E && z < ksplit ? part[((size_t)z * M + m) * E + e] : 0.f;
+    float l = v[0];
+#pragma unroll
+    for (int z = 1; z < ROUTE_MAX_Z; ++z)
+      if (z < ksplit) l += v[z];
+    sc[i] = e < E ? 1.f / (1.f + expf(-l)) : -4.f;  // -4: below every candidate and the initial best
+  }
+  if (lane < n_group) gmax[lane] = 0;  // +0.0f: every score is >= 0
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < ROUTE_EPL; ++i) {
+    const int e = lane + 64 * i;
+    if (e < E) atomicMax(&gmax[e / gs], __float_as_int(sc[i]));
+  }
+  __syncthreads();
+  bool keep_g = false;
   if (lane < n_group) {
-    float v = sc[lane * gs];
-    for (int i = 1; i < gs; ++i) v = fmaxf(v, sc[lane * gs + i]);
-    gmax[lane] = v;
-    keep[lane] = 0;
-  }
-  __syncthreads();
-  if (lane == 0) {
-    for (int t = 0; t < topk_group; ++t) {
-      int best = -1;
-      for (int g = 0; g < n_group; ++g)
-        if (!keep[g] && (best < 0 || gmax[g] > gmax[best])) best = g;
-      keep[best] = 1;
+    const float gv = __int_as_float(gmax[lane]);
+    int rank = 0;
+    for (int g = 0; g < n_group; ++g) {
+      const float ov = __int_as_float(gmax[g]);
+      rank += ov > gv || (ov == gv && g < lane);
     }
+    keep_g = rank < topk_group;
   }
-  __syncthreads();
+  const uint64_t keep = __ballot(keep_g);
   // candidate scores: experts of dropped groups take part as 0.0 (the
   // reference's masked_scores), chosen ones are removed as -1
-  for (int e = lane; e < E; e += 64)
-    if (!keep[e / gs]) sc[e] = 0.f;
-  __syncthreads();
-  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < ROUTE_EPL; ++i) {
+    const int e = lane + 64 * i;
+    if (e < E && !((keep >> (e / gs)) & 1)) sc[i] = 0.f;
+  }
+  float sum = 0.f, my_w = 0.f;
+  int my_idx = 0;
   for (int t = 0; t < top_k; ++t) {
     float bv = -2.f;
     int bi = E;
-    for (int e = lane; e < E; e += 64) {
-      const float v = sc[e];
-      if (v > bv) { bv = v; bi = e; }  // ascending e per lane: ties keep the lower index
-    }
+#pragma unroll
+    for (int i = 0; i < ROUTE_EPL; ++i)
+      if (sc[i] > bv) {  // ascending e per lane: ties keep the lower index
+        bv = sc[i];
+        bi = lane + 64 * i;
+      }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const float ov = __shfl_xor(bv, o, 64);
       const int oi = __shfl_xor(bi, o, 64);
       if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
     }
-    if (lane == 0) {
-      idx_out[(size_t)m * top_k + t] = bi;
-      w_out[(size_t)m * top_k + t] = bv;
-      sc[bi] = -1.f;
+#pragma unroll
+    for (int i = 0; i < ROUTE_EPL; ++i)
+      if (lane + 64 * i == bi) sc[i] = -1.f;
+    if (lane == t) {
+      my_idx = bi;
+      my_w = bv;
     }
     sum += bv;
-    __syncthreads();
   }
-  if (norm && lane < top_k) {
-    const float d = sum + 1e-9f;
-    w_out[(size_t)m * top_k + lane] = w_out[(size_t)m * top_k + lane] / d;
+  if (lane < top_k) {
+    idx_out[(size_t)m * top_k + lane] = my_idx;
+    w_out[(size_t)m * top_k + lane] = norm ? my_w / (sum + 1e-9f) : my_w;
   }
 }
 
@@ -344,7 +365,7 @@ extern "C" {
 // K splits of the router logits: about 128 workgroups for decode-sized batches
 static int route_ksplit(int64_t m, int64_t n_experts) {
   const int64_t tiles = ((n_experts + 15) / 16) * ((m + 15) / 16);
-  return (int)std::max<int64_t>(1, std::min<int64_t>(8, 128 / std::max<int64_t>(tiles, 1)));
+  return (int)std::max<int64_t>(1, std::min<int64_t>(ROUTE_MAX_Z, 128 / std::max<int64_t>(tiles, 1)));
 }
 
 size_t amla_moe_route_workspace_bytes(int64_t m, int64_t n_experts) {
