@@ -123,6 +123,7 @@ int launch_gemm_sched(const GemvParams &p, const MoeSched &s, int max_entries, h
 // gemm_ws_bytes(M, N, K) bytes, tiles past the last full round of 256
 // workgroups are cut into K parts (fp32 partial sums in split_ws, summed in
 // part order by a finishing kernel); without it every tile takes the whole K.
+constexpr int GEMV_MAX_PARTS = 32;  // K parts of the skinny GEMM (summed by its finishing passes)
 constexpr int GEMM_MAX_PARTS = 8;
 struct GemmSplit {
   int full;        // tiles with the whole K

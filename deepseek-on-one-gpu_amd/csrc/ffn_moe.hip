@@ -49,6 +49,36 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
     h[t] = f2bf(silu_bf16(bf2f(g[t])) * bf2f(u[t]));
 }
 
+// The K-part sums of [gate | up] (fp32, [part][m][2n]) added in part order
+// and rounded to bf16 as gemv_finish stores them, then
+// h[m, j] = bf16( bf16(silu(gate)) * up ): gemv_finish and silu_mul_rows_kernel
+// in one pass.  Thread: 4 consecutive columns of one row.
+__global__ __launch_bounds__(64) void gu_finish_silu_kernel(const float *__restrict__ part, int M, int n, int kparts,
+                                                            uint16_t *__restrict__ h) {
+  const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (i >= (int64_t)M * (n >> 2)) return;
+  const int m = (int)(i / (n >> 2)), j = (int)(i % (n >> 2)) * 4;
+  const size_t N = 2 * (size_t)n;
+  f32x4 g[GEMV_MAX_PARTS], u[GEMV_MAX_PARTS];
+#pragma unroll
+  for (int q = 0; q < GEMV_MAX_PARTS; ++q)
+    if (q < kparts) {
+      const float *row = part + ((size_t)q * M + m) * N;
+      g[q] = *reinterpret_cast<const f32x4 *>(row + j);
+      u[q] = *reinterpret_cast<const f32x4 *>(row + n + j);
+    }
+  f32x4 gs = g[0], us = u[0];
+#pragma unroll
+  for (int q = 1; q < GEMV_MAX_PARTS; ++q)
+    if (q < kparts) {
+      gs += g[q];
+      us += u[q];
+    }
+  u32x2 o = {pack_bf16(silu_bf16(round_bf16(gs.x)) * round_bf16(us.x), silu_bf16(round_bf16(gs.y)) * round_bf16(us.y)),
+             pack_bf16(silu_bf16(round_bf16(gs.z)) * round_bf16(us.z), silu_bf16(round_bf16(gs.w)) * round_bf16(us.w))};
+  *reinterpret_cast<u32x2 *>(h + (size_t)m * n + j) = o;
+}
+
 static int launch_silu_mul(const uint16_t *g, const uint16_t *u, int64_t n, uint16_t *h, hipStream_t st) {
   const int64_t n8 = (aligned16(g) && aligned16(u) && aligned16(h)) ? n / 8 : 0;
   const int64_t work = std::max<int64_t>(n8, n - n8 * 8);
@@ -197,7 +227,17 @@ int amla_swiglu(const void *x, int64_t m, int64_t k, const void *gate_w, const f
     rc = launch_gemm(a, GEMV_PLAIN, st);
     if (!rc) rc = launch_gemm(b, GEMV_PLAIN, st);
   } else {
-    rc = launch_gemv(p, GEMV_PLAIN, plan_gemv((int)m, (int)(2 * n), (int)k), st);
+    const GemvPlan pl = plan_gemv((int)m, (int)(2 * n), (int)k);
+    if (pl.kparts > 1) {
+      // the K-part finish and silu * up in one pass (n % 128 == 0)
+      if ((rc = launch_gemv(p, GEMV_PLAIN, pl, st, false))) return rc;
+      const int64_t items = m * (n / 4);
+      gu_finish_silu_kernel<<<(unsigned)((items + 63) / 64), 64, 0, st>>>(part, (int)m, (int)n, pl.kparts, h);
+      if ((rc = check_launch("swiglu gate|up finish + silu_mul"))) return rc;
+      return fp8_linear_into(h, (int)m, (int)n, static_cast<const uint8_t *>(down_w), down_s, (int)k,
+                             static_cast<uint16_t *>(y), part, st);
+    }
+    rc = launch_gemv(p, GEMV_PLAIN, pl, st);
   }
   if (rc) return rc;
   silu_mul_rows_kernel<<<dim3((unsigned)std::max<int64_t>(1, std::min<int64_t>(n / 8 / 256, 16)),

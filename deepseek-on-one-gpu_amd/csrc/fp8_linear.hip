@@ -163,7 +163,6 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
 // MFMA K order inside a 128-wide block: lane (row l%16, group g = l/16) holds
 // weight chunks g and 4+g (bytes 16g.., 64+16g..) = K slots 0-7, 8-15 (first
 // chunk) and 64.., 72.. (second); x fragments follow the same order.
-constexpr int GEMV_MAX_PARTS = 32;  // K parts summed by gemv_finish
 constexpr int GEMV_MAX_RG = 16;     // 16-row tiles per workgroup
 constexpr int GEMV_KPB = 16;        // max 128-wide blocks per K part (2 KB of a row)
 // Weight tiles resident: nbuf (current + nbuf - 1 in flight).  Measured on
