@@ -195,9 +195,11 @@ AMLA_DEV int split_tile(int nb, int s, int j) { return (int)(((int64_t)j * nb) /
 // plus two (cos, sin) table blocks (tiles of even / odd index), copied two
 // tiles ahead like the rows, and the tile's probabilities P^T of all heads.
 constexpr int NST = 3;
-// 1184 B rows (592 bf16): the score fragment reads (32 lanes: 16 rows x two
-// 16 B chunks) and the transpose reads (64 lanes: 16 rows x 4 x 8 B) both land
-// on distinct banks of the 512 B bank window (row stride = 74 x 16 B = 148 x 8 B)
+// 1184 B rows (592 bf16).  A 16-byte LDS read is served 16 consecutive lanes
+// per pass, free of bank conflicts when their addresses differ in bits 4-7
+// (measured on MI355X), so the score fragment reads (16 rows of one chunk per
+// pass, stride 74 x 16 B) pair rows r and r + 8; an odd pitch (1168 B) removes
+// that and measured the same, the second passes being hidden in this kernel
 constexpr int KROW = QKD + 16;
 constexpr int K_BYTES = TT * KROW * 2;
 constexpr int RAW_BYTES = TT * ROPE * 2;

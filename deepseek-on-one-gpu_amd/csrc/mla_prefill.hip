@@ -520,12 +520,14 @@ constexpr int F_RPW = F_KT / F_NW;                 // key rows each wave copies 
 constexpr int F_NST = 3;                           // LDS stages (copies run two tiles ahead)
 // one stage: k_nope as two arrays of 128 B half-rows (dims 0-63 of every key,
 // then dims 64-127), rope-key rows (128 B), values as two arrays of 128 B
-// half-rows.  LDS has 128 banks of 4 B (a 512 B window = four half-rows): a
-// 16-byte read serves 32 lanes per pass and a transpose read 64 lanes, so the
-// chunks are swizzled per row (chunk c of a k_nope / rope half-row r at
-// c ^ ((r >> 2) & 7), 64-byte segment g of a value half-row at g ^ ((r >> 2) & 1))
-// and the 32 key rows of a fragment read, and the 8 x 64 B of a transpose
-// read, each cover the window once.
+// half-rows.  A 16-byte LDS read is served 16 consecutive lanes per pass, free
+// of bank conflicts when their addresses differ in bits 4-7 (measured on
+// MI355X: any two of the 16 equal there cost a second pass); a transpose read
+// serves 64 lanes over a 512 B window.  So chunk c of a k_nope / rope half-row
+// r sits at c ^ ((r >> 1) & 7) (the 16 key rows of a fragment read pass: two
+// parities of the row x eight slots), and the 64-byte segment g of a value
+// half-row at g ^ ((r >> 2) & 1) (the 8 x 64 B of a transpose read cover the
+// window once).
 constexpr int F_HALF = F_KT * 128;                 // one array of half-rows
 constexpr int F_NOPE = 0, F_RPE = 2 * F_HALF, F_VAL = 3 * F_HALF;
 constexpr int F_STAGE = F_VAL + 2 * F_HALF;        // 40 KB
@@ -556,7 +558,7 @@ struct FlashLane {
 };
 
 // chunk of a k_nope / rope half-row slot c8 of copy row r8 (key row 8 w + r8) holds
-AMLA_DEV int flash_kchunk(int wave, int lane) { return (lane & 7) ^ ((2 * wave + (lane >> 5)) & 7); }
+AMLA_DEV int flash_kchunk(int wave, int lane) { return (lane & 7) ^ ((4 * wave + (lane >> 4)) & 7); }
 // chunk of a value half-row slot c8 holds (the 64-byte segment moves with bit 2 of the row)
 AMLA_DEV int flash_vchunk(int lane) { return (lane & 7) ^ (4 * ((lane >> 5) & 1)); }
 
@@ -681,7 +683,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
 
   // per-lane LDS offsets.  K fragment (A of S^T): key row 32 kg + j32, chunk
   // 2 ks + hh of half-row array ks / 4 (arrays 0, 1: k_nope; 2: rope), at slot
-  // (2 ks + hh) ^ ((j32 >> 2) & 7).  V^T by ds_read_b64_tr_b16: in a 16-lane
+  // (2 ks + hh) ^ ((j32 >> 1) & 7).  V^T by ds_read_b64_tr_b16: in a 16-lane
   // group g, lane L addresses value row t + L/4 and columns c0 + 4 (L%4) .. +3
   // with c0 = 32 vt + 16 (g & 1), and receives column c0 + L of rows t .. t+3;
   // rows t = 8i + 4 hh, so the segment of column block vt sits at (vt & 1) ^ hh.
@@ -689,7 +691,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
   const int vrow = L16 >> 2;
   int koff[4];
 #pragma unroll
-  for (int k4 = 0; k4 < 4; ++k4) koff[k4] = F_NOPE + j32 * 128 + 16 * ((2 * k4 + hh) ^ ((j32 >> 2) & 7));
+  for (int k4 = 0; k4 < 4; ++k4) koff[k4] = F_NOPE + j32 * 128 + 16 * ((2 * k4 + hh) ^ ((j32 >> 1) & 7));
   int voff[2];  // vt even / odd
 #pragma unroll
   for (int par = 0; par < 2; ++par)
