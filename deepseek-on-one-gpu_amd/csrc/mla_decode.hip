@@ -1116,16 +1116,15 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   pa.ckv_bstride = (int64_t)a->max_seq * LORA; pa.kpe_bstride = (int64_t)a->max_seq * ROPE;
   pa.kv_lora = LORA; pa.rope = ROPE; pa.pos = a->positions; pa.seq_len = 1; pa.max_rows = a->max_seq;
   pa.part = reinterpret_cast<float *>(ws + L.lin);
+  if ((rc = launch_gemv(pa, GEMV_QKVA, L.pa, st, false))) return rc;  // K parts are summed below
   // 2. q_a_layernorm (inference/ops.py:130): fused into the K-part finish, or
   //    a row norm in place when the GEMV needs no finishing pass
   mark(ev, 1, st);
   const uint16_t *gq = reinterpret_cast<const uint16_t *>(a->gamma_q);
   if (L.pa.kparts > 1) {
-    if ((rc = launch_gemv(pa, GEMV_QKVA, L.pa, st, false))) return rc;
     if ((rc = launch_qkva_finish_norm(pa, L.pa.kparts, gq, a->eps, st))) return rc;
-  } else {
-    if ((rc = launch_gemv(pa, GEMV_QKVA, L.pa, st))) return rc;
-    if ((rc = launch_rms_norm(qa, B, a->q_lora, a->q_lora, gq, a->eps, qa, a->q_lora, st))) return rc;
+  } else if ((rc = launch_rms_norm(qa, B, a->q_lora, a->q_lora, gq, a->eps, qa, a->q_lora, st))) {
+    return rc;
   }
 
   // 3. q = q_a_norm W_qb^T, RoPE on q_pe at pos[b] (inference/ops.py:131-133, :156)

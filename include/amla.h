@@ -129,8 +129,9 @@ int amla_mla_decode(const amla_mla_args *args, void *stream);
 
 /* Measurement hook with no counterpart in the reference: amla_mla_decode that
  * also records events[i] (hipEvent_t) on `stream` before each of its 7 stages
- * (q_a|kv_a projection, q_a norm, q_b projection + RoPE, W_UK absorption,
- * attention, split merge + W_UV, o_proj) and events[7] after the last, so a
+ * (q_a|kv_a projection, preceded by the input RMSNorm in layer mode; q_a norm
+ * with the projection's K-part finish; q_b projection + RoPE; W_UK absorption;
+ * attention; split merge + W_UV; o_proj) and events[7] after the last, so a
  * benchmark can time each kernel on the stream it runs on. */
 int amla_mla_decode_profiled(const amla_mla_args *args, void *stream, void *const *events);
 
