@@ -141,3 +141,30 @@ def test_sample_in_a_hip_graph():
             graph.replay()
             torch.cuda.synchronize()
             assert torch.equal(static_out, eager), (temp, r)
+
+
+def test_sample_with_masked_tokens():
+    """Logits set to -inf (banned tokens) have probability 0: never drawn, by the chunked and the
+    one-workgroup kernels alike (the same token), also when top_p >= 1 keeps every token and when
+    a single token is left; a near-zero temperature draws the argmax."""
+    print("[case] sample with -inf logits", flush=True)
+    g = torch.Generator().manual_seed(33)
+    rows, n = 8, 129280
+    lg_cpu = torch.randn(rows, n, generator=g) * 2
+    lg_cpu[torch.rand(rows, n, generator=g) < 0.5] = -float("inf")
+    lg_cpu[3, :] = -float("inf")
+    lg_cpu[3, 77777] = 1.5                      # one token left
+    lg = lg_cpu.to(DEV)
+    finite = torch.isfinite(lg_cpu)
+    for temp, top_p, seed in ((1.0, 0.9, 1), (1.0, 1.0, 2), (0.7, 5.0, 3), (1.0, 0.0, 4)):
+        got = ops.sample(lg, temp, top_p, seed=seed)
+        want = _one_workgroup_per_row(lg, temp, top_p, seed)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (temp, top_p)
+        got = got.cpu()
+        assert finite[torch.arange(rows), got].all(), (temp, top_p)
+        assert got[3].item() == 77777
+        kept, _ = H.nucleus(lg_cpu, temp, top_p)
+        assert kept[torch.arange(rows), got].all(), (temp, top_p)
+    cold = ops.sample(lg, 1e-3, 0.9, seed=5).cpu()
+    assert cold.tolist() == H.greedy(lg_cpu).tolist()
