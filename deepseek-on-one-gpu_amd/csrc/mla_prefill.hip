@@ -880,17 +880,20 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
   for (int j = 0; j < ntiles; ++j) {
     const int g = 2 * j;
     // ---- group g (even): S_{g+1} (same tile, half 1) || exp of scA; PV_g || max of scB.
-    // The score steps run at raised wave priority: the other wave of the SIMD
-    // then fills their gaps with its own PV and softmax work (flash 882 -> 865
-    // us at S = 4096; priority around the PV steps, or fixed per wave, gained
-    // nothing)
-    __builtin_amdgcn_s_setprio(1);
+    // Wave priority by phase: score steps 2, PV steps 1, the rest (max update,
+    // waits, barrier) 0, so the two waves of a SIMD drift apart and one fills
+    // the other's gaps (flash 882 -> 865 us at S = 4096 with the score steps
+    // raised, a further 1.3 % with the PV steps between; a fixed priority per
+    // wave gained nothing, the prologue's score step raised lost 1.5 %)
+    __builtin_amdgcn_s_setprio(2);
     FL_S(scB, 1, scA, 1, -1, fsm);
     __builtin_amdgcn_s_setprio(0);
     FL_VBASE(stg);
     {
       const bool diag = 32 * (g + 1) + 31 > pos0 + s_wave;
+      __builtin_amdgcn_s_setprio(1);
       FL_PV(0, scB, g + 1, 1, diag);
+      __builtin_amdgcn_s_setprio(0);
     }
     FL_MAXFIN();
     // ---- group g+1 (odd): S_{g+2} (tile j+1, half 0) || exp of scB; PV_{g+1} || max of scA.
@@ -910,12 +913,14 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
       }
     }
     FL_KBASE(stn);
-    __builtin_amdgcn_s_setprio(1);
+    __builtin_amdgcn_s_setprio(2);
     FL_S(scA, 0, scB, 1, dmat, fsm + (stn == F_NST - 1 ? 0 : stn + 1) * F_STAGE);
     __builtin_amdgcn_s_setprio(0);
     {
       const bool diag = 32 * (g + 2) + 31 > pos0 + s_wave;
+      __builtin_amdgcn_s_setprio(1);
       FL_PV(1, scA, g + 2, 1, diag);
+      __builtin_amdgcn_s_setprio(0);
     }
     if (more) FL_MAXFIN();
     stg = stn;
