@@ -68,6 +68,12 @@ def test_null_and_bad_arguments_fail_before_launch():
     a.workspace_bytes = 16
     assert L.amla_mla_decode(ctypes.byref(a), None) == -2
     assert b"workspace" in L.amla_last_error()
+    # the profiling hook checks its eight events before anything else
+    assert L.amla_mla_decode_profiled(ctypes.byref(a), None, None) == -1
+    evs = (ctypes.c_void_p * 8)(*([p] * 8))
+    evs[3] = None
+    assert L.amla_mla_decode_profiled(ctypes.byref(a), None, evs) == -1
+    assert b"null event 3" in L.amla_last_error()
     a.seq_len = 2
     assert L.amla_mla_decode(ctypes.byref(a), None) == -1      # decode needs S == 1
     # fp8_linear shape constraints
