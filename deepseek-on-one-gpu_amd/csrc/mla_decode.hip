@@ -1021,11 +1021,14 @@ static DecodeLayout decode_layout(const amla_mla_args &a) {
   L.pb = plan_gemv(B, a.heads * HD, a.q_lora);
   L.po = plan_gemv(B, a.hidden, a.heads * a.v_dim);
   // splits over the batch: one per CU, at least two tiles each for the
-  // longest possible context; the plan itself is made on the device from the
-  // positions (seq_splits), so a ragged batch is balanced by its total tokens
+  // longest possible context, or one tile each while the batch holds at most
+  // 64 tiles (a split's fixed cost then outweighs its second tile); the plan
+  // itself is made on the device from the positions (seq_splits), so a ragged
+  // batch is balanced by its total tokens
   const int maxT = mla_context_bound(a);
   const int ntiles = (maxT + TT - 1) / TT;
-  L.units = std::max(1, std::min(256, B * std::max(1, ntiles / 2)));
+  const int bt = B * ntiles;
+  L.units = std::max(1, std::min(256, bt <= 64 ? bt : B * std::max(1, ntiles / 2)));
   L.slots = L.units + B;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes, 256); return o; };

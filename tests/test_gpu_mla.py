@@ -131,14 +131,16 @@ def test_decode_split_count_does_not_matter():
 def test_decode_overflow_recompute():
     """A cached rope key 500x larger than the rest, in the second tile of its
     split: heads whose score jumps more than 2^64 above the split's reference
-    max take the exact recomputation path of the combine kernel."""
+    max take the exact recomputation path of the combine kernel.  Context 4201
+    is 132 tiles of 32 rows in 66 splits of two tiles; row 1510 is in tile 47,
+    the second of split 23."""
     tag = "overflow"
     lay = _layer("mla/" + tag)
-    pos = 2000
+    pos = 4200
     hidden = synth.make_hidden(R1, 1, 1, tag)
-    ckv, kpe = synth.make_kv_cache(R1, 1, 2008, pos, tag)
+    ckv, kpe = synth.make_kv_cache(R1, 1, 4208, pos, tag)
     kpe[0, 1510] = (kpe[0, 1510].float() * 500).to(torch.bfloat16)
-    tab = _rope(2008)
+    tab = _rope(4208)
     want = R.mla_attention(hidden, lay.attn_weights, (ckv.clone(), kpe.clone()), pos, tab, R1)
     got = ops.mla_attention(hidden.to(DEV), _to_dev(lay.attn_weights), (ckv.to(DEV), kpe.to(DEV)), pos, tab.to(DEV), R1)
     assert_parity(got.cpu(), want, "overflow recompute")
