@@ -13,19 +13,20 @@
 // the rotation of the raw cached rope key (ops.py:158-159), both applied on the
 // fly, once per row instead of once per row and head.
 //
-// Launch sequence per layer (batch <= 16):
-//   gemv  QKVA : q_a | kv_a from hidden in one pass over K, the input RMSNorm
-//                (layer mode) fused into the x staging; kv_a straight into
-//                the caches, q_a (bf16) to the workspace
-//   gemv  QROPE: q = rms_norm(q_a) W_qb^T with q_a_layernorm fused into the x
-//                staging; RoPE on the q_pe rows at pos[b]
-// (larger batches: rms_norm, K-part q_a | kv_a GEMV, a finish with the q_a
-// norm fused, then q_b)
-//   absorb     : qt = gamma_kv * W_UK^T q_nope  -> qbuf (B, H, 576) with q_pe,
-//                stored in attn_kernel's fragment order
-//   attn       : split over context, online softmax, bf16 partial O, (m, l)
+// Launch sequence per layer:
+//   rms_norm   : input RMSNorm of hidden (layer mode only)
+//   gemv  QKVA : q_a | kv_a in K parts (fp32 partial sums)
+//   finish     : sums the K parts, writes the new cache row (raw latent + raw
+//                k_pe) and q_a_layernorm(q_a) (a row norm in place when the
+//                GEMV needs no K parts)
+//   gemv  QROPE: q = q_a_norm W_qb^T, RoPE on the q_pe rows at pos[b]
+//   absorb     : qt = gamma_kv * W_UK^T q_nope -> qbuf (B, H, 576) with q_pe,
+//                stored in attn_kernel's fragment order; one more workgroup
+//                makes the split plan from the positions
+//   attn       : split over context, fixed-reference softmax, bf16 partial O, (m, l)
 //   combine_uv : merge splits, gamma_kv, W_UV -> (B, H*128) bf16
-//   gemv  PLAIN/RESID : wo
+//   gemv  PLAIN/RESID : wo (+ residual), then its K-part finish
+#include <limits.h>
 #include <math.h>
 
 #include <mutex>
@@ -53,10 +54,118 @@ AMLA_DEV size_t qfrag_index(int b, int h, int c) {
   return ((((size_t)b * (HEADS / 16) + (h >> 4)) * (QKD / 32) + (c >> 5)) * 64 + lane) * 8 + (c & 7);
 }
 
+// ---------------------------------------------------------------- split plan
+
+// Split plan of a decode batch, made on the device from the positions (no
+// host synchronisation):
+//   sequence b has N_b = ceil(T_b / TT) tiles (T_b = min(pos[b] + 1, tmax));
+//   L is the smallest split length with sum_b ceil(N_b / L) <= units (reached
+//   by L = max N_b at the latest, as batch <= units);
+//   sequence b gets s_b = max(1, ceil(N_b / L)) splits in consecutive slots
+//   first_b = s_0 + .. + s_{b-1}, and split j of b covers tiles
+//   [j N_b / s_b, (j + 1) N_b / s_b), at most L of them.
+// The launch takes as long as its longest split when every split has a CU, so
+// a ragged batch is balanced by its total tokens, not by its longest sequence.
+// A batch whose sequences all have the same tile count n has the plan in
+// closed form (L = ceil(n / floor(units / B)), s_b = ceil(n / L), first_b =
+// b s_b), which the attention and combine launches form themselves.  For any
+// other batch one workgroup of the absorb launch writes the plan to a table
+// that they read (int32): [0] L, [1] sum of s_b, [PLAN_HDR + 2b] first_b and
+// [PLAN_HDR + 2b + 1] s_b (one 8-byte load), [PLAN_HDR + 2B + slot] the
+// sequence of each slot (-1 past the plan).
+constexpr int PLAN_HDR = 4;
+inline size_t plan_ints(int B, int slots) { return PLAN_HDR + 2 * (size_t)B + slots; }
+
+AMLA_DEV int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Smallest and largest tile count of the batch (uniform scalar loads).
+AMLA_DEV int2 batch_tile_range(const int32_t *pos, int tmax, int B) {
+  int lo = INT_MAX, hi = 0;
+  for (int b = 0; b < B; ++b) {
+    const int T = min(pos[b] + 1, tmax);
+    const int n = T > 0 ? ceil_div(T, TT) : 0;
+    lo = min(lo, n);
+    hi = max(hi, n);
+  }
+  return int2{lo, hi};
+}
+
+// Splits per sequence of a batch whose sequences all have n tiles.
+AMLA_DEV int uniform_splits(int n, int units, int B) {
+  return n > 0 ? ceil_div(n, ceil_div(n, units / B)) : 1;
+}
+
+// The table of a batch with unequal tile counts: one 256-thread workgroup,
+// batch <= 64 (the decode limit); lds holds 2 * B + 4 ints.
+AMLA_DEV void build_split_plan(const int32_t *__restrict__ pos, int tmax, int B, int units, int slots,
+                               int32_t *__restrict__ plan, int *lds) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int *nt = lds, *first = lds + B, *sh = lds + 2 * B;
+  if (tid < B) {
+    const int T = min(pos[tid] + 1, tmax);
+    nt[tid] = T > 0 ? ceil_div(T, TT) : 0;
+  }
+  __syncthreads();
+  int N = 0, most = 0;
+  for (int b = 0; b < B; ++b) {
+    N += nt[b];
+    most = max(most, nt[b]);
+  }
+  // smallest L in [lo, hi] that fits: 256 candidates per round, the last one
+  // hi itself (which fits), so each round keeps the interval between two
+  // neighbouring candidates
+  int lo = max(1, ceil_div(N, units)), hi = max(lo, most);
+  while (lo < hi) {
+    const int step = (hi - lo + 254) / 255;
+    const int cand = min(hi, lo + step * tid);
+    int f = 0;
+    for (int b = 0; b < B; ++b) f += ceil_div(nt[b], cand);
+    const unsigned long long fits = __builtin_amdgcn_ballot_w64(f <= units);
+    if (lane == 0) sh[wave] = fits ? wave * 64 + __builtin_ctzll(fits) : 256;
+    __syncthreads();
+    const int k = min(min(sh[0], sh[1]), min(sh[2], sh[3]));
+    __syncthreads();
+    if (k == 0) {
+      hi = lo;
+    } else if (k == 256) {  // not reached while batch <= units
+      lo = hi;
+    } else {
+      const int top = min(hi, lo + step * k);
+      lo = lo + step * (k - 1) + 1;
+      hi = top;
+    }
+  }
+  const int L = lo;
+  if (tid == 0) {
+    int acc = 0;
+    for (int b = 0; b < B; ++b) {
+      const int sb = max(1, ceil_div(nt[b], L));
+      first[b] = acc;
+      plan[PLAN_HDR + 2 * b] = acc;
+      plan[PLAN_HDR + 2 * b + 1] = sb;
+      acc += sb;
+    }
+    plan[0] = L;
+    plan[1] = acc;
+    sh[0] = acc;
+  }
+  __syncthreads();
+  const int total = sh[0];
+  for (int slot = tid; slot < slots; slot += 256) {
+    int b = -1;
+    if (slot < total) {
+      b = 0;
+      while (b + 1 < B && first[b + 1] <= slot) ++b;
+    }
+    plan[PLAN_HDR + 2 * B + slot] = b;
+  }
+}
+
 // ---------------------------------------------------------------- absorb
 
 // One workgroup per (head, 128-column quarter of the latent, group of 8
-// sequences).  Thread (dg, cc) sums rows 8*dg .. 8*dg+7 of W_UK[h] (eight
+// sequences), and workgroup (HEADS, 0, 0) writes the split plan table of a
+// batch with unequal tile counts.  Thread (dg, cc) sums rows 8*dg .. 8*dg+7 of W_UK[h] (eight
 // independent 8-byte loads in flight) for 8 latent columns; the 16 row groups
 // reduce through LDS.  W_UK[h] = kv_b rows h*256 .. h*256+127 lie in one
 // 128-row scale block.
@@ -64,16 +173,25 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
                                                      const uint8_t *__restrict__ wkvb,
                                                      const float *__restrict__ skvb,
                                                      const uint16_t *__restrict__ gamma,
-                                                     int B, uint16_t *__restrict__ qbuf) {
+                                                     int B, uint16_t *__restrict__ qbuf,
+                                                     const int32_t *__restrict__ pos, int tmax, int units,
+                                                     int slots, int32_t *__restrict__ plan) {
   constexpr int BB = 8;
+  __shared__ float qn[BB][NOPE];
+  __shared__ f32x4 red[16][BB][16][2];
+  if (blockIdx.x >= HEADS) {
+    if (blockIdx.x == HEADS && blockIdx.y == 0 && blockIdx.z == 0) {
+      const int2 r = batch_tile_range(pos, tmax, B);
+      if (r.x != r.y) build_split_plan(pos, tmax, B, units, slots, plan, reinterpret_cast<int *>(&red[0][0][0][0]));
+    }
+    return;
+  }
   const int h = blockIdx.x, quarter = blockIdx.y;
   const int b0 = blockIdx.z * BB;
   const int nb = min(BB, B - b0);
   const int tid = threadIdx.x;
   const int cc = tid & 15, dg = tid >> 4;
   const int c0 = quarter * 128 + cc * 8;  // this thread's 8 latent columns
-  __shared__ float qn[BB][NOPE];
-  __shared__ f32x4 red[16][BB][16][2];
   const uint8_t *wp = wkvb + ((size_t)h * (NOPE + VD) + dg * 8) * LORA + c0;
   u32x2 raw[8];
 #pragma unroll
@@ -142,6 +260,7 @@ struct AttnParams {
   int tmax;                          // context bound (rows of cache and rope table that may be read)
   int units;         // splits shared out over the batch (the grid has units + batch workgroups)
   int batch;
+  const int32_t *plan;  // split plan (build_split_plan)
   float scale_log2;  // softmax scale * log2(e)
   float eps;
   uint16_t *part_o;  // (units + B, H, 512) bf16 by split slot: sum_t p_t r_t c_t, p relative to the split's reference max
@@ -149,15 +268,7 @@ struct AttnParams {
                    // (split, head) whose scores overflowed the reference (recomputed by the combine)
 };
 
-// Split plan of a decode batch, computed from the device positions by every
-// attention workgroup and by the combine (no host synchronisation, the same
-// integers everywhere): sequence b has N_b = ceil(T_b / TT) tiles
-// (T_b = min(pos[b] + 1, tmax)) and gets s_b = max(1, floor(units * N_b / N))
-// splits (N = sum of N_b), in consecutive slots first_b = s_0 + .. + s_{b-1};
-// split j of b covers tiles [j N_b / s_b, (j + 1) N_b / s_b).  So every split
-// holds about N / units tiles whatever the spread of contexts (a ragged batch
-// is balanced by its total tokens, not by its longest sequence), and
-// sum s_b <= units + B slots.
+// A sequence's splits in the plan: first slot, count, and its tile count.
 struct SeqSplits {
   int first, count, ntiles;
 };
@@ -167,22 +278,14 @@ AMLA_DEV int seq_tiles(const AttnParams &p, int b) {
   return T > 0 ? (T + TT - 1) / TT : 0;
 }
 
-AMLA_DEV int total_tiles(const AttnParams &p) {
-  int n = 0;
-  for (int b = 0; b < p.batch; ++b) n += seq_tiles(p, b);
-  return n;
-}
-
-AMLA_DEV int seq_split_count(const AttnParams &p, int nb, int N) {
-  return N > 0 ? max(1, (int)(((int64_t)p.units * nb) / N)) : 1;
-}
-
 AMLA_DEV SeqSplits seq_splits(const AttnParams &p, int b) {
-  const int N = total_tiles(p);
-  int first = 0;
-  for (int c = 0; c < b; ++c) first += seq_split_count(p, seq_tiles(p, c), N);
-  const int nb = seq_tiles(p, b);
-  return SeqSplits{first, seq_split_count(p, nb, N), nb};
+  const int2 r = batch_tile_range(p.pos, p.tmax, p.batch);
+  if (r.x == r.y) {
+    const int s = uniform_splits(r.x, p.units, p.batch);
+    return SeqSplits{b * s, s, r.x};
+  }
+  const int2 fs = *reinterpret_cast<const int2 *>(p.plan + PLAN_HDR + 2 * b);
+  return SeqSplits{fs.x, fs.y, seq_tiles(p, b)};
 }
 
 // tile range of split j of a sequence with nb tiles in s splits
@@ -371,24 +474,21 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   const int li = lane & 15, lg = lane >> 4;
   // this workgroup's (sequence, split) from the batch's split plan; slots past
   // the plan have no work
-  int b = 0, split = 0, nb = 0, ns = 1;
-  {
-    const int N = total_tiles(p);
-    int first = 0;
-    b = -1;
-    for (int c = 0; c < p.batch; ++c) {
-      const int t = seq_tiles(p, c);
-      const int sc = seq_split_count(p, t, N);
-      if (b < 0 && slot < first + sc) {
-        b = c;
-        split = slot - first;
-        nb = t;
-        ns = sc;
-      }
-      first += sc;
-    }
+  int b, split, ns;
+  const int2 range = batch_tile_range(p.pos, p.tmax, p.batch);
+  if (range.x == range.y) {
+    ns = uniform_splits(range.x, p.units, p.batch);
+    b = slot / ns;
+    split = slot % ns;
+    if (b >= p.batch) return;
+  } else {
+    b = __builtin_amdgcn_readfirstlane(p.plan[PLAN_HDR + 2 * p.batch + slot]);
     if (b < 0) return;
+    const int2 fs = *reinterpret_cast<const int2 *>(p.plan + PLAN_HDR + 2 * b);
+    split = slot - __builtin_amdgcn_readfirstlane(fs.x);
+    ns = __builtin_amdgcn_readfirstlane(fs.y);
   }
+  const int nb = seq_tiles(p, b);
   const int T = min(p.pos[b] + 1, p.tmax);
   const int tb = split_tile(nb, ns, split);
   const int te = split_tile(nb, ns, split + 1);
@@ -882,8 +982,7 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
   // ---- fast merge: wave w, sequence b0 + w.  The first 16 splits' partial
   // rows are in flight while the max and the weights are formed.
   if (wave < nb) {
-    const int b = b0 + wave;
-    const SeqSplits sp = seq_splits(ap, b);
+    const SeqSplits sp = seq_splits(ap, b0 + wave);
     const size_t base = (size_t)sp.first * HEADS + h;
     const u32x4 *po = reinterpret_cast<const u32x4 *>(ap.part_o + base * LORA) + lane;
     const size_t stride = (size_t)HEADS * LORA / 8;
@@ -1008,9 +1107,9 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
 // ---------------------------------------------------------------- orchestration
 
 struct DecodeLayout {
-  size_t xn, qa, q, qbuf, part_ml, part_o, attn, lin, total;
+  size_t plan, xn, qa, q, qbuf, part_ml, part_o, attn, lin, total;
   GemvPlan pa, pb, po;
-  int units, slots;  // split plan size (device side: seq_splits) and partial slots
+  int units, slots;  // split budget (build_split_plan) and partial slots
 };
 
 static DecodeLayout decode_layout(const amla_mla_args &a) {
@@ -1023,8 +1122,7 @@ static DecodeLayout decode_layout(const amla_mla_args &a) {
   // splits over the batch: one per CU, at least two tiles each for the
   // longest possible context, or one tile each while the batch holds at most
   // 64 tiles (a split's fixed cost then outweighs its second tile); the plan
-  // itself is made on the device from the positions (seq_splits), so a ragged
-  // batch is balanced by its total tokens
+  // itself is made on the device from the positions (build_split_plan)
   const int maxT = mla_context_bound(a);
   const int ntiles = (maxT + TT - 1) / TT;
   const int bt = B * ntiles;
@@ -1032,6 +1130,7 @@ static DecodeLayout decode_layout(const amla_mla_args &a) {
   L.slots = L.units + B;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes, 256); return o; };
+  L.plan = take(plan_ints(B, L.slots) * 4);  // first: a test reads the table back
   L.xn = take((size_t)B * a.hidden * 2);
   L.qa = take((size_t)B * a.q_lora * 2);
   L.q = take((size_t)B * a.heads * HD * 2);
@@ -1144,9 +1243,15 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
 
   // 4. absorb W_UK into the query
   mark(ev, 3, st);
-  absorb_kernel<<<dim3(HEADS, LORA / 128, (B + 7) / 8), 256, 0, st>>>(
+  int32_t *plan = reinterpret_cast<int32_t *>(ws + L.plan);
+  const int tmax = mla_context_bound(*a);
+  // x = HEADS + 8: workgroup (HEADS, 0, 0) writes the plan table, the others
+  // past HEADS return at once; a row length that is a multiple of 8 keeps the
+  // quarters of head h on one XCD (workgroup i runs on XCD i mod 8), where
+  // they share its query rows in L2
+  absorb_kernel<<<dim3(HEADS + 8, LORA / 128, (B + 7) / 8), 256, 0, st>>>(
       q, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv),
-      B, qbuf);
+      B, qbuf, a->positions, tmax, L.units, L.slots, plan);
   if ((rc = check_launch("mla absorb"))) return rc;
 
   // 5. attention over the latent cache, split over context
@@ -1156,8 +1261,8 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   ap.ckv = reinterpret_cast<const uint16_t *>(a->ckv_cache);
   ap.kpe = reinterpret_cast<const uint16_t *>(a->kpe_cache);
   ap.ckv_bstride = (int64_t)a->max_seq * LORA; ap.kpe_bstride = (int64_t)a->max_seq * ROPE;
-  ap.rope_table = a->rope_table; ap.pos = a->positions; ap.tmax = mla_context_bound(*a);
-  ap.units = L.units; ap.batch = B;
+  ap.rope_table = a->rope_table; ap.pos = a->positions; ap.tmax = tmax;
+  ap.units = L.units; ap.batch = B; ap.plan = plan;
   ap.scale_log2 = a->softmax_scale * 1.4426950408889634f;
   ap.eps = a->eps;
   ap.part_o = reinterpret_cast<uint16_t *>(ws + L.part_o);

@@ -3,13 +3,15 @@
 Full DeepSeek-R1 MLA dimensions; the oracle (oracle/ref_ops.py, torch on the
 CPU with the reference's rounding points) runs on identical seeded inputs.
 """
+import ctypes
 import functools
 
 import pytest
 import torch
 
 from oracle import ref_ops as R
-from amla import ops, synth
+from amla import ops, synth, torch_ops
+from amla._lib import lib
 from amla.config import DeepSeekConfig
 from _tol import assert_parity, assert_bf16_ulps
 
@@ -236,3 +238,58 @@ def test_bad_arguments_raise_before_launch():
     bad["o_proj"] = (aw["o_proj"][0][:, :8192].contiguous(), aw["o_proj"][1])
     with pytest.raises(ValueError):
         ops.mla_attention(hidden, bad, (ckv, kpe), 0, tab, R1)
+
+
+def _plan_mirror(lengths, tmax, units, slots):
+    """The decode split plan: the smallest split length L (in 32-row tiles) with
+    sum_b ceil(N_b / L) <= units, s_b = max(1, ceil(N_b / L)) splits per sequence in
+    consecutive slots; the table as the kernels store it (L, sum s_b, two spare ints,
+    (first_b, s_b) pairs, the sequence of each slot), minus the spare ints."""
+    tiles = [(min(t, tmax) + 31) // 32 for t in lengths]
+    fits = lambda L: sum(-(-n // L) for n in tiles) <= units
+    L = next(L for L in range(1, max(tiles) + 1) if fits(L))
+    s = [max(1, -(-n // L)) for n in tiles]
+    first = [sum(s[:b]) for b in range(len(s))]
+    pairs = [v for fk in zip(first, s) for v in fk]
+    slot_seq = [-1] * slots
+    for b, (f, k) in enumerate(zip(first, s)):
+        slot_seq[f:f + k] = [b] * k
+    longest = max(max((j + 1) * n // k - j * n // k for j in range(k)) for n, k in zip(tiles, s))
+    assert longest <= L
+    return [L, sum(s)], pairs + slot_seq
+
+
+@pytest.mark.parametrize("case", ["ragged5", "config3", "short"])
+def test_split_plan_is_the_shortest_longest_split(case):
+    """The split plan table that the absorb launch writes for a batch with unequal tile
+    counts (the first region of the decode workspace) equals the min-max rule above; the
+    attention and the combine read it, so the parity tests check that they agree.
+    Batches of equal tile counts use the same rule in closed form (no table)."""
+    g = torch.Generator().manual_seed(5)
+    if case == "ragged5":
+        lengths, max_seq = [1 + int(v) for v in torch.randint(0, 1600, (5,), generator=g)], 1600
+    elif case == "config3":
+        lengths, max_seq = synth.ragged_lengths(32, 1024, 16384, "config3"), 16384
+    else:
+        lengths, max_seq = [1, 40, 257], 264
+    B = len(lengths)
+    print(f"[case] split plan {case} B={B} max_seq={max_seq}", flush=True)
+    aw = _to_dev(_layer("mla/plan").attn_weights)
+    hidden = synth.make_hidden(R1, B, 1, "plan").to(DEV)
+    ckv = torch.zeros(B, max_seq, 512, dtype=torch.bfloat16, device=DEV)
+    kpe = torch.zeros(B, max_seq, 64, dtype=torch.bfloat16, device=DEV)
+    pos = torch.tensor([t - 1 for t in lengths], dtype=torch.int32)
+    tab = _rope(max_seq).to(DEV)
+    out = torch.empty_like(hidden)
+    operands = ops._mla_operands(hidden, aw, (ckv, kpe), pos.to(DEV), tab, R1)
+    a = torch_ops.fill_mla_args(out=out, **operands)
+    ws = torch.empty(lib().amla_mla_decode_workspace_bytes(a), dtype=torch.uint8, device=DEV)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    assert lib().amla_mla_decode(ctypes.byref(a), torch.cuda.current_stream().cuda_stream) == 0, lib().amla_last_error()
+    torch.cuda.synchronize()
+    ntiles = -(-max_seq // 32)
+    units = min(256, B * ntiles if B * ntiles <= 64 else B * max(1, ntiles // 2))
+    slots = units + B
+    head, table = _plan_mirror(lengths, max_seq, units, slots)
+    got = ws[:4 * (4 + 2 * B + slots)].view(torch.int32).cpu().tolist()
+    assert got[:2] == head and got[4:] == table
