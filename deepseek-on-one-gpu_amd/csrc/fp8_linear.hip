@@ -173,14 +173,17 @@ constexpr int GEMV_KPB = 16;        // max 128-wide blocks per K part (2 KB of a
 // block 16 % faster with 2 or 3 than with 4).
 __host__ __device__ inline int gemv_nbuf(int tile_bytes) { return tile_bytes >= 32 * 1024 ? 3 : 2; }
 
-// LDS: [nbuf][16 rows][ceil4(kpb) * 128] weights | [M][kpb * 256 + 16] x (MT > 1) |
+// LDS: [nbuf][16 rows][ceil4(kpb) * 128] weights | [M][kpb * 256 + 16] x (MT > 2) |
 //      [2][4 waves][MT][64] f32x4 partial tiles | [rg][MT][64] f32x4 results
+// Up to two 16-row tiles of x (M <= 32) are held in registers instead, each
+// wave's fragments loaded once per workgroup (64 VGPRs per tile).
+__host__ __device__ constexpr bool gemv_x_in_registers(int MT) { return MT <= 2; }
 __host__ __device__ inline int gemv_kpb4(int kpb) { return (kpb + 3) & ~3; }
 __host__ __device__ inline int gemv_xrow(int kpb) { return kpb * 256 + 16; }
 
 template <int MT, int MODE>
 AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int kpb) {
-  constexpr bool XREG = MT == 1;
+  constexpr bool XREG = gemv_x_in_registers(MT);
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
@@ -235,19 +238,22 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
     for (int b = 0; b < nbuf - 1; ++b) dma_tile(tile_begin + b, b);
   }
 
-  // MT 1: this wave's x fragments (blocks wave + 4j of the part, row li; rows
-  // >= M are zeros), in the MFMA K order of the weight fragments below
+  // MT <= 2: this wave's x fragments (blocks wave + 4j of the part, rows
+  // 16t + li; rows >= M are zeros), in the MFMA K order of the weight
+  // fragments below
   constexpr int NJ = GEMV_KPB / 4;
-  u32x4 xr[XREG ? NJ : 1][4];
+  u32x4 xr[XREG ? MT : 1][XREG ? NJ : 1][4];
   if constexpr (XREG) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int bl = wave + 4 * j;
-      const bool ok = bl < nbp && li < p.M;
-      const uint16_t *xp = p.x + (size_t)li * p.ldx + (size_t)(kb_begin + bl) * 128 + lg * 16;
+    for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) xr[j][q] = ok ? ldg16(xp + (q & 1) * 8 + (q >> 1) * 64) : u32x4{0, 0, 0, 0};
-    }
+      for (int j = 0; j < NJ; ++j) {
+        const int bl = wave + 4 * j, m = 16 * t + li;
+        const bool ok = bl < nbp && m < p.M;
+        const uint16_t *xp = p.x + (size_t)m * p.ldx + (size_t)(kb_begin + bl) * 128 + lg * 16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xr[t][j][q] = ok ? ldg16(xp + (q & 1) * 8 + (q >> 1) * 64) : u32x4{0, 0, 0, 0};
+      }
   }
 
   if constexpr (!XREG) {
@@ -303,10 +309,10 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
           const int m = t * 16 + li;
           bf16x8 x0, x1, x2, x3;
           if constexpr (XREG) {
-            x0 = as_bf16x8(xr[j][0]);
-            x1 = as_bf16x8(xr[j][1]);
-            x2 = as_bf16x8(xr[j][2]);
-            x3 = as_bf16x8(xr[j][3]);
+            x0 = as_bf16x8(xr[t][j][0]);
+            x1 = as_bf16x8(xr[t][j][1]);
+            x2 = as_bf16x8(xr[t][j][2]);
+            x3 = as_bf16x8(xr[t][j][3]);
           } else if (m < p.M) {
             const uint8_t *xp = xs + m * XROW + bl * 256 + lg * 32;
             x0 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xp));
@@ -379,7 +385,8 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(GemvParams p, GemvGro
 
 size_t gemv_lds_bytes(int M, int MT, int kpb, int rg) {
   const int tile = 16 * gemv_kpb4(kpb) * 128;
-  return (size_t)gemv_nbuf(tile) * tile + (MT == 1 ? 0 : (size_t)M * gemv_xrow(kpb)) + 2 * 4 * MT * 64 * 16 +
+  return (size_t)gemv_nbuf(tile) * tile + (gemv_x_in_registers(MT) ? 0 : (size_t)M * gemv_xrow(kpb)) +
+         2 * 4 * MT * 64 * 16 +
          (size_t)rg * MT * 64 * 16;
 }
 
