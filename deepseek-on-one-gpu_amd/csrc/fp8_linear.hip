@@ -173,17 +173,17 @@ constexpr int GEMV_KPB = 16;        // max 128-wide blocks per K part (2 KB of a
 // block 16 % faster with 2 or 3 than with 4).
 __host__ __device__ inline int gemv_nbuf(int tile_bytes) { return tile_bytes >= 32 * 1024 ? 3 : 2; }
 
-// LDS: [nbuf][16 rows][ceil4(kpb) * 128] weights | [M][kpb * 256 + 16] x (MT > 2) |
+// LDS: [nbuf][16 rows][ceil4(kpb) * 128] weights |
 //      [2][4 waves][MT][64] f32x4 partial tiles | [rg][MT][64] f32x4 results
-// Up to two 16-row tiles of x (M <= 32) are held in registers instead, each
-// wave's fragments loaded once per workgroup (64 VGPRs per tile).
-__host__ __device__ constexpr bool gemv_x_in_registers(int MT) { return MT <= 2; }
+// x is held in registers: each wave's fragments of the MT 16-row tiles,
+// loaded once per workgroup (16 VGPRs per tile and 128-wide block of the
+// wave, at most 128 VGPRs: a K part of up to 16 blocks for MT <= 2, 8 for
+// MT = 4).
+__host__ __device__ constexpr int gemv_kpb_max(int MT) { return MT == 4 ? 8 : GEMV_KPB; }
 __host__ __device__ inline int gemv_kpb4(int kpb) { return (kpb + 3) & ~3; }
-__host__ __device__ inline int gemv_xrow(int kpb) { return kpb * 256 + 16; }
 
 template <int MT, int MODE>
 AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int kpb) {
-  constexpr bool XREG = gemv_x_in_registers(MT);
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
@@ -195,14 +195,12 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
   const int kb_begin = part * kpb;
   const int nbp = min(kpb, KB - kb_begin);  // blocks of this part
   const int nseg = (nbp + 3) >> 2;          // 512 B segments per row
-  const int XROW = gemv_xrow(kpb);
   const int TILE_BYTES = 16 * gemv_kpb4(kpb) * 128;
   const int nbuf = gemv_nbuf(TILE_BYTES);
 
   extern __shared__ __align__(16) uint8_t gsm[];
   uint8_t *const wbuf = gsm;
-  uint8_t *const xs = gsm + nbuf * TILE_BYTES;
-  f32x4 *const red = reinterpret_cast<f32x4 *>(xs + (XREG ? 0 : p.M * XROW));
+  f32x4 *const red = reinterpret_cast<f32x4 *>(gsm + nbuf * TILE_BYTES);
   f32x4 *const done = red + 2 * 4 * MT * 64;
 
   // weight copies of one tile: row pairs i = 2*wave, 2*wave+1, every segment
@@ -238,31 +236,20 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
     for (int b = 0; b < nbuf - 1; ++b) dma_tile(tile_begin + b, b);
   }
 
-  // MT <= 2: this wave's x fragments (blocks wave + 4j of the part, rows
-  // 16t + li; rows >= M are zeros), in the MFMA K order of the weight
-  // fragments below
-  constexpr int NJ = GEMV_KPB / 4;
-  u32x4 xr[XREG ? MT : 1][XREG ? NJ : 1][4];
-  if constexpr (XREG) {
+  // this wave's x fragments (blocks wave + 4j of the part, rows 16t + li;
+  // rows >= M are zeros), in the MFMA K order of the weight fragments below
+  constexpr int NJ = gemv_kpb_max(MT) / 4;
+  u32x4 xr[MT][NJ][4];
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+  for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int bl = wave + 4 * j, m = 16 * t + li;
-        const bool ok = bl < nbp && m < p.M;
-        const uint16_t *xp = p.x + (size_t)m * p.ldx + (size_t)(kb_begin + bl) * 128 + lg * 16;
+    for (int j = 0; j < NJ; ++j) {
+      const int bl = wave + 4 * j, m = 16 * t + li;
+      const bool ok = bl < nbp && m < p.M;
+      const uint16_t *xp = p.x + (size_t)m * p.ldx + (size_t)(kb_begin + bl) * 128 + lg * 16;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) xr[t][j][q] = ok ? ldg16(xp + (q & 1) * 8 + (q >> 1) * 64) : u32x4{0, 0, 0, 0};
-      }
-  }
-
-  if constexpr (!XREG) {
-    // x[:, part] -> LDS (only rows < M; the fragments of rows >= M are zeros)
-    for (int idx = tid; idx < p.M * nbp * 16; idx += 256) {
-      const int m = idx / (nbp * 16), c = idx % (nbp * 16);
-      *reinterpret_cast<u32x4 *>(xs + m * XROW + c * 16) = ldg16(p.x + (size_t)m * p.ldx + (size_t)kb_begin * 128 + c * 8);
+      for (int q = 0; q < 4; ++q) xr[t][j][q] = ok ? ldg16(xp + (q & 1) * 8 + (q >> 1) * 64) : u32x4{0, 0, 0, 0};
     }
-  }
 
   for (int tile = tile_begin, it = 0, buf = 0; tile < tile_end; ++tile, ++it, buf = buf == nbuf - 1 ? 0 : buf + 1) {
     const int nt = tile * 16;
@@ -306,27 +293,11 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
         fp8x16_to_bf16x16(w1, a2, a3);
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-          const int m = t * 16 + li;
-          bf16x8 x0, x1, x2, x3;
-          if constexpr (XREG) {
-            x0 = as_bf16x8(xr[t][j][0]);
-            x1 = as_bf16x8(xr[t][j][1]);
-            x2 = as_bf16x8(xr[t][j][2]);
-            x3 = as_bf16x8(xr[t][j][3]);
-          } else if (m < p.M) {
-            const uint8_t *xp = xs + m * XROW + bl * 256 + lg * 32;
-            x0 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xp));
-            x1 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xp + 16));
-            x2 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xp + 128));
-            x3 = as_bf16x8(*reinterpret_cast<const u32x4 *>(xp + 144));
-          } else {
-            x0 = x1 = x2 = x3 = as_bf16x8(u32x4{0, 0, 0, 0});
-          }
           f32x4 c = {0.f, 0.f, 0.f, 0.f};
-          c = mfma16(a0, x0, c);
-          c = mfma16(a1, x1, c);
-          c = mfma16(a2, x2, c);
-          c = mfma16(a3, x3, c);
+          c = mfma16(a0, as_bf16x8(xr[t][j][0]), c);
+          c = mfma16(a1, as_bf16x8(xr[t][j][1]), c);
+          c = mfma16(a2, as_bf16x8(xr[t][j][2]), c);
+          c = mfma16(a3, as_bf16x8(xr[t][j][3]), c);
           acc[t] += scw[j] * c;
         }
       }
@@ -383,11 +354,9 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(GemvParams p, GemvGro
   gemv_body<MT, GEMV_PLAIN>(q, blockIdx.x % gr.units, rg, kparts, kpb);
 }
 
-size_t gemv_lds_bytes(int M, int MT, int kpb, int rg) {
+size_t gemv_lds_bytes(int MT, int kpb, int rg) {
   const int tile = 16 * gemv_kpb4(kpb) * 128;
-  return (size_t)gemv_nbuf(tile) * tile + (gemv_x_in_registers(MT) ? 0 : (size_t)M * gemv_xrow(kpb)) +
-         2 * 4 * MT * 64 * 16 +
-         (size_t)rg * MT * 64 * 16;
+  return (size_t)gemv_nbuf(tile) * tile + 2 * 4 * MT * 64 * 16 + (size_t)rg * MT * 64 * 16;
 }
 
 // Sums the K parts of gemv_kernel in part order and applies the epilogue.
@@ -530,13 +499,13 @@ GemvPlan plan_gemv(int M, int N, int K) {
   const int KB = K / 128;
   const int MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   // K part: whole K when it fits (no finishing pass), else the largest block
-  // count <= GEMV_KPB (multiple of 4) that splits K into equal parts; both
-  // within the LDS budget with one tile per unit
+  // count <= gemv_kpb_max(MT) (multiple of 4) that splits K into equal parts;
+  // both within the LDS budget with one tile per unit
   constexpr size_t LDS_MAX = 160 * 1024;
   // rows of K >= 2048 (o_proj, the FFN and expert projections) take 16 KB
   // tiles (more K parts, two workgroups per CU): measured faster than 32 KB
-  int kmax = K >= 2048 ? 8 : GEMV_KPB;
-  while (kmax > 4 && gemv_lds_bytes(M, MT, kmax, 1) > LDS_MAX) kmax -= 4;
+  int kmax = K >= 2048 ? 8 : gemv_kpb_max(MT);
+  while (kmax > 4 && gemv_lds_bytes(MT, kmax, 1) > LDS_MAX) kmax -= 4;
   int kpb = KB <= kmax ? KB : 0;
   if (!kpb) {
     for (int c = kmax; c >= 4; c -= 4)
@@ -553,9 +522,9 @@ GemvPlan plan_gemv(int M, int N, int K) {
   int best_rg = 1;
   int64_t best_cost = INT64_MAX;
   for (int rg = 1; rg <= GEMV_MAX_RG; ++rg) {
-    if (gemv_lds_bytes(M, MT, kpb, rg) > LDS_MAX) break;
+    if (gemv_lds_bytes(MT, kpb, rg) > LDS_MAX) break;
     const int64_t units = (int64_t)((tiles + rg - 1) / rg) * pl.kparts;
-    const int64_t slots = 256 * std::min<int64_t>(2, LDS_MAX / gemv_lds_bytes(M, MT, kpb, rg));
+    const int64_t slots = 256 * std::min<int64_t>(2, LDS_MAX / gemv_lds_bytes(MT, kpb, rg));
     const int64_t cost = ((units + slots - 1) / slots) * (rg + 1);
     if (cost <= best_cost) {
       best_cost = cost;
@@ -564,7 +533,7 @@ GemvPlan plan_gemv(int M, int N, int K) {
   }
   pl.rg = best_rg;
   pl.groups = ((tiles + pl.rg - 1) / pl.rg) * pl.kparts;
-  pl.lds = gemv_lds_bytes(M, MT, kpb, pl.rg);
+  pl.lds = gemv_lds_bytes(MT, kpb, pl.rg);
   pl.part_bytes = pl.kparts > 1 ? (size_t)pl.kparts * M * N * 4 : 0;
   return pl;
 }
@@ -576,11 +545,11 @@ GemvPlan plan_gemv_grouped(int M, int N, int K) {
   const int MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   const int tiles = N / 16;
   int rg = std::min(GEMV_MAX_RG, tiles);
-  while (rg > pl.rg && gemv_lds_bytes(M, MT, pl.kpb, rg) > 160 * 1024) --rg;
+  while (rg > pl.rg && gemv_lds_bytes(MT, pl.kpb, rg) > 160 * 1024) --rg;
   if (rg > pl.rg) {
     pl.rg = rg;
     pl.groups = ((tiles + rg - 1) / rg) * pl.kparts;
-    pl.lds = gemv_lds_bytes(M, MT, pl.kpb, rg);
+    pl.lds = gemv_lds_bytes(MT, pl.kpb, rg);
   }
   return pl;
 }
@@ -620,6 +589,8 @@ int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t 
   if (p0.w1 && p0.n_split % 128)
     return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM: the first weight segment must be a multiple of 128 rows");
   const int MT = p0.M <= 16 ? 1 : (p0.M <= 32 ? 2 : 4);
+  if (pl.kpb > gemv_kpb_max(MT) || gemv_lds_bytes(MT, pl.kpb, pl.rg) > pl.lds)
+    return fail(AMLA_EINVAL, "skinny fp8 GEMM: plan for a smaller M");
   if (MT == 1) launch_mt<1>(p0, mode, pl, st);
   else if (MT == 2) launch_mt<2>(p0, mode, pl, st);
   else launch_mt<4>(p0, mode, pl, st);
@@ -657,10 +628,10 @@ int launch_gemv_grouped(const GemvParams &p, GemvGroups gr, const GemvPlan &pl, 
   }
   if (p.N % 16 || p.K % 128 || pl.kparts > GEMV_MAX_PARTS || (p.w1 && p.n_split % 128))
     return fail(AMLA_EUNSUPPORTED, "grouped skinny GEMM: unsupported shape N=%d K=%d", p.N, p.K);
-  if (gemv_lds_bytes(max_m, max_m <= 16 ? 1 : (max_m <= 32 ? 2 : 4), pl.kpb, pl.rg) > pl.lds)
+  const int MT = max_m <= 16 ? 1 : (max_m <= 32 ? 2 : 4);
+  if (gemv_lds_bytes(MT, pl.kpb, pl.rg) > pl.lds || pl.kpb > gemv_kpb_max(MT))
     return fail(AMLA_EINVAL, "grouped skinny GEMM: plan for a smaller M");
   gr.units = pl.groups;
-  const int MT = max_m <= 16 ? 1 : (max_m <= 32 ? 2 : 4);
   if (MT == 1) launch_grouped_mt<1>(p, gr, pl, st);
   else if (MT == 2) launch_grouped_mt<2>(p, gr, pl, st);
   else launch_grouped_mt<4>(p, gr, pl, st);
@@ -693,7 +664,7 @@ int launch_gemv_sched(const GemvParams &p, const MoeSched &s, int max_entries, i
     return fail(AMLA_EUNSUPPORTED, "scheduled skinny GEMM: unsupported shape N=%d K=%d", p.N, p.K);
   if (pl.kparts > 1 && !p.part) return fail(AMLA_EWORKSPACE, "scheduled skinny GEMM: missing partial sums");
   const int MT = max_m <= 16 ? 1 : (max_m <= 32 ? 2 : 4);
-  if (gemv_lds_bytes(max_m, MT, pl.kpb, pl.rg) > pl.lds)
+  if (gemv_lds_bytes(MT, pl.kpb, pl.rg) > pl.lds || pl.kpb > gemv_kpb_max(MT))
     return fail(AMLA_EINVAL, "scheduled skinny GEMM: plan for a smaller M");
   if ((int64_t)max_entries * pl.groups > INT32_MAX) return fail(AMLA_EUNSUPPORTED, "scheduled skinny GEMM: grid");
   if (MT == 1) launch_sched_mt<1>(p, s, max_entries, pl, st);

@@ -61,8 +61,10 @@ def test_swiglu_small(M):
     assert_parity(got, F.dense_ffn(x, w), f"swiglu small M={M}")
 
 
-@pytest.mark.parametrize("which,M", [("dense", 8), ("expert", 8), ("expert", 1), ("expert", 96)])
+@pytest.mark.parametrize("which,M", [("dense", 8), ("dense", 32), ("dense", 64), ("expert", 8), ("expert", 1),
+                                     ("expert", 96)])
 def test_swiglu_r1_shapes(which, M):
+    """Dense at M = 64: down_proj's K = 18432 in 18 parts of 8 blocks (x held in registers)."""
     print(f"[case] swiglu r1 {which} M={M}", flush=True)
     d = R1.hidden_size
     i = R1.intermediate_size if which == "dense" else R1.moe_intermediate_size
