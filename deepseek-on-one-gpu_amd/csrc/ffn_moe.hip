@@ -729,8 +729,9 @@ constexpr int MOE_TILE_ROWS = 256;  // rows of a GEMM tile entry
 
 struct MoeDevLayout {
   int sb;                      // largest group on the skinny path
-  int max_small, max_tiles;    // schedule entries (worst case)
-  size_t hdr, gather, scatter, small, tiles, xs, ys, gu, h, part, total;
+  int sb1;                     // largest group of the one-tile skinny launch (<= 16 rows)
+  int max_small, max_small4, max_tiles;  // schedule entries (worst case)
+  size_t hdr, cls, gather, scatter, small, small4, tiles, xs, ys, gu, h, part, total;
 };
 
 static MoeDevLayout moe_dev_layout(int64_t m, int64_t d, int top_k, int64_t n, int64_t E) {
@@ -739,14 +740,20 @@ static MoeDevLayout moe_dev_layout(int64_t m, int64_t d, int top_k, int64_t n, i
   // a token names an expert once in a routing, so a group has at most m rows;
   // larger groups (repeated indices) and groups over 64 rows take the GEMM
   L.sb = (int)std::min<int64_t>(std::min<int64_t>(m, 64), S);
+  // skinny groups of up to 16 rows and of 17..sb rows take separate launches
+  // (one x tile, or the tiles the largest needs), each sized for its own worst case
+  L.sb1 = std::min(L.sb, 16);
   L.max_small = (int)std::min<int64_t>(E, S);
+  L.max_small4 = L.sb > L.sb1 ? (int)std::min<int64_t>(E, S / (L.sb1 + 1)) : 0;
   L.max_tiles = (int)((S + MOE_TILE_ROWS - 1) / MOE_TILE_ROWS + std::min<int64_t>(E, S / (L.sb + 1)));
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
   L.hdr = take(16);
+  L.cls = take(8);
   L.gather = take((size_t)S * 4);
   L.scatter = take((size_t)S * 4);
   L.small = take((size_t)L.max_small * 16);
+  L.small4 = take((size_t)std::max(L.max_small4, 1) * 16);
   L.tiles = take((size_t)std::max(L.max_tiles, 1) * 16);
   L.xs = take((size_t)S * d * 2);
   L.ys = take((size_t)S * d * 2);
@@ -780,19 +787,22 @@ AMLA_DEV int block_scan_incl(int v, int *wsum, int lane, int wave) {
 // position (rank among equal experts of the 64-slot step by ballots), so the
 // order is slot order within each expert whatever the timing.  Outputs:
 //   gather[p] = token of position p, scatter[p] = slot of position p;
-//   small[]   = (expert, first position, rows) of experts with 1..sb slots;
+//   small[]   = (expert, first position, rows) of experts with 1..sb1 slots;
+//   small4[]  = the same for experts with sb1+1..sb slots;
 //   tiles[]   = (expert, first position, rows <= 256) of the larger ones;
-//   hdr       = {routed slots, small entries, tile entries, skipped slots}.
+//   hdr       = {routed slots, small + small4 entries, tile entries, skipped slots};
+//   cls       = {small entries, small4 entries}.
 // Slots with a negative index are left out; an index >= E, or an expert with a
 // null or misaligned weight, is left out and counted as skipped.
 __global__ __launch_bounds__(1024) void moe_sort_kernel(const int64_t *__restrict__ idx, int S, int top_k, int E,
-                                                        int sb, const void *const *__restrict__ wtab,
-                                                        int32_t *__restrict__ hdr, int32_t *__restrict__ gather,
-                                                        int32_t *__restrict__ scatter, int32_t *__restrict__ small,
+                                                        int sb, int sb1, const void *const *__restrict__ wtab,
+                                                        int32_t *__restrict__ hdr, int32_t *__restrict__ cls,
+                                                        int32_t *__restrict__ gather, int32_t *__restrict__ scatter,
+                                                        int32_t *__restrict__ small, int32_t *__restrict__ small4,
                                                         int32_t *__restrict__ tiles) {
   __shared__ int32_t cur[MSORT_WAVES][MSORT_MAXE];  // per-wave counts, then per-wave next positions
   __shared__ int32_t eok[MSORT_MAXE];
-  __shared__ int32_t wsum[3][MSORT_WAVES];
+  __shared__ int32_t wsum[4][MSORT_WAVES];
   __shared__ int32_t skipped;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int i = tid; i < MSORT_WAVES * MSORT_MAXE; i += 1024) (&cur[0][0])[i] = 0;
@@ -831,10 +841,12 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int64_t *__restric
       tot += c;
     }
   }
-  const int is_small = tot >= 1 && tot <= sb;
+  const int is_small = tot >= 1 && tot <= sb1;
+  const int is_small4 = tot > sb1 && tot <= sb;
   const int ntile = tot > sb ? (tot + MOE_TILE_ROWS - 1) / MOE_TILE_ROWS : 0;
   const int pos_incl = block_scan_incl(tot, wsum[0], lane, wave);
   const int small_incl = block_scan_incl(is_small, wsum[1], lane, wave);
+  const int small4_incl = block_scan_incl(is_small4, wsum[3], lane, wave);
   const int tile_incl = block_scan_incl(ntile, wsum[2], lane, wave);
   const int first = pos_incl - tot;
   if (tid < E) {
@@ -844,6 +856,10 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int64_t *__restric
       int32_t *en = small + 4 * (small_incl - 1);
       en[0] = tid; en[1] = first; en[2] = tot; en[3] = 0;
     }
+    if (is_small4) {
+      int32_t *en = small4 + 4 * (small4_incl - 1);
+      en[0] = tid; en[1] = first; en[2] = tot; en[3] = 0;
+    }
     for (int j = 0; j < ntile; ++j) {
       int32_t *en = tiles + 4 * (tile_incl - ntile + j);
       en[0] = tid; en[1] = first + j * MOE_TILE_ROWS; en[2] = min(MOE_TILE_ROWS, tot - j * MOE_TILE_ROWS); en[3] = 0;
@@ -851,8 +867,10 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int64_t *__restric
   }
   if (tid == 1023) {
     hdr[0] = pos_incl;
-    hdr[1] = small_incl;
+    hdr[1] = small_incl + small4_incl;
     hdr[2] = tile_incl;
+    cls[0] = small_incl;
+    cls[1] = small4_incl;
   }
   __syncthreads();
   if (tid == 0) hdr[3] = skipped;
@@ -919,13 +937,16 @@ int amla_moe_experts_dev(const void *hidden, int64_t m, int64_t d, int top_k, co
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int S = (int)(m * top_k), n = (int)n_inter, D = (int)d, E = (int)n_experts;
   int rc;
-  moe_sort_kernel<<<1, 1024, 0, st>>>(indices, S, top_k, E, L.sb, weight_table, hdr, gather, scatter, small, tiles);
+  int32_t *cls = reinterpret_cast<int32_t *>(ws + L.cls), *small4 = reinterpret_cast<int32_t *>(ws + L.small4);
+  moe_sort_kernel<<<1, 1024, 0, st>>>(indices, S, top_k, E, L.sb, L.sb1, weight_table, hdr, cls, gather, scatter,
+                                      small, small4, tiles);
   if ((rc = check_launch("moe_experts_dev schedule"))) return rc;
   RowList none = {};
   move_rows_kernel<false><<<S, 256, 0, st>>>(static_cast<const uint16_t *>(hidden), d, S, none, gather, xs, hdr);
   if ((rc = check_launch("moe_experts_dev gather"))) return rc;
-  const MoeSched small_gu = {weight_table, small, hdr + 1, E, 0}, tiles_gu = {weight_table, tiles, hdr + 2, E, 0};
-  const MoeSched small_dn = {weight_table, small, hdr + 1, E, 1}, tiles_dn = {weight_table, tiles, hdr + 2, E, 1};
+  const MoeSched small_gu = {weight_table, small, cls, E, 0}, tiles_gu = {weight_table, tiles, hdr + 2, E, 0};
+  const MoeSched small_dn = {weight_table, small, cls, E, 1}, tiles_dn = {weight_table, tiles, hdr + 2, E, 1};
+  const MoeSched small4_gu = {weight_table, small4, cls + 1, E, 0}, small4_dn = {weight_table, small4, cls + 1, E, 1};
   GemvParams pg = {};  // [gate | up] x (rows, D) -> gu (rows, 2n)
   pg.x = xs; pg.ldx = D; pg.N = 2 * n; pg.K = D; pg.n_split = n; pg.y = gu; pg.ldy = 2 * n; pg.seq_len = 1;
   pg.part = part;
@@ -933,12 +954,14 @@ int amla_moe_experts_dev(const void *hidden, int64_t m, int64_t d, int top_k, co
   pd.x = hb; pd.ldx = n; pd.N = D; pd.K = n; pd.n_split = D; pd.y = ys; pd.ldy = D; pd.seq_len = 1;
   pd.part = part;
   if ((rc = launch_gemm_sched(pg, tiles_gu, L.max_tiles, st))) return rc;
-  if ((rc = launch_gemv_sched(pg, small_gu, L.max_small, L.sb, plan_gemv_grouped(L.sb, 2 * n, D), st))) return rc;
+  if ((rc = launch_gemv_sched(pg, small_gu, L.max_small, L.sb1, plan_gemv_grouped(L.sb1, 2 * n, D), st))) return rc;
+  if ((rc = launch_gemv_sched(pg, small4_gu, L.max_small4, L.sb, plan_gemv_grouped(L.sb, 2 * n, D), st))) return rc;
   silu_mul_rows_kernel<<<dim3((unsigned)std::max(1, std::min(n / 8 / 256, 16)), (unsigned)std::min(S, 65535)), 256,
                          0, st>>>(gu, S, n, hb, hdr);
   if ((rc = check_launch("moe_experts_dev silu_mul"))) return rc;
   if ((rc = launch_gemm_sched(pd, tiles_dn, L.max_tiles, st))) return rc;
-  if ((rc = launch_gemv_sched(pd, small_dn, L.max_small, L.sb, plan_gemv_grouped(L.sb, D, n), st))) return rc;
+  if ((rc = launch_gemv_sched(pd, small_dn, L.max_small, L.sb1, plan_gemv_grouped(L.sb1, D, n), st))) return rc;
+  if ((rc = launch_gemv_sched(pd, small4_dn, L.max_small4, L.sb, plan_gemv_grouped(L.sb, D, n), st))) return rc;
   move_rows_kernel<true><<<S, 256, 0, st>>>(ys, d, S, none, scatter, static_cast<uint16_t *>(expert_out), hdr);
   return check_launch("moe_experts_dev scatter");
 }

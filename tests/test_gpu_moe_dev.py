@@ -58,10 +58,11 @@ def _want(h, idx, table, skip=lambda e: False):
 
 
 @pytest.mark.parametrize("E,K,m,dup", [(256, 8, 8, False), (6, 3, 150, False), (16, 8, 200, False),
-                                       (2, 1, 300, False), (8, 4, 5, True), (1, 4, 1, True)])
+                                       (2, 1, 300, False), (8, 4, 5, True), (1, 4, 1, True),
+                                       (4, 2, 40, False), (12, 3, 60, False)])
 def test_moe_experts_dev_vs_expert_ffn(E, K, m, dup):
-    """Skinny groups (at most min(m, 64) slots), GEMM tiles (larger groups) and groups made
-    larger than m by repeated indices."""
+    """Skinny groups (at most min(m, 64) slots: up to 16 rows in one launch, 17 and more in
+    another), GEMM tiles (larger groups) and groups made larger than m by repeated indices."""
     print(f"[case] moe_experts_dev E={E} K={K} m={m} dup={dup}", flush=True)
     d, i = 256, 256
     h = _x((m, d), f"mdev{E}{K}{m}")
