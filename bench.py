@@ -156,17 +156,32 @@ def attn_traffic(B, T):
 # ------------------------------------------------------------------ CPU baseline
 
 def _cpu_model():
+    """Model name plus family / model / stepping, nominal clock and L2 size from /proc/cpuinfo
+    (a virtualised host may report only a generic model name)."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = (x.strip() for x in line.split(":", 1))
+                info.setdefault(k, v)
+            elif info:
+                break          # first processor block only
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    parts = [info.get("model name", "unknown")]
+    if "cpu family" in info:
+        parts.append(f"family {info['cpu family']} model {info.get('model', '?')} stepping {info.get('stepping', '?')}")
+    if "cpu MHz" in info:
+        parts.append(f"{float(info['cpu MHz']):.0f} MHz")
+    if "cache size" in info:
+        parts.append(f"cache {info['cache size']}")
+    flags = info.get("flags", "").split()
+    parts.append("avx512" if "avx512f" in flags else "no avx512")
+    return ", ".join(parts)
 
 
-def _median_s(fn, reps=3):
-    fn()                                     # warm-up (thread pool, allocator)
+def _median_s(fn, reps=3, warm=None):
+    (warm or fn)()                           # warm-up (thread pool, allocator)
     ts = []
     for _ in range(reps):
         t0 = time.perf_counter()
@@ -177,12 +192,12 @@ def _median_s(fn, reps=3):
 
 def cpu_baseline(T, B):
     """The oracle (the torch-CPU restatement of the reference's op sequence) on
-    the host cores.  Headline: one layer x one sequence at the full context,
-    median of 3 after a warm-up, scaled x B sequences (the reference's position
-    is one int, so a batch is B independent sequences).  Also one timed run each
-    (after the warm-up above) of decode B=1 at context 257 and 4096, the 15
-    fp8_linear calls of the 5 projection shapes x M in {1, 8, 64}, and prefill of
-    4096 tokens; these are in cpu_baseline_configs."""
+    the host cores, every figure the median of 3 timed runs after a warm-up run.
+    Headline: one layer x one sequence at the full context, scaled x B sequences
+    (the reference's position is one int, so a batch is B independent sequences).
+    cpu_baseline_configs: decode B=1 at context 257 and 4096, the 15 fp8_linear
+    calls of the 5 projection shapes x M in {1, 8, 64}, and prefill of 4096
+    tokens (warmed up by a 256-token prefill, the timed runs at 4096)."""
     from oracle import ref_ops as R
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
@@ -194,28 +209,28 @@ def cpu_baseline(T, B):
         tab = R.precompute_rope_freqs(CFG, Tc)
         return lambda: R.mla_attention(h, lay.attn_weights, (ckv, kpe), Tc - 1, tab, CFG)
 
+    def entry(sec):
+        return {"us": round(sec * 1e6, 1), "median_of": 3}
+
     dt = _median_s(decode(T))
-    cfgs = {}
-    f = decode(257)
-    t0 = time.perf_counter(); f(); cfgs["decode_b1_ctx257_us"] = round((time.perf_counter() - t0) * 1e6, 1)
-    f = decode(4096)
-    t0 = time.perf_counter(); f(); cfgs["decode_b1_ctx4096_us"] = round((time.perf_counter() - t0) * 1e6, 1)
+    cfgs = {"decode_b1_ctx257": entry(_median_s(decode(257))),
+            "decode_b1_ctx4096": entry(_median_s(decode(4096)))}
     lin = {}
     for name in synth.projection_shapes(CFG):
         w, sc = lay.attn_weights[name]
         for M in (1, 8, 64):
             x = synth.randn((M, w.shape[1]), synth.seed_of("cpu", name, M), 1.0).to(torch.bfloat16)
-            t0 = time.perf_counter()
-            R.fp8_linear(x, w, sc)
-            lin[f"{name}_m{M}"] = round((time.perf_counter() - t0) * 1e6, 1)
-    cfgs["fp8_linear_us"] = lin
-    S = 4096
-    hp = synth.make_hidden(CFG, 1, S, "cpu-prefill")
-    cp = (torch.zeros(1, S, 512, dtype=torch.bfloat16), torch.zeros(1, S, 64, dtype=torch.bfloat16))
-    tab = R.precompute_rope_freqs(CFG, S)
-    t0 = time.perf_counter()
-    R.mla_attention(hp, lay.attn_weights, cp, 0, tab, CFG)
-    cfgs["prefill_4096_us"] = round((time.perf_counter() - t0) * 1e6, 1)
+            lin[f"{name}_m{M}"] = entry(_median_s(lambda: R.fp8_linear(x, w, sc)))
+    cfgs["fp8_linear"] = lin
+
+    def prefill(S):
+        hp = synth.make_hidden(CFG, 1, S, "cpu-prefill")
+        cp = (torch.zeros(1, S, 512, dtype=torch.bfloat16), torch.zeros(1, S, 64, dtype=torch.bfloat16))
+        tab = R.precompute_rope_freqs(CFG, S)
+        return lambda: R.mla_attention(hp, lay.attn_weights, cp, 0, tab, CFG)
+
+    cfgs["prefill_4096"] = entry(_median_s(prefill(4096), warm=prefill(256)))
+    cfgs["host"] = f"{_cpu_model()}, {cores} threads"
     return ({"value": round(dt * B * 1e6, 1), "unit": "us/layer", "cores": cores, "kind": "port",
              "sample": f"oracle mla_attention, 1 layer x 1 sequence at context {T}: median of 3 after a warm-up "
                        f"{dt:.3f} s, x{B} sequences (extrapolated); host {_cpu_model()}, {cores} threads"},
@@ -329,6 +344,13 @@ def ffn_extras(B, dev):
         ops.moe_block(x, gw, shared, experts, CFG)
     ms = _time_eager(graph.replay, 10)
     out["moe_block_b8_graph_us"] = round(ms * 1000, 2)
+    # batch 64: most chosen experts get 2-8 tokens, some more than 16 (the 17-64 row class)
+    x64 = (torch.randn(64, 1, d, generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+    idx64, _ = ops.route(x64, gw, CFG)
+    out["moe_block_b64_experts"] = int(torch.unique(idx64).numel())
+    out["moe_block_b64_us"] = round(_time_eager(lambda: ops.moe_block(x64, gw, shared, experts, CFG), 10) * 1000, 2)
+    out["moe_block_b64_host_grouping_us"] = round(
+        _time_eager(lambda: ops.moe_block(x64, gw, shared, experts, CFG, device_grouping=False), 10) * 1000, 2)
     del graph, experts, shared
     torch.cuda.empty_cache()
     return out

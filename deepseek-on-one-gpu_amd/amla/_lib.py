@@ -46,6 +46,8 @@ SIGNATURES = [
     ("amla_fp8_linear", c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64,
                                 c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
     ("amla_fp8_linear_workspace_bytes", c_size_t, [c_int64, c_int64, c_int64]),
+    ("amla_fp8_linear_f32", c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+                                    c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
     ("amla_rms_norm", c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p,
                               c_int64, c_void_p]),
     ("amla_apply_rope", c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),

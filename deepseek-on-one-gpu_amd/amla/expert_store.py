@@ -119,11 +119,18 @@ class ExpertStore:
                         raise ValueError(f"ExpertStore: {key} is {meta['dtype']} {meta['shape']}, "
                                          f"expected {dtype} {list(shape)}")
                     b0, b1 = meta["data_offsets"]
+                    nbytes = math.prod(shape) * torch.empty((), dtype=dtype).element_size()
+                    if b1 - b0 != nbytes:
+                        raise ValueError(f"ExpertStore: {key} spans {b1 - b0} bytes in {shard}, its shape "
+                                         f"{list(shape)} needs {nbytes}")
                     f.seek(data0 + b0)
-                    view = buf[base + off:base + off + (b1 - b0)]
-                    got = f.readinto(view)
-                    if got != b1 - b0:
-                        raise IOError(f"ExpertStore: short read of {key} ({got} of {b1 - b0} bytes)")
+                    view = buf[base + off:base + off + nbytes]
+                    done = 0
+                    while done < nbytes:      # a raw read may return fewer bytes than asked
+                        got = f.readinto(view[done:])
+                        if not got:
+                            raise IOError(f"ExpertStore: {shard} ends inside {key} ({done} of {nbytes} bytes)")
+                        done += got
 
     # -------------------------------------------------------------- slots
 

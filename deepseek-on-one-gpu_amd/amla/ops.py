@@ -92,12 +92,16 @@ def fp8_block_dequant(weight: torch.Tensor, scale_inv: torch.Tensor) -> torch.Te
 
 def fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Tensor,
                out_dtype: torch.dtype = BF16) -> torch.Tensor:
-    """inference/ops.py:15-44: bf16( x @ dequant(weight, scale_inv).T ), fp32 accumulation."""
+    """inference/ops.py:15-44: ( x @ dequant(weight, scale_inv).T ).to(out_dtype), fp32 accumulation.
+
+    bf16 rounds in the kernel's epilogue (``torch.ops.amla.fp8_linear``); any other out_dtype
+    takes the fp32 result (``torch.ops.amla.fp8_linear_f32``) cast with ``.to(out_dtype)`` as the
+    reference does."""
     _need_cuda(x, "x")
     if x.dtype != BF16:
         raise TypeError(f"fp8_linear: x must be bfloat16 (got {x.dtype})")
-    if out_dtype != BF16:
-        raise TypeError("fp8_linear: only out_dtype=torch.bfloat16 is implemented")
+    if not isinstance(out_dtype, torch.dtype) or not (out_dtype.is_floating_point or out_dtype.is_complex):
+        raise TypeError(f"fp8_linear: out_dtype must be a floating-point dtype (got {out_dtype})")
     _need(weight, "weight", FP8, x.device)
     _need(scale_inv, "scale_inv", torch.float32, x.device)
     n, k = weight.shape
@@ -106,9 +110,12 @@ def fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Tensor,
     if scale_inv.shape != (math.ceil(n / 128), math.ceil(k / 128)):
         raise ValueError(f"scale_inv shape {tuple(scale_inv.shape)} does not match weight {n}x{k}")
     x2 = x.reshape(-1, k)
-    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+    if x2.stride(-1) != 1 or x2.stride(0) % 8:
         x2 = x2.contiguous()
-    return torch.ops.amla.fp8_linear(x2, weight, scale_inv).view(*x.shape[:-1], n)
+    if out_dtype == BF16:
+        return torch.ops.amla.fp8_linear(x2, weight, scale_inv).view(*x.shape[:-1], n)
+    y = torch.ops.amla.fp8_linear_f32(x2, weight, scale_inv).view(*x.shape[:-1], n)
+    return y if out_dtype == torch.float32 else y.to(out_dtype)
 
 
 # ------------------------------------------------------------------ RoPE
@@ -320,17 +327,9 @@ def swiglu(x: torch.Tensor, gate_proj: torch.Tensor, gate_scale: torch.Tensor, u
     _fp8_pair(up_proj, up_scale, "up_proj", (n, k), x.device)
     _fp8_pair(down_proj, down_scale, "down_proj", (k, n), x.device)
     x2 = x.reshape(-1, k)
-    if not x2.is_contiguous() or x2.data_ptr() % 16:
+    if not x2.is_contiguous():
         x2 = x2.contiguous()
-    m = x2.shape[0]
-    y = torch.empty(m, k, dtype=BF16, device=x.device)
-    if m:
-        need = lib().amla_swiglu_workspace_bytes(m, k, n)
-        ws = workspace(x.device, need)
-        check(lib().amla_swiglu(x2.data_ptr(), m, k, gate_proj.data_ptr(), gate_scale.data_ptr(),
-                                up_proj.data_ptr(), up_scale.data_ptr(), n, down_proj.data_ptr(),
-                                down_scale.data_ptr(), y.data_ptr(), ws.data_ptr(), ws.numel(), _stream_ptr(x)),
-              "swiglu")
+    y = torch.ops.amla.swiglu(x2, gate_proj, gate_scale, up_proj, up_scale, down_proj, down_scale)
     return y.view(*x.shape[:-1], k)
 
 
@@ -377,14 +376,18 @@ def route(hidden: torch.Tensor, gate_weight: torch.Tensor, config) -> tuple[torc
 _stacked_cache: dict = {}
 
 
+def _stacked_key(experts: dict, E: int, d: int) -> tuple:
+    return tuple((experts[k][0].data_ptr(), experts[k][1].data_ptr(), tuple(experts[k][0].shape),
+                  tuple(experts[k][1].shape), experts[k][0].dtype, experts[k][1].dtype, experts[k][0].stride(),
+                  experts[k][1].stride(), str(experts[k][0].device)) for k in ("gate_proj", "up_proj", "down_proj")) + (E, d)
+
+
 def _stacked_expert_tables(experts: dict, E: int, d: int, dev):
     """Pointer tables of stacked expert weights (validated once per set of tensors)."""
-    key = tuple((experts[k][0].data_ptr(), experts[k][1].data_ptr(), tuple(experts[k][0].shape),
-                 tuple(experts[k][1].shape), experts[k][0].dtype, experts[k][1].dtype, experts[k][0].stride(),
-                 experts[k][1].stride(), str(experts[k][0].device)) for k in ("gate_proj", "up_proj", "down_proj")) + (E, d)
+    key = _stacked_key(experts, E, d)
     hit = _stacked_cache.get(key)
     if hit is not None:
-        return hit
+        return hit[0], hit[1]
     tabs = []
     n_inter = experts["gate_proj"][0].shape[1]
     for key_name, shape in (("gate_proj", (E, n_inter, d)), ("up_proj", (E, n_inter, d)), ("down_proj", (E, d, n_inter))):
@@ -400,26 +403,23 @@ def _stacked_expert_tables(experts: dict, E: int, d: int, dev):
             tabs.append((ctypes.c_void_p * E)(*[t.data_ptr() + e * step for e in range(E)]))
     if len(_stacked_cache) > 64:
         _stacked_cache.clear()
-    _stacked_cache[key] = (tabs, n_inter)
+    # [host tables, n_inter, device table (made on first use)]: one entry per full key
+    # (pointers, shapes, strides, dtypes, device, E, d), so a device table is never reused for
+    # other tensors that happen to start at the same addresses
+    _stacked_cache[key] = [tabs, n_inter, None]
     return tabs, n_inter
-
-
-_device_table_cache: dict = {}
 
 
 def _stacked_device_table(experts: dict, E: int, d: int, dev):
     """Device pointer table [gate_w | gate_s | up_w | up_s | down_w | down_s] x E of stacked
-    expert weights (amla_moe_experts_dev), made once per set of tensors."""
+    expert weights (amla_moe_experts_dev), made once per set of tensors and kept with the
+    host tables of the same key."""
     tabs, n_inter = _stacked_expert_tables(experts, E, d, dev)
-    key = tuple(t[0] for t in tabs) + (E, str(dev))
-    hit = _device_table_cache.get(key)
-    if hit is None:
+    entry = _stacked_cache[_stacked_key(experts, E, d)]
+    if entry[2] is None:
         flat = [int(t[e] or 0) for t in tabs for e in range(E)]
-        hit = torch.tensor(flat, dtype=torch.int64).to(dev)
-        if len(_device_table_cache) > 64:
-            _device_table_cache.clear()
-        _device_table_cache[key] = hit
-    return hit, n_inter
+        entry[2] = torch.tensor(flat, dtype=torch.int64).to(dev)
+    return entry[2], n_inter
 
 
 def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, shared_weights: dict, experts, config, *,

@@ -6,6 +6,8 @@ implementation so that FakeTensor tracing, ``torch.compile`` and ``make_fx`` see
 the op, its output shape and its in-place writes:
 
 * ``amla::fp8_linear(x, weight, scale_inv)``           inference/ops.py:15-44
+* ``amla::fp8_linear_f32(x, weight, scale_inv)``       the same with fp32 output (out_dtype)
+* ``amla::swiglu(x, gate, gate_scale, up, up_scale, down, down_scale)``  inference/ops.py:186-192
 * ``amla::rms_norm(x, weight, eps)``                   inference/ops.py:10-12
 * ``amla::apply_rope(x, freqs)``                       inference/ops.py:86-97
 * ``amla::mla_decode(...)`` / ``amla::mla_prefill(...)``  inference/ops.py:100-183;
@@ -45,26 +47,73 @@ def _scratch(dev: torch.device, nbytes: int) -> Tensor:
 
 # ------------------------------------------------------------------ fp8_linear
 
-@torch.library.custom_op("amla::fp8_linear", mutates_args=(), device_types="cuda")
-def fp8_linear(x: Tensor, weight: Tensor, scale_inv: Tensor) -> Tensor:
-    """y (M, N) bf16 = bf16(x (M, K) @ dequant(weight, scale_inv).T); x rows 16-byte aligned."""
+def _rows16(x: Tensor) -> Tensor:
+    """x itself when its base is 16-byte aligned, else an aligned copy (the kernels load 16-byte
+    chunks); checked here, inside the operator, where the tensor is real."""
+    return x if x.data_ptr() % 16 == 0 else x.clone(memory_format=torch.contiguous_format)
+
+
+def _linear(x: Tensor, weight: Tensor, scale_inv: Tensor, f32: bool) -> Tensor:
+    x = _rows16(x)
     m, k = x.shape
     n = weight.shape[0]
-    y = torch.empty(m, n, dtype=BF16, device=x.device)
+    y = torch.empty(m, n, dtype=torch.float32 if f32 else BF16, device=x.device)
     if m == 0:
         return y
     L = lib()
     need = L.amla_fp8_linear_workspace_bytes(m, n, k) if m <= 64 else 0
     ws = _scratch(x.device, need) if need else None
-    check(L.amla_fp8_linear(x.data_ptr(), m, k, x.stride(0), weight.data_ptr(), scale_inv.data_ptr(), n,
-                            y.data_ptr(), n, ws.data_ptr() if ws is not None else None,
-                            ws.numel() if ws is not None else 0, _stream(x.device)), "fp8_linear")
+    fn = L.amla_fp8_linear_f32 if f32 else L.amla_fp8_linear
+    check(fn(x.data_ptr(), m, k, x.stride(0), weight.data_ptr(), scale_inv.data_ptr(), n, y.data_ptr(), n,
+             ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(x.device)),
+          "fp8_linear_f32" if f32 else "fp8_linear")
     return y
+
+
+@torch.library.custom_op("amla::fp8_linear", mutates_args=(), device_types="cuda")
+def fp8_linear(x: Tensor, weight: Tensor, scale_inv: Tensor) -> Tensor:
+    """y (M, N) bf16 = bf16(x (M, K) @ dequant(weight, scale_inv).T); x rows with unit stride."""
+    return _linear(x, weight, scale_inv, False)
 
 
 @fp8_linear.register_fake
 def _(x, weight, scale_inv):
     return x.new_empty(x.shape[0], weight.shape[0])
+
+
+@torch.library.custom_op("amla::fp8_linear_f32", mutates_args=(), device_types="cuda")
+def fp8_linear_f32(x: Tensor, weight: Tensor, scale_inv: Tensor) -> Tensor:
+    """y (M, N) fp32 = x (M, K) @ dequant(weight, scale_inv).T, fp32 accumulation, no rounding."""
+    return _linear(x, weight, scale_inv, True)
+
+
+@fp8_linear_f32.register_fake
+def _(x, weight, scale_inv):
+    return x.new_empty(x.shape[0], weight.shape[0], dtype=torch.float32)
+
+
+@torch.library.custom_op("amla::swiglu", mutates_args=(), device_types="cuda")
+def swiglu(x: Tensor, gate_proj: Tensor, gate_scale: Tensor, up_proj: Tensor, up_scale: Tensor, down_proj: Tensor,
+           down_scale: Tensor) -> Tensor:
+    """(M, K) bf16 -> down(silu(gate(x)) * up(x)) (M, K) bf16, every product rounded as in the reference."""
+    x = _rows16(x)
+    m, k = x.shape
+    n = gate_proj.shape[0]
+    y = torch.empty(m, k, dtype=BF16, device=x.device)
+    if m == 0:
+        return y
+    L = lib()
+    need = L.amla_swiglu_workspace_bytes(m, k, n)
+    ws = _scratch(x.device, need)
+    check(L.amla_swiglu(x.data_ptr(), m, k, gate_proj.data_ptr(), gate_scale.data_ptr(), up_proj.data_ptr(),
+                        up_scale.data_ptr(), n, down_proj.data_ptr(), down_scale.data_ptr(), y.data_ptr(),
+                        ws.data_ptr(), ws.numel(), _stream(x.device)), "swiglu")
+    return y
+
+
+@swiglu.register_fake
+def _(x, gate_proj, gate_scale, up_proj, up_scale, down_proj, down_scale):
+    return torch.empty_like(x)
 
 
 # ------------------------------------------------------------------ rms_norm / apply_rope

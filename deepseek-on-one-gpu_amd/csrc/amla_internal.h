@@ -24,11 +24,13 @@ enum GemvMode : int {
   GEMV_RESID = 1,  // y[m, n] = bf16(res[m, n] + bf16(acc))
   GEMV_QKVA = 2,   // rows < n_split -> y; the rest -> latent / rope-key cache rows
   GEMV_QROPE = 3,  // y = bf16(acc); rows with (n % head_dim) >= nope rotated by RoPE at pos(m)
+  GEMV_F32 = 4,    // y[m, n] = acc as fp32 (y is a float buffer, ldy counted in floats)
 };
 
 struct GemvParams {
   const uint16_t *x;  // (M, K) bf16, row stride ldx
   int M, ldx;
+  const uint16_t *xg;  // optional (K) bf16 per-column factor: the GEMM takes bf16(x * xg) as its input
   const uint8_t *w0;  // rows [0, n_split) (all rows unless QKVA)
   const float *s0;
   const uint8_t *w1;  // rows [n_split, N) for QKVA, or for any mode when set (two stacked weights)
@@ -68,8 +70,11 @@ size_t gemv_lds_bytes(int MT, int kpb, int rg);  // MT = 16-row tiles of x (1, 2
 int launch_gemv(const GemvParams &p, int mode, const GemvPlan &plan, hipStream_t stream, bool finish = true);
 // QKVA finish with the q_a RMSNorm fused: sums the K parts, writes the kv_a
 // rows into the caches and rms_norm(q_a, gamma, eps) (both roundings of
-// inference/ops.py:12) into p.y; one workgroup per row.
-int launch_qkva_finish_norm(const GemvParams &p, int kparts, const uint16_t *gamma, float eps, hipStream_t stream);
+// inference/ops.py:12) into p.y; one workgroup per row.  With x_raw (the
+// GEMM ran on bf16(x * input_gamma), p.xg), every sum is first multiplied by
+// the row's input RMSNorm factor rsqrt(mean(x_raw^2) + eps_in).
+int launch_qkva_finish_norm(const GemvParams &p, int kparts, const uint16_t *gamma, float eps, hipStream_t stream,
+                            const uint16_t *x_raw = nullptr, float eps_in = 0.f);
 
 // Independent skinny GEMMs of one shape in one launch (GEMV_PLAIN): the
 // fields below replace those of the shared GemvParams for group g.

@@ -101,6 +101,8 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
   if (MODE == GEMV_PLAIN) {
     u32x2 o = {pack_bf16(v.x, v.y), pack_bf16(v.z, v.w)};
     *reinterpret_cast<u32x2 *>(p.y + (size_t)m * p.ldy + n) = o;
+  } else if (MODE == GEMV_F32) {
+    *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.y) + (size_t)m * p.ldy + n) = v;
   } else if (MODE == GEMV_RESID) {
     const u32x2 r = *reinterpret_cast<const u32x2 *>(p.res + (size_t)m * p.ldr + n);
     u32x2 o = {pack_bf16(lo_bf(r.x) + round_bf16(v.x), hi_bf(r.x) + round_bf16(v.y)),
@@ -250,6 +252,24 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
 #pragma unroll
       for (int q = 0; q < 4; ++q) xr[t][j][q] = ok ? ldg16(xp + (q & 1) * 8 + (q >> 1) * 64) : u32x4{0, 0, 0, 0};
     }
+  if (p.xg) {  // input bf16(x * g) per column (the input RMSNorm's gamma; its row factor is applied by the finish)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int bl = wave + 4 * j;
+      if (bl < nbp) {
+        const uint16_t *gp = p.xg + (size_t)(kb_begin + bl) * 128 + lg * 16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x4 g = ldg16(gp + (q & 1) * 8 + (q >> 1) * 64);
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              xr[t][j][q][e] = pack_bf16(lo_bf(xr[t][j][q][e]) * lo_bf(g[e]), hi_bf(xr[t][j][q][e]) * hi_bf(g[e]));
+        }
+      }
+    }
+  }
 
   for (int tile = tile_begin, it = 0, buf = 0; tile < tile_end; ++tile, ++it, buf = buf == nbuf - 1 ? 0 : buf + 1) {
     const int nt = tile * 16;
@@ -427,12 +447,22 @@ __global__ __launch_bounds__(64) void gemv_finish_sched(GemvParams p, MoeSched s
 // normalises the bf16 q_a columns: r = rsqrt(mean(q_a^2) + eps),
 // y = bf16(bf16(q_a * r) * gamma)  (inference/ops.py:10-12, :130).
 constexpr int QKVA_FIN_MAXG = 3;  // float4 groups per thread: N <= 3 * 4 * 256
+constexpr int QKVA_FIN_MAXX = 4;  // 16-byte chunks of the raw input row per thread: K <= 4 * 8 * 256
 __global__ __launch_bounds__(256) void qkva_finish_norm_kernel(GemvParams p, int kparts, const uint16_t *gamma,
-                                                               float eps) {
+                                                               float eps, const uint16_t *x_raw, float eps_in) {
   const int m = blockIdx.x, tid = threadIdx.x;
   const int ng = p.N >> 2;
   f32x4 v[QKVA_FIN_MAXG];
   float ss = 0.f;
+  // the raw input row's sum of squares (input RMSNorm, inference/forward.py:92): its loads go out first
+  u32x4 xv[QKVA_FIN_MAXX];
+  if (x_raw) {
+#pragma unroll
+    for (int i = 0; i < QKVA_FIN_MAXX; ++i) {
+      const int c = tid + 256 * i;
+      xv[i] = c < (p.K >> 3) ? ldg16(x_raw + (size_t)m * p.ldx + c * 8) : u32x4{0, 0, 0, 0};
+    }
+  }
   // every part of every group in flight before the first add (parts in
   // batches of 8)
   f32x4 s[QKVA_FIN_MAXG];
@@ -455,6 +485,23 @@ __global__ __launch_bounds__(256) void qkva_finish_norm_kernel(GemvParams p, int
       for (int q = 0; q < 8; ++q)
         if (q0 + q < kparts) s[i] += t[i][q];  // part order
   }
+  __shared__ float part[4];
+  __shared__ float partx[4];
+  if (x_raw) {
+    // r_in = rsqrt(mean(x^2) + eps_in): the GEMM summed W . bf16(x * gamma_in), so each sum times r_in
+    // is the projection of the normed input (rounded once, to bf16(x * gamma_in), instead of twice)
+    float sx = 0.f;
+#pragma unroll
+    for (int i = 0; i < QKVA_FIN_MAXX; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sx += lo_bf(xv[i][e]) * lo_bf(xv[i][e]) + hi_bf(xv[i][e]) * hi_bf(xv[i][e]);
+    sx = wave_sum(sx);
+    if ((tid & 63) == 0) partx[tid >> 6] = sx;
+    __syncthreads();
+    const float rin = rsqrtf(((partx[0] + partx[1]) + (partx[2] + partx[3])) / (float)p.K + eps_in);
+#pragma unroll
+    for (int i = 0; i < QKVA_FIN_MAXG; ++i) s[i] *= rin;
+  }
 #pragma unroll
   for (int i = 0; i < QKVA_FIN_MAXG; ++i) {
     const int g = tid + 256 * i;
@@ -469,7 +516,6 @@ __global__ __launch_bounds__(256) void qkva_finish_norm_kernel(GemvParams p, int
     }
   }
   ss = wave_sum(ss);
-  __shared__ float part[4];
   if ((tid & 63) == 0) part[tid >> 6] = ss;
   __syncthreads();
   const float r = __builtin_amdgcn_rsqf(((part[0] + part[1]) + (part[2] + part[3])) / (float)p.n_split + eps);
@@ -485,11 +531,14 @@ __global__ __launch_bounds__(256) void qkva_finish_norm_kernel(GemvParams p, int
   }
 }
 
-int launch_qkva_finish_norm(const GemvParams &p, int kparts, const uint16_t *gamma, float eps, hipStream_t st) {
+int launch_qkva_finish_norm(const GemvParams &p, int kparts, const uint16_t *gamma, float eps, hipStream_t st,
+                            const uint16_t *x_raw, float eps_in) {
   if (p.N > QKVA_FIN_MAXG * 4 * 256 || p.N % 4 || p.n_split % 4)
     return fail(AMLA_EUNSUPPORTED, "q_a/kv_a finish: N=%d exceeds %d or is not a multiple of 4", p.N,
                 QKVA_FIN_MAXG * 4 * 256);
-  qkva_finish_norm_kernel<<<dim3((unsigned)p.M), 256, 0, st>>>(p, kparts, gamma, eps);
+  if (x_raw && (p.K > QKVA_FIN_MAXX * 8 * 256 || p.K % 8 || p.ldx % 8 || !aligned16(x_raw)))
+    return fail(AMLA_EUNSUPPORTED, "q_a/kv_a finish: input row of %d is not foldable", p.K);
+  qkva_finish_norm_kernel<<<dim3((unsigned)p.M), 256, 0, st>>>(p, kparts, gamma, eps, x_raw, eps_in);
   return check_launch("q_a/kv_a finish");
 }
 
@@ -572,6 +621,7 @@ static void launch_mt(const GemvParams &p, int mode, const GemvPlan &pl, hipStre
     case GEMV_PLAIN: launch_cfg<MT, GEMV_PLAIN>(p, pl, st); break;
     case GEMV_RESID: launch_cfg<MT, GEMV_RESID>(p, pl, st); break;
     case GEMV_QKVA: launch_cfg<MT, GEMV_QKVA>(p, pl, st); break;
+    case GEMV_F32: launch_cfg<MT, GEMV_F32>(p, pl, st); break;
     default: launch_cfg<MT, GEMV_QROPE>(p, pl, st); break;
   }
 }
@@ -601,6 +651,7 @@ int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t 
       case GEMV_PLAIN: gemv_finish<GEMV_PLAIN><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
       case GEMV_RESID: gemv_finish<GEMV_RESID><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
       case GEMV_QKVA: gemv_finish<GEMV_QKVA><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
+      case GEMV_F32: gemv_finish<GEMV_F32><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
       default: gemv_finish<GEMV_QROPE><<<blocks, 64, 0, st>>>(p0, pl.kparts); break;
     }
   }
@@ -775,7 +826,7 @@ using namespace amla;
 
 extern "C" {
 
-int amla_abi_version(void) { return 102; }
+int amla_abi_version(void) { return 103; }
 
 const char *amla_last_error(void) { return g_last_error.c_str(); }
 
@@ -837,6 +888,43 @@ int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void
     p.part = reinterpret_cast<float *>(workspace);
   }
   return launch_gemv(p, GEMV_PLAIN, pl, st);
+}
+
+int amla_fp8_linear_f32(const void *x, int64_t m, int64_t k, int64_t ldx, const void *weight,
+                        const float *scale_inv, int64_t n, float *y, int64_t ldy, void *workspace,
+                        size_t workspace_bytes, void *stream) {
+  if (!x || !weight || !scale_inv || !y) return fail(AMLA_EINVAL, "fp8_linear_f32: null pointer");
+  if (m < 0 || n <= 0 || k <= 0) return fail(AMLA_EINVAL, "fp8_linear_f32: bad shape m=%lld n=%lld k=%lld",
+                                             (long long)m, (long long)n, (long long)k);
+  if (ldx < k || ldy < n) return fail(AMLA_EINVAL, "fp8_linear_f32: row stride smaller than the row");
+  if (m == 0) return AMLA_OK;
+  if (n % 16 || k % 128 || ldx % 8 || ldy % 4 || !aligned16(x) || !aligned16(weight) || !aligned16(y))
+    return fail(AMLA_EUNSUPPORTED,
+                "fp8_linear_f32: needs n %% 16 == 0, k %% 128 == 0, ldx %% 8 == 0, ldy %% 4 == 0 and 16-byte "
+                "aligned x/weight/y (n=%lld k=%lld)",
+                (long long)n, (long long)k);
+  GemvParams p = {};
+  p.x = reinterpret_cast<const uint16_t *>(x);
+  p.M = (int)m;
+  p.ldx = (int)ldx;
+  p.w0 = reinterpret_cast<const uint8_t *>(weight);
+  p.s0 = scale_inv;
+  p.N = (int)n;
+  p.K = (int)k;
+  p.n_split = (int)n;
+  p.y = reinterpret_cast<uint16_t *>(y);  // fp32 rows in GEMV_F32 mode
+  p.ldy = (int)ldy;
+  p.seq_len = 1;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (m > 64) return launch_gemm(p, GEMV_F32, st);
+  const GemvPlan pl = plan_gemv((int)m, (int)n, (int)k);
+  if (pl.part_bytes) {
+    if (!workspace || workspace_bytes < pl.part_bytes || !aligned16(workspace))
+      return fail(AMLA_EWORKSPACE, "fp8_linear_f32: needs %zu bytes of 16-byte aligned workspace (got %zu)",
+                  pl.part_bytes, workspace ? workspace_bytes : (size_t)0);
+    p.part = reinterpret_cast<float *>(workspace);
+  }
+  return launch_gemv(p, GEMV_F32, pl, st);
 }
 
 int amla_rms_norm(const void *x, int64_t rows, int64_t dim, int64_t ldx, const void *gamma, float eps,

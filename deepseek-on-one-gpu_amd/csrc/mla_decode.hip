@@ -520,7 +520,12 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       wait_vmcnt<0>();
     }
     prepare_own_rows(smem, smem + TAB_OFF + (tb & 1) * TAB_BYTES, wave, lane, p.eps);
-    __syncthreads();
+    // LDS-only barrier: __syncthreads would also wait for the second tile's
+    // copies (each wave waited for its own first-tile copies above; the second
+    // tile is waited for at the first score step)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     bool have_ref = false;
     for (int tile = tb; tile < te; ++tile) {
       const int it = tile - tb;
@@ -669,7 +674,8 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
         } else if (ks == 12) {
           const uint32_t ra = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
               (__attribute__((address_space(3))) const uint8_t *)(cur + RT_OFF + (4 * lg) * 4)));
-          asm volatile("ds_read_b128 %0, %2 offset:0\n\tds_read_b128 %1, %2 offset:64" : "=v"(rc[0]), "=v"(rc[1]) : "v"(ra));
+          // early-clobber outputs: the second read still needs the address register
+          asm volatile("ds_read_b128 %0, %2 offset:0\n\tds_read_b128 %1, %2 offset:64" : "=&v"(rc[0]), "=&v"(rc[1]) : "v"(ra));
         }
         // unconditional (no branch per copy): past the split's end the last
         // tile is copied again (an L2 hit) into a stage nothing reads any more;
@@ -1197,18 +1203,22 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   uint16_t *qbuf = reinterpret_cast<uint16_t *>(ws + L.qbuf);
 
   // 1. [input RMSNorm, layer mode] q_a | kv_a  (kv_a written raw into the
-  //    caches, inference/ops.py:136-141; forward.py:92)
+  //    caches, inference/ops.py:136-141; forward.py:92).  With K parts the
+  //    norm is folded: the GEMM reads bf16(x * input_gamma) and the K-part
+  //    finish multiplies each sum by the row's rsqrt(mean(x^2) + eps); with a
+  //    single K part it is its own launch first.
   mark(ev, 0, st);
   const uint16_t *xin = x;
-  if (a->input_gamma) {
+  const uint16_t *gin = reinterpret_cast<const uint16_t *>(a->input_gamma);
+  const bool fold_norm = gin && L.pa.kparts > 1 && a->hidden <= 8192;
+  if (gin && !fold_norm) {
     uint16_t *xn = reinterpret_cast<uint16_t *>(ws + L.xn);
-    if ((rc = launch_rms_norm(x, B, a->hidden, a->hidden, reinterpret_cast<const uint16_t *>(a->input_gamma), a->eps,
-                              xn, a->hidden, st)))
-      return rc;
+    if ((rc = launch_rms_norm(x, B, a->hidden, a->hidden, gin, a->eps, xn, a->hidden, st))) return rc;
     xin = xn;
   }
   GemvParams pa = {};
   pa.x = xin; pa.M = B; pa.ldx = a->hidden;
+  pa.xg = fold_norm ? gin : nullptr;
   pa.w0 = reinterpret_cast<const uint8_t *>(a->w_q_a); pa.s0 = a->s_q_a;
   pa.w1 = reinterpret_cast<const uint8_t *>(a->w_kv_a); pa.s1 = a->s_kv_a;
   pa.N = a->q_lora + LORA + ROPE; pa.K = a->hidden; pa.n_split = a->q_lora;
@@ -1224,7 +1234,7 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
   mark(ev, 1, st);
   const uint16_t *gq = reinterpret_cast<const uint16_t *>(a->gamma_q);
   if (L.pa.kparts > 1) {
-    if ((rc = launch_qkva_finish_norm(pa, L.pa.kparts, gq, a->eps, st))) return rc;
+    if ((rc = launch_qkva_finish_norm(pa, L.pa.kparts, gq, a->eps, st, fold_norm ? x : nullptr, a->eps))) return rc;
   } else if ((rc = launch_rms_norm(qa, B, a->q_lora, a->q_lora, gq, a->eps, qa, a->q_lora, st))) {
     return rc;
   }

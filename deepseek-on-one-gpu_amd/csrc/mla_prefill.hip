@@ -28,6 +28,8 @@ AMLA_DEV void pstore4(const GemvParams &p, int m, int n, f32x4 v) {
   if (MODE == GEMV_PLAIN) {
     u32x2 o = {pack_bf16(v.x, v.y), pack_bf16(v.z, v.w)};
     *reinterpret_cast<u32x2 *>(p.y + (size_t)m * p.ldy + n) = o;
+  } else if (MODE == GEMV_F32) {
+    *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.y) + (size_t)m * p.ldy + n) = v;
   } else if (MODE == GEMV_RESID) {
     const u32x2 r = *reinterpret_cast<const u32x2 *>(p.res + (size_t)m * p.ldr + n);
     u32x2 o = {pack_bf16(lo_bf(r.x) + round_bf16(v.x), hi_bf(r.x) + round_bf16(v.y)),
@@ -70,7 +72,9 @@ AMLA_DEV void pstore4(const GemvParams &p, int m, int n, f32x4 v) {
 // Eight consecutive outputs n .. n+7 (n % 8 == 0) already rounded to bf16.
 template <int MODE>
 AMLA_DEV void pstore8(const GemvParams &p, int m, int n, u32x4 v) {
-  if (MODE == GEMV_PLAIN) {
+  if (MODE == GEMV_F32) {
+    // not reached: fp32 outputs take the unstaged epilogue (launch_gemm)
+  } else if (MODE == GEMV_PLAIN) {
     *reinterpret_cast<u32x4 *>(p.y + (size_t)m * p.ldy + n) = v;
   } else if (MODE == GEMV_RESID) {
     const u32x4 r = *reinterpret_cast<const u32x4 *>(p.res + (size_t)m * p.ldr + n);
@@ -448,14 +452,16 @@ int launch_gemm(const GemvParams &p, int mode, hipStream_t st, float *split_ws, 
     return fail(AMLA_EINVAL, "fp8 GEMM: cache rows / rope rows of the epilogue not set");
   if ((mode == GEMV_QKVA || p.w1) && p.n_split % G_BN)
     return fail(AMLA_EUNSUPPORTED, "fp8 GEMM: the first weight segment must be a multiple of 256 rows");
-  static bool attr_set[4] = {false, false, false, false};  // dynamic LDS above 64 KB, once per mode
+  static bool attr_set[5] = {false, false, false, false, false};  // dynamic LDS above 64 KB, once per mode
   const void *fn = mode == GEMV_PLAIN  ? (const void *)gemm_kernel<GEMV_PLAIN>
                    : mode == GEMV_RESID ? (const void *)gemm_kernel<GEMV_RESID>
                    : mode == GEMV_QKVA  ? (const void *)gemm_kernel<GEMV_QKVA>
+                   : mode == GEMV_F32   ? (const void *)gemm_kernel<GEMV_F32>
                                         : (const void *)gemm_kernel<GEMV_QROPE>;
-  if (!attr_set[mode & 3]) {
+  if (mode < 0 || mode > 4) return fail(AMLA_EINVAL, "fp8 GEMM: unknown epilogue mode %d", mode);
+  if (!attr_set[mode]) {
     (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS);
-    attr_set[mode & 3] = true;
+    attr_set[mode] = true;
   }
   // 16-byte output stores need N, the row strides and the bases of every
   // output (and of the residual) on 8-element boundaries
@@ -465,6 +471,7 @@ int launch_gemm(const GemvParams &p, int mode, hipStream_t st, float *split_ws, 
     staged = staged && aligned16(p.ckv) && aligned16(p.kpe) && p.kv_lora % 8 == 0 && p.rope % 8 == 0 &&
              p.ckv_bstride % 8 == 0 && p.kpe_bstride % 8 == 0;
   if (mode == GEMV_QROPE) staged = staged && p.head_dim % 8 == 0 && p.nope % 8 == 0;
+  if (mode == GEMV_F32) staged = false;  // fp32 rows: 16-byte stores of four outputs from the accumulators
   GemmSplit sp = plan_gemm_split(p.M, p.N, p.K);
   if (sp.parts > 1 && (!staged || !split_ws || split_ws_bytes < sp.bytes || !aligned16(split_ws))) {
     // no room for the partial sums (or outputs without 16-byte stores): whole tiles
@@ -477,6 +484,7 @@ int launch_gemm(const GemvParams &p, int mode, hipStream_t st, float *split_ws, 
     case GEMV_PLAIN: gemm_kernel<GEMV_PLAIN><<<grid, G_NW * 64, G_LDS, st>>>(p, staged, sp); break;
     case GEMV_RESID: gemm_kernel<GEMV_RESID><<<grid, G_NW * 64, G_LDS, st>>>(p, staged, sp); break;
     case GEMV_QKVA: gemm_kernel<GEMV_QKVA><<<grid, G_NW * 64, G_LDS, st>>>(p, staged, sp); break;
+    case GEMV_F32: gemm_kernel<GEMV_F32><<<grid, G_NW * 64, G_LDS, st>>>(p, staged, sp); break;
     default: gemm_kernel<GEMV_QROPE><<<grid, G_NW * 64, G_LDS, st>>>(p, staged, sp); break;
   }
   int rc = check_launch("fp8 GEMM");

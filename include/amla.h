@@ -54,6 +54,16 @@ int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void
                     size_t workspace_bytes, void *stream);
 size_t amla_fp8_linear_workspace_bytes(int64_t m, int64_t n, int64_t k);
 
+/* Replaces fp8_linear(x, weight, scale_inv, out_dtype=torch.float32),
+ * inference/ops.py:15-44 (the fp32 result before `.to(out_dtype)`, :44):
+ *   y[i, j] = sum_k x[i, k] * f32(weight[j, k]) * scale_inv[j/128, k/128]
+ * as amla_fp8_linear, with y (m, n) fp32, row stride ldy (in floats, ldy % 4
+ * == 0, y 16-byte aligned).  Same workspace (amla_fp8_linear_workspace_bytes).
+ * Any other out_dtype is this result cast by the caller, as in the reference. */
+int amla_fp8_linear_f32(const void *x, int64_t m, int64_t k, int64_t ldx, const void *weight,
+                        const float *scale_inv, int64_t n, float *y, int64_t ldy, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
 /* Replaces rms_norm(x, weight, eps), inference/ops.py:10-12:
  *   r = rsqrt(mean(f32(x)^2) + eps);  y = bf16( bf16(f32(x) * r) * gamma )
  * x (rows, dim) bf16, row stride ldx; gamma (dim) bf16; y (rows, dim), ldy. */

@@ -25,7 +25,7 @@ def test_every_declared_symbol_is_exported():
     for n in names:
         assert hasattr(L, n), n
     assert {s[0] for s in _lib.SIGNATURES} == set(names)
-    assert L.amla_abi_version() == 102
+    assert L.amla_abi_version() == 103
 
 
 def test_args_struct_layout_matches_c(tmp_path):

@@ -83,3 +83,61 @@ def test_errors(ckpt, tmp_path):
     wrong = SimpleNamespace(hidden_size=D, moe_intermediate_size=2 * I)
     with pytest.raises(ValueError):
         ExpertStore(d, wrong, capacity_bytes=1 << 24).get_expert(0, 0)
+
+
+class _ShortReads:
+    """A raw file whose reads return at most 1000 bytes (as signals, FUSE or network filesystems may)."""
+
+    def __init__(self, path, mode="r", buffering=-1):
+        self.f = open(path, mode, buffering=buffering)
+        self.short = buffering == 0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.f.close()
+
+    def seek(self, off):
+        return self.f.seek(off)
+
+    def read(self, *a):
+        return self.f.read(*a)
+
+    def readinto(self, view):
+        return self.f.readinto(view[:1000] if self.short else view)
+
+
+def test_short_raw_reads_are_completed(ckpt, monkeypatch):
+    import amla.expert_store as es
+    d, ref = ckpt
+    monkeypatch.setattr(es, "open", _ShortReads, raising=False)
+    st = ExpertStore(d, CFG, capacity_bytes=1 << 24)
+    for key in ((0, 1), (1, E - 1)):
+        _same(st.get_expert(*key), ref[key])
+
+
+def test_header_span_must_match_shape(ckpt, tmp_path):
+    """A shard header whose byte offsets disagree with the tensor's shape is refused before any
+    byte lands in the arena (it would spill into the next tensor's slot)."""
+    import json
+    import shutil
+    import struct
+    d, _ = ckpt
+    for name in os.listdir(d):
+        shutil.copy(os.path.join(d, name), tmp_path / name)
+    shard = tmp_path / "model-00001-of-00002.safetensors"
+    raw = shard.read_bytes()
+    n = struct.unpack("<Q", raw[:8])[0]
+    header = json.loads(raw[8:8 + n])
+    key = "model.layers.0.mlp.experts.0.gate_proj.weight"
+    b0, b1 = header[key]["data_offsets"]
+    header[key]["data_offsets"] = [b0, b1 - 16]
+    text = json.dumps(header, separators=(",", ":")).encode()
+    text += b" " * (n - len(text))
+    assert len(text) == n
+    shard.write_bytes(raw[:8] + text + raw[8 + n:])
+    st = ExpertStore(str(tmp_path), CFG, capacity_bytes=1 << 24)
+    with pytest.raises(ValueError, match="spans"):
+        st.get_expert(0, 0)
+    assert st.get_expert(1, 0) is not None        # the failed slot went back to the free list

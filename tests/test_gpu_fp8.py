@@ -67,6 +67,27 @@ def test_fp8_linear_large_m(M, name):
     assert_bf16_ulps(got, want, 2, f"fp8_linear {name} M={M}")
 
 
+@pytest.mark.parametrize("name,M", [("q_b_proj", 1), ("o_proj", 8), ("kv_b_proj", 64), ("q_a_proj", 100),
+                                    ("kv_a_proj_with_mqa", 300)])
+def test_fp8_linear_out_dtype(name, M):
+    """out_dtype (inference/ops.py:19, :44): fp32 is the unrounded fp32 result, within fp32
+    summation-order error of the oracle's (a dropped 128-wide block or a wrong scale would miss by
+    about 1/128 of the magnitude sum); float16 is that result cast, as the reference casts it."""
+    print(f"[case] fp8_linear out_dtype {name} M={M}", flush=True)
+    w, s = _w(name)
+    x = synth.randn((M, SHAPES[name][1]), synth.seed_of("fp8x32", name, M)).to(torch.bfloat16)
+    got = ops.fp8_linear(x.to(DEV), w.to(DEV), s.to(DEV), out_dtype=torch.float32)
+    got16 = ops.fp8_linear(x.to(DEV), w.to(DEV), s.to(DEV), out_dtype=torch.float16)
+    torch.cuda.synchronize()
+    assert got.dtype == torch.float32 and got.shape == (M, SHAPES[name][0])
+    want = R.fp8_linear(x, w, s, out_dtype=torch.float32)
+    mag = x.float().abs() @ R.fp8_block_dequant(w, s).abs().T
+    err = (got.cpu() - want).abs()
+    assert (err <= 2.0 ** -16 * mag).all(), f"max err {err.max().item():.3e}"
+    assert got16.dtype == torch.float16
+    assert torch.equal(got16.cpu(), got.cpu().to(torch.float16))
+
+
 def test_fp8_linear_repeat_is_deterministic():
     w, s = _w("o_proj")
     x = synth.randn((8, SHAPES["o_proj"][1]), 5).to(torch.bfloat16).to(DEV)

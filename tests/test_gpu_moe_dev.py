@@ -105,18 +105,74 @@ def test_moe_experts_dev_skips_and_counts():
     assert_parity(got[keep], want[keep], "moe_experts_dev with skipped slots")
 
 
-def test_moe_experts_dev_r1_expert_shape():
-    """Decode-sized batch at the R1 expert shape (hidden 7168, intermediate 2048): the K-part
-    sums of the skinny path at full size."""
-    print("[case] moe_experts_dev R1 shape m=8 K=2 E=4", flush=True)
-    E, K, m, d, i = 4, 2, 8, 7168, 2048
-    h = _x((m, d), "mdev-r1")
-    g = torch.Generator().manual_seed(77)
+@pytest.mark.parametrize("m", [8, 40])
+def test_moe_experts_dev_r1_expert_shape(m):
+    """Decode-sized batches at the R1 expert shape (hidden 7168, intermediate 2048): the K-part
+    sums of the skinny path at full size, for groups of at most 16 rows (m = 8) and of 17-64
+    rows (m = 40: each of the 4 experts gets about 20 rows), the class whose K parts and finish
+    are sized from the 64-row bound."""
+    print(f"[case] moe_experts_dev R1 shape m={m} K=2 E=4", flush=True)
+    E, K, d, i = 4, 2, 7168, 2048
+    h = _x((m, d), f"mdev-r1-{m}")
+    g = torch.Generator().manual_seed(77 + m)
     idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(m)])
+    counts = torch.bincount(idx.flatten(), minlength=E)
+    if m > 16:
+        assert int(counts.min()) > 16, "every group should take the 17-64 row class"
     table = {e: _mlp(d, i, f"mdev-r1-{e}") for e in range(E)}
     got, hdr = _run_dev(h, idx, _stacked(table, E), E, i)
     assert hdr[0] == m * K and hdr[3] == 0
-    assert_parity(got, _want(h, idx, table), "moe_experts_dev R1 shape")
+    assert_parity(got, _want(h, idx, table), f"moe_experts_dev R1 shape m={m}")
+
+
+def test_moe_block_batch64_r1_shape_device_and_host_grouping_agree():
+    """moe_block at batch 64 with R1-shaped experts (16 stacked experts, 8 per token): device
+    grouping (groups of 17-64 rows) against host grouping, and the device path's expert
+    outputs against the oracle's expert_ffn per slot."""
+    print("[case] moe_block batch 64 R1 expert shape, device vs host grouping", flush=True)
+    E, K, m, d, i = 16, 8, 64, 7168, 2048
+    cfg = _cfg(E, 4, 2, K)
+    h = _x((m, 1, d), "mdev-b64")
+    gw = synth.randn((E, d), synth.seed_of("mdev-b64-router", E), 0.02).to(torch.bfloat16)
+    shared = _mlp(d, i, "mdev-b64-shared")
+    table = {e: _mlp(d, i, f"mdev-b64-{e}") for e in range(E)}
+    stacked = _stacked(table, E)
+    hd, gwd, shd = h.to(DEV), gw.to(DEV), _dev(shared)
+    dev_got = ops.moe_block(hd, gwd, shd, stacked, cfg)
+    host_got = ops.moe_block(hd, gwd, shd, stacked, cfg, device_grouping=False)
+    idx, _ = ops.route(hd, gwd, cfg)
+    torch.cuda.synchronize()
+    idx = idx.reshape(m, K).cpu()
+    counts = torch.bincount(idx.flatten(), minlength=E)
+    assert int(counts.max()) > 16, "some group should take the 17-64 row class"
+    assert_parity(dev_got, host_got, "moe_block batch 64: device vs host grouping")
+    got, hdr = _run_dev(h.reshape(m, d), idx, stacked, E, i)
+    assert hdr[0] == m * K and hdr[3] == 0
+    assert_parity(got, _want(h.reshape(m, d), idx, table), "moe_experts_dev batch 64 R1 shape")
+
+
+def test_device_table_not_reused_for_new_tensors_at_the_same_addresses():
+    """Two stacked expert sets in a row with the same E but a different intermediate size; the
+    first is freed before the second is made, so the allocator may hand out the same base
+    addresses: the second call must get its own pointer table (right per-expert steps)."""
+    print("[case] stacked device table keyed by shapes", flush=True)
+    E, K, m, d = 4, 2, 6, 256
+    h = _x((m, d), "mdev-key")
+    g = torch.Generator().manual_seed(5)
+    idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(m)])
+    for i in (256, 512):
+        table = {e: _mlp(d, i, f"mdev-key-{i}-{e}") for e in range(E)}
+        stacked = _stacked(table, E)
+        got, hdr = _run_dev(h, idx, stacked, E, i)
+        assert hdr[0] == m * K and hdr[3] == 0
+        assert_parity(got, _want(h, idx, table), f"moe_experts_dev n_inter={i}")
+        dtab, n_inter = ops._stacked_device_table(stacked, E, d, torch.device(DEV))
+        step = stacked["gate_proj"][0][0].numel()
+        assert n_inter == i
+        assert int(dtab[1]) - int(dtab[0]) == step
+        del stacked, table, dtab
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
 
 
 def test_moe_block_device_and_host_grouping_agree_with_the_oracle():

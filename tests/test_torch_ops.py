@@ -73,9 +73,36 @@ def test_linear_norm_rope_fake_shapes():
         w = torch.empty(1536, 7168, dtype=torch.float8_e4m3fn, device="cuda")
         s = torch.empty(12, 56, dtype=torch.float32, device="cuda")
         y = ops.fp8_linear(x, w, s)
+        y32 = ops.fp8_linear(x, w, s, out_dtype=torch.float32)
+        y16 = ops.fp8_linear(x, w, s, out_dtype=torch.float16)
+        gu = torch.empty(256, 7168, dtype=torch.float8_e4m3fn, device="cuda")
+        gs = torch.empty(2, 56, dtype=torch.float32, device="cuda")
+        dw = torch.empty(7168, 256, dtype=torch.float8_e4m3fn, device="cuda")
+        ds = torch.empty(56, 2, dtype=torch.float32, device="cuda")
+        sw = ops.swiglu(x, gu, gs, gu, gs, dw, ds)
         g = torch.empty(7168, dtype=torch.bfloat16, device="cuda")
         n = ops.rms_norm(x, g)
         q = torch.empty(2, 128, 4, 64, dtype=torch.bfloat16, device="cuda")
         f = torch.empty(4, 32, dtype=torch.complex64, device="cuda")
         r = ops.apply_rope(q, f)
     assert y.shape == (3, 1, 1536) and n.shape == x.shape and r.shape == q.shape
+    assert y32.dtype == torch.float32 and y16.dtype == torch.float16 and y32.shape == y.shape
+    assert sw.shape == x.shape and sw.dtype == torch.bfloat16
+
+
+def test_shims_read_no_data_pointer_of_fake_tensors():
+    """Alignment is checked inside the operators, on real tensors: tracing the linear and the
+    SwiGLU shims under FakeTensorMode warns about no data-pointer access."""
+    import warnings
+    mode = FakeTensorMode()
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        with mode:
+            x = torch.empty(2, 7168, dtype=torch.bfloat16, device="cuda")[:, :7168]
+            w = torch.empty(1536, 7168, dtype=torch.float8_e4m3fn, device="cuda")
+            s = torch.empty(12, 56, dtype=torch.float32, device="cuda")
+            ops.fp8_linear(x, w, s)
+            gu = torch.empty(256, 7168, dtype=torch.float8_e4m3fn, device="cuda")
+            gs = torch.empty(2, 56, dtype=torch.float32, device="cuda")
+            ops.swiglu(x, gu, gs, gu, gs, torch.empty(7168, 256, dtype=torch.float8_e4m3fn, device="cuda"),
+                       torch.empty(56, 2, dtype=torch.float32, device="cuda"))
