@@ -1118,9 +1118,13 @@ struct DecodeLayout {
   int units, slots;  // split budget (build_split_plan) and partial slots
 };
 
+// Sequences per decode launch sequence: a larger batch runs in chunks of this
+// many, one after another on the stream, sharing one workspace.
+constexpr int DECODE_MAX_BATCH = 64;
+
 static DecodeLayout decode_layout(const amla_mla_args &a) {
   DecodeLayout L = {};
-  const int B = a.batch;
+  const int B = std::min(a.batch, DECODE_MAX_BATCH);
   const int HD = a.qk_nope + a.qk_rope;
   L.pa = plan_gemv(B, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
   L.pb = plan_gemv(B, a.heads * HD, a.q_lora);
@@ -1185,11 +1189,35 @@ static inline void mark(hipEvent_t const *ev, int i, hipStream_t st) {
   if (ev) (void)hipEventRecord(ev[i], st);
 }
 
+static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const *ev);
+
 static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const *ev = nullptr) {
   int rc = check_mla_common(a, "mla_decode");
   if (rc) return rc;
   if (a->seq_len != 1) return fail(AMLA_EINVAL, "mla_decode: seq_len must be 1 (use mla_prefill)");
-  if (a->batch > 64) return fail(AMLA_EUNSUPPORTED, "mla_decode: batch > 64 not supported");
+  if (a->batch <= DECODE_MAX_BATCH) return decode_chunk(a, st, ev);
+  // inference/ops.py:119 takes any batch: chunks of DECODE_MAX_BATCH sequences
+  // in order on the stream (each chunk's launches finish before the next
+  // chunk's reuse the workspace)
+  for (int b0 = 0; b0 < a->batch; b0 += DECODE_MAX_BATCH) {
+    amla_mla_args c = *a;
+    c.batch = std::min(DECODE_MAX_BATCH, a->batch - b0);
+    const size_t row = (size_t)a->hidden * 2;
+    c.positions = a->positions + b0;
+    c.hidden_states = static_cast<const char *>(a->hidden_states) + (size_t)b0 * row;
+    c.out = static_cast<char *>(a->out) + (size_t)b0 * row;
+    if (a->residual) c.residual = static_cast<const char *>(a->residual) + (size_t)b0 * row;
+    if (a->attn_out) c.attn_out = static_cast<char *>(a->attn_out) + (size_t)b0 * a->heads * a->v_dim * 2;
+    c.ckv_cache = static_cast<char *>(a->ckv_cache) + (size_t)b0 * a->max_seq * a->kv_lora * 2;
+    c.kpe_cache = static_cast<char *>(a->kpe_cache) + (size_t)b0 * a->max_seq * a->qk_rope * 2;
+    if ((rc = decode_chunk(&c, st, ev))) return rc;
+  }
+  return AMLA_OK;
+}
+
+// One launch sequence for at most DECODE_MAX_BATCH sequences (args checked).
+static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const *ev) {
+  int rc = AMLA_OK;
   const DecodeLayout L = decode_layout(*a);
   if (a->workspace_bytes < L.total)
     return fail(AMLA_EWORKSPACE, "mla_decode: workspace %zu bytes < %zu needed", a->workspace_bytes, L.total);

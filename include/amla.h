@@ -105,8 +105,10 @@ typedef struct amla_mla_args {
   const void *hidden_states;  /* (B, S, hidden) bf16, already input-normed unless input_gamma */
   void *out;                  /* (B, S, hidden) bf16 */
   /* optional transformer_layer attention half (inference/forward.py:92-94):
-   * if input_gamma != NULL, hidden_states is normed with it first; if
-   * residual != NULL, out = residual + attention (bf16 add). */
+   * if input_gamma != NULL, hidden_states is normed with it first (in decode
+   * folded into the q_a|kv_a projection: bf16(x * input_gamma) projected, the
+   * sums scaled by the row's rsqrt(mean(x^2) + eps)); if residual != NULL,
+   * out = residual + attention (bf16 add). */
   const void *input_gamma;
   const void *residual;
   /* block-FP8 projections (weight e4m3fn row-major, scale_inv fp32) */
@@ -134,7 +136,9 @@ typedef struct amla_mla_args {
 
 /* Replaces mla_attention(...) for S == 1, inference/ops.py:100-183, computed in
  * absorbed form (q_nope.W_UK into latent space, scores on the raw latent +
- * rope cache, online softmax split over context, latent.W_UV back to heads). */
+ * rope cache, online softmax split over context, latent.W_UV back to heads).
+ * Any batch (ops.py:119): more than 64 sequences run as chunks of 64, one after
+ * another on the stream, in one workspace sized for 64. */
 int amla_mla_decode(const amla_mla_args *args, void *stream);
 
 /* Measurement hook with no counterpart in the reference: amla_mla_decode that

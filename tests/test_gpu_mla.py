@@ -13,7 +13,7 @@ from oracle import ref_ops as R
 from amla import ops, synth, torch_ops
 from amla._lib import lib
 from amla.config import DeepSeekConfig
-from _tol import assert_parity, assert_bf16_ulps
+from _tol import assert_bf16_ulps, assert_closer_than, assert_parity
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -76,6 +76,32 @@ def _check_cache(gc, rc, rows):
     assert torch.equal(gc[0][mask], rc[0][mask]) and torch.equal(gc[1][mask], rc[1][mask])
 
 
+def _check_layer_cache(gc, rc, hidden, gamma, aw, lo, hi):
+    """Cache rows written by the layer entry (input RMSNorm first).  Decode folds that norm into
+    the q_a|kv_a projection: it projects bf16(x * gamma) and scales the fp32 sums by the row's
+    rsqrt(mean(x^2) + eps), so the normed input is never rounded to bf16 as in
+    inference/ops.py:12.  The rows then agree with the oracle to the output tolerance (not to
+    2 bf16 ulps) and are about as close as the oracle (within 10%) to the float64 projection of the exactly
+    normed input."""
+    cfg = R1
+    x = hidden.double()
+    xn = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + cfg.rms_norm_eps) * gamma.double()
+    w = R.fp8_block_dequant(*aw["kv_a_proj_with_mqa"]).double()
+    kva = xn @ w.T
+    lora = cfg.kv_lora_rank
+    for i, what in ((0, "ckv rows"), (1, "kpe rows")):
+        got = gc[i][:, lo:hi].float()
+        want = rc[i][:, lo:hi].float()
+        assert_parity(got, want, f"layer {what}")
+        t = kva[..., :lora] if i == 0 else kva[..., lora:]
+        assert_closer_than(got, want, t, f"layer {what} vs fp64", factor=1.1)
+    # nothing else was touched
+    for i in (0, 1):
+        mask = torch.ones(gc[i].shape[:2], dtype=torch.bool)
+        mask[:, lo:hi] = False
+        assert torch.equal(gc[i][mask], rc[i][mask])
+
+
 def test_decode_t257(golden):
     got, want, gc, rc = _run_case("decode257", 1, 1, 256, 264)
     assert_parity(got, want, "decode B=1 T=257")
@@ -90,6 +116,77 @@ def test_decode_t257(golden):
         tab = R.precompute_rope_freqs(R1, e["max_seq"]).to(DEV)
         out = ops.mla_attention(hidden.to(DEV), _to_dev(lay.attn_weights), (ckv.to(DEV), kpe.to(DEV)), 256, tab, R1)
         assert_parity(out.cpu(), tens["r1_decode_t257.out"].view(torch.bfloat16), "decode vs reference golden")
+
+
+def test_prefill_s8_vs_reference_golden(golden):
+    """amla_mla_prefill on the inputs of the reference's own R1 prefill of 8 tokens
+    (tests/golden/make_golden.py wrote the reference's output and cache rows)."""
+    from test_oracle import _rebuild
+    tens, man = golden
+    e = man["r1_prefill_s8"]
+    print("[case] prefill S=8 vs reference golden", flush=True)
+    cfg, lay, hidden, ckv, kpe = _rebuild(e)
+    assert synth.sha256_of(hidden) == e["sha256"]["hidden"]
+    assert synth.sha256_of(lay.attn_weights["o_proj"][0]) == e["sha256"]["o_proj"]
+    tab = R.precompute_rope_freqs(cfg, e["max_seq"]).to(DEV)
+    c = (ckv.to(DEV), kpe.to(DEV))
+    out = ops.mla_attention(hidden.to(DEV), _to_dev(lay.attn_weights), c, e["position"], tab, cfg)
+    torch.cuda.synchronize()
+    assert_parity(out.cpu(), tens["r1_prefill_s8.out"].view(torch.bfloat16), "prefill S=8 vs reference golden")
+    p, S = e["position"], e["S"]
+    assert_bf16_ulps(c[0][:, p:p + S].cpu(), tens["r1_prefill_s8.ckv_new"].view(torch.bfloat16), 2, "ckv rows")
+    assert_bf16_ulps(c[1][:, p:p + S].cpu(), tens["r1_prefill_s8.kpe_new"].view(torch.bfloat16), 2, "kpe rows")
+
+
+@pytest.mark.parametrize("S,layer", [(1, False), (1, True), (40, False), (40, True)])
+def test_unit_gammas(S, layer):
+    """Every RMSNorm weight exactly 1 (q_a_layernorm, kv_a_layernorm and the layer's input norm):
+    the gamma folded into the absorbed query, the latent and the GEMM inputs is then the identity,
+    so this isolates the rest of each path."""
+    tag = f"gamma1/S{S}/L{int(layer)}"
+    print(f"[case] unit gammas S={S} layer={layer}", flush=True)
+    lay = synth.make_layer(R1, tag, gamma_mode="ones")
+    assert bool((lay.attn_weights["q_a_layernorm"].float() == 1).all())
+    B, pos, max_seq = 3, 300, 344
+    hidden = synth.make_hidden(R1, B, S, tag)
+    ckv, kpe = synth.make_kv_cache(R1, B, max_seq, pos, tag)
+    tab = _rope(max_seq)
+    rc = (ckv.clone(), kpe.clone())
+    if layer:
+        want = R.transformer_layer_attention(hidden, lay.input_layernorm, lay.attn_weights, rc, pos, tab, R1)
+    else:
+        want = R.mla_attention(hidden, lay.attn_weights, rc, pos, tab, R1)
+    gc = (ckv.to(DEV), kpe.to(DEV))
+    if layer:
+        got = ops.mla_layer(hidden.to(DEV), lay.input_layernorm.to(DEV), _to_dev(lay.attn_weights), gc, pos,
+                            tab.to(DEV), R1)
+    else:
+        got = ops.mla_attention(hidden.to(DEV), _to_dev(lay.attn_weights), gc, pos, tab.to(DEV), R1)
+    torch.cuda.synchronize()
+    assert_parity(got.cpu(), want, f"unit gammas S={S} layer={layer}")
+    gc = (gc[0].cpu(), gc[1].cpu())
+    if layer:
+        _check_layer_cache(gc, rc, hidden, lay.input_layernorm, lay.attn_weights, pos, pos + S)
+    else:
+        _check_cache(gc, rc, [(pos, pos + S)] * B)
+
+
+def test_decode_batch_above_64_runs_in_chunks():
+    """inference/ops.py:119 takes any batch: 70 sequences (a chunk of 64 and one of 6, the
+    workspace sized for 64) against the oracle."""
+    B, max_seq, pos = 70, 96, 80
+    got, want, gc, rc = _run_case("decode70", B, 1, pos, max_seq)
+    assert_parity(got, want, "decode B=70")
+    _check_cache(gc, rc, [(pos, pos + 1)] * B)
+    lay = _layer("mla/decode70")
+    hidden = synth.make_hidden(R1, B, 1, "decode70")
+    ckv, kpe = synth.make_kv_cache(R1, B, max_seq, pos, "decode70")
+    a = ops._mla_operands(hidden.to(DEV), _to_dev(lay.attn_weights), (ckv.to(DEV), kpe.to(DEV)), pos,
+                          _rope(max_seq).to(DEV), R1)
+    args = torch_ops.fill_mla_args(out=torch.empty_like(a["hidden"]), **a)
+    small = torch_ops.fill_mla_args(out=torch.empty_like(a["hidden"][:64]), **{**a, "hidden": a["hidden"][:64]})
+    assert lib().amla_mla_decode_workspace_bytes(ctypes.byref(args)) == \
+        lib().amla_mla_decode_workspace_bytes(ctypes.byref(small))
 
 
 def test_decode_t4096():
@@ -184,10 +281,12 @@ def test_prefill_chunk_after_cache():
 
 
 def test_layer_mode_decode_and_prefill():
-    got, want, _, _ = _run_case("layerdec", 2, 1, 700, 704, layer_mode=True)
-    assert_parity(got, want, "layer decode")
-    got, want, _, _ = _run_case("layerpre", 1, 96, 0, 96, layer_mode=True)
-    assert_parity(got, want, "layer prefill")
+    for tag, B, S, pos, max_seq in (("layerdec", 2, 1, 700, 704), ("layerpre", 1, 96, 0, 96)):
+        got, want, gc, rc = _run_case(tag, B, S, pos, max_seq, layer_mode=True)
+        assert_parity(got, want, f"layer {tag}")
+        lay = _layer("mla/" + tag)
+        _check_layer_cache(gc, rc, synth.make_hidden(R1, B, S, tag), lay.input_layernorm, lay.attn_weights,
+                           pos, pos + S)
 
 
 def test_prefill_row_equals_decode():
