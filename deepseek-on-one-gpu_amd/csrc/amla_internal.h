@@ -62,7 +62,7 @@ struct GemvPlan {
 };
 
 GemvPlan plan_gemv(int M, int N, int K);
-size_t gemv_lds_bytes(int MT, int kpb, int rg);  // MT = 16-row tiles of x (1, 2 or 4)
+size_t gemv_lds_bytes(int MT, int kpb, int rg, int kparts);  // MT = 16-row tiles of x (1, 2 or 4)
 // Launches the skinny GEMM for M <= 64 (N % 16 == 0, K % 128 == 0, 16-byte aligned rows);
 // p.part must hold plan.part_bytes when plan.kparts > 1.
 // finish = false leaves the fp32 K-part sums in p.part (plan.kparts > 1) for

@@ -177,11 +177,14 @@ __host__ __device__ inline int gemv_nbuf(int tile_bytes) { return tile_bytes >= 
 
 // LDS: [nbuf][16 rows][ceil4(kpb) * 128] weights |
 //      [2][4 waves][MT][64] f32x4 partial tiles | [rg][MT][64] f32x4 results
+// (not for 64-row x with K parts: there every thread of the workgroup holds
+// one fp32 sum of a reduced tile and stores it at once, so long units take no
+// more LDS).
 // x is held in registers: each wave's fragments of the MT 16-row tiles,
 // loaded once per workgroup (16 VGPRs per tile and 128-wide block of the
-// wave, at most 128 VGPRs: a K part of up to 16 blocks for MT <= 2, 8 for
-// MT = 4).
-__host__ __device__ constexpr int gemv_kpb_max(int MT) { return MT == 4 ? 8 : GEMV_KPB; }
+// wave: a K part of up to 16 blocks for MT <= 2 (128 VGPRs), 12 for MT = 4
+// (192 VGPRs, so that K = 1536 needs no K parts at 64 rows)).
+__host__ __device__ constexpr int gemv_kpb_max(int MT) { return MT == 4 ? 12 : GEMV_KPB; }
 __host__ __device__ inline int gemv_kpb4(int kpb) { return (kpb + 3) & ~3; }
 
 template <int MT, int MODE>
@@ -332,13 +335,19 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
       v += rb[(1 * MT + t) * 64 + ln];
       v += rb[(2 * MT + t) * 64 + ln];
       v += rb[(3 * MT + t) * 64 + ln];
-      done[(it * MT + t) * 64 + ln] = v;
+      if (MT < 4 || kparts == 1) {
+        done[(it * MT + t) * 64 + ln] = v;
+      } else {  // 64-row x, K parts: every thread holds one fp32 sum of the tile, stored at once (no LDS held)
+        const int m = t * 16 + (ln & 15);
+        if (m < p.M) *reinterpret_cast<f32x4 *>(p.part + ((size_t)part * p.M + m) * p.N + nt + 4 * (ln >> 4)) = v;
+      }
     }
     // red[it & 1] is rewritten two tiles later, after the next two barriers
   }
   lds_barrier();
-  // results of the unit: epilogue (one K part) or fp32 partial sums
-  const int nitems = (tile_end - tile_begin) * MT * 64;
+  // results of the unit: epilogue (one K part) or fp32 partial sums (64-row
+  // x with K parts stored them per tile)
+  const int nitems = MT < 4 || kparts == 1 ? (tile_end - tile_begin) * MT * 64 : 0;
   for (int idx = tid; idx < nitems; idx += 256) {
     const int tl = idx / (MT * 64), t = (idx >> 6) % MT, ln = idx & 63;
     const int m = t * 16 + (ln & 15);
@@ -352,7 +361,7 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
 }
 
 template <int MT, int MODE>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kparts, int kpb) {
+__global__ __launch_bounds__(256, 2) void gemv_kernel(GemvParams p, int rg, int kparts, int kpb) {
   gemv_body<MT, MODE>(p, blockIdx.x, rg, kparts, kpb);
 }
 
@@ -360,7 +369,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p, int rg, int kpa
 // takes workgroups [g * units, (g + 1) * units) with its own x, weights, M,
 // output and partial-sum buffer (routed experts of a MoE layer).
 template <int MT>
-__global__ __launch_bounds__(256) void gemv_grouped_kernel(GemvParams p, GemvGroups gr, int rg, int kparts, int kpb) {
+__global__ __launch_bounds__(256, 2) void gemv_grouped_kernel(GemvParams p, GemvGroups gr, int rg, int kparts, int kpb) {
   const int g = blockIdx.x / gr.units;
   GemvParams q = p;
   q.x = gr.g[g].x;
@@ -374,9 +383,10 @@ __global__ __launch_bounds__(256) void gemv_grouped_kernel(GemvParams p, GemvGro
   gemv_body<MT, GEMV_PLAIN>(q, blockIdx.x % gr.units, rg, kparts, kpb);
 }
 
-size_t gemv_lds_bytes(int MT, int kpb, int rg) {
+size_t gemv_lds_bytes(int MT, int kpb, int rg, int kparts) {
   const int tile = 16 * gemv_kpb4(kpb) * 128;
-  return (size_t)gemv_nbuf(tile) * tile + 2 * 4 * MT * 64 * 16 + (size_t)rg * MT * 64 * 16;
+  return (size_t)gemv_nbuf(tile) * tile + 2 * 4 * MT * 64 * 16 +
+         (MT < 4 || kparts == 1 ? (size_t)rg * MT * 64 * 16 : 0);
 }
 
 // Sums the K parts of gemv_kernel in part order and applies the epilogue.
@@ -416,7 +426,7 @@ __global__ __launch_bounds__(64) void gemv_finish_grouped(GemvParams p, GemvGrou
 // Skinny GEMMs of a device schedule (routed experts): entry g = blockIdx.x /
 // units; entries past the device count return at once (uniform per workgroup).
 template <int MT>
-__global__ __launch_bounds__(256) void gemv_sched_kernel(GemvParams p, MoeSched s, int units, int rg, int kparts,
+__global__ __launch_bounds__(256, 2) void gemv_sched_kernel(GemvParams p, MoeSched s, int units, int rg, int kparts,
                                                          int kpb) {
   const int g = blockIdx.x / units;
   if (g >= *s.count) return;
@@ -553,8 +563,8 @@ GemvPlan plan_gemv(int M, int N, int K) {
   constexpr size_t LDS_MAX = 160 * 1024;
   // rows of K >= 2048 (o_proj, the FFN and expert projections) take 16 KB
   // tiles (more K parts, two workgroups per CU): measured faster than 32 KB
-  int kmax = K >= 2048 ? 8 : gemv_kpb_max(MT);
-  while (kmax > 4 && gemv_lds_bytes(MT, kmax, 1) > LDS_MAX) kmax -= 4;
+  int kmax = K >= 2048 && MT < 4 ? 8 : gemv_kpb_max(MT);
+  while (kmax > 4 && gemv_lds_bytes(MT, kmax, 1, 1) > LDS_MAX) kmax -= 4;
   int kpb = KB <= kmax ? KB : 0;
   if (!kpb) {
     for (int c = kmax; c >= 4; c -= 4)
@@ -565,16 +575,18 @@ GemvPlan plan_gemv(int M, int N, int K) {
   pl.kparts = (KB + kpb - 1) / kpb;
   // tiles per unit: fewest rounds of the workgroups the machine holds (256,
   // or 512 when two fit one CU's LDS: measured faster for q_a | kv_a and q_b,
-  // whose units then run two per CU) x (tiles per unit + one tile's worth of
-  // per-workgroup start-up), then the largest unit (fewer x stagings), within
-  // the LDS budget
+  // whose units then run two per CU) x (tiles per unit + the per-workgroup
+  // start-up: one tile's worth, four for 64-row x, whose fragments are eight
+  // weight tiles' worth of bytes), then the largest unit (fewer x stagings),
+  // within the LDS budget
+  const int startup = MT == 4 ? 4 : 1;
   int best_rg = 1;
   int64_t best_cost = INT64_MAX;
   for (int rg = 1; rg <= GEMV_MAX_RG; ++rg) {
-    if (gemv_lds_bytes(MT, kpb, rg) > LDS_MAX) break;
+    if (gemv_lds_bytes(MT, kpb, rg, pl.kparts) > LDS_MAX) break;
     const int64_t units = (int64_t)((tiles + rg - 1) / rg) * pl.kparts;
-    const int64_t slots = 256 * std::min<int64_t>(2, LDS_MAX / gemv_lds_bytes(MT, kpb, rg));
-    const int64_t cost = ((units + slots - 1) / slots) * (rg + 1);
+    const int64_t slots = 256 * std::min<int64_t>(2, LDS_MAX / gemv_lds_bytes(MT, kpb, rg, pl.kparts));
+    const int64_t cost = ((units + slots - 1) / slots) * (rg + startup);
     if (cost <= best_cost) {
       best_cost = cost;
       best_rg = rg;
@@ -582,7 +594,7 @@ GemvPlan plan_gemv(int M, int N, int K) {
   }
   pl.rg = best_rg;
   pl.groups = ((tiles + pl.rg - 1) / pl.rg) * pl.kparts;
-  pl.lds = gemv_lds_bytes(MT, kpb, pl.rg);
+  pl.lds = gemv_lds_bytes(MT, kpb, pl.rg, pl.kparts);
   pl.part_bytes = pl.kparts > 1 ? (size_t)pl.kparts * M * N * 4 : 0;
   return pl;
 }
@@ -594,11 +606,11 @@ GemvPlan plan_gemv_grouped(int M, int N, int K) {
   const int MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   const int tiles = N / 16;
   int rg = std::min(GEMV_MAX_RG, tiles);
-  while (rg > pl.rg && gemv_lds_bytes(MT, pl.kpb, rg) > 160 * 1024) --rg;
+  while (rg > pl.rg && gemv_lds_bytes(MT, pl.kpb, rg, pl.kparts) > 160 * 1024) --rg;
   if (rg > pl.rg) {
     pl.rg = rg;
     pl.groups = ((tiles + rg - 1) / rg) * pl.kparts;
-    pl.lds = gemv_lds_bytes(MT, pl.kpb, rg);
+    pl.lds = gemv_lds_bytes(MT, pl.kpb, rg, pl.kparts);
   }
   return pl;
 }
@@ -639,7 +651,7 @@ int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t 
   if (p0.w1 && p0.n_split % 128)
     return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM: the first weight segment must be a multiple of 128 rows");
   const int MT = p0.M <= 16 ? 1 : (p0.M <= 32 ? 2 : 4);
-  if (pl.kpb > gemv_kpb_max(MT) || gemv_lds_bytes(MT, pl.kpb, pl.rg) > pl.lds)
+  if (pl.kpb > gemv_kpb_max(MT) || gemv_lds_bytes(MT, pl.kpb, pl.rg, pl.kparts) > pl.lds)
     return fail(AMLA_EINVAL, "skinny fp8 GEMM: plan for a smaller M");
   if (MT == 1) launch_mt<1>(p0, mode, pl, st);
   else if (MT == 2) launch_mt<2>(p0, mode, pl, st);
@@ -680,7 +692,7 @@ int launch_gemv_grouped(const GemvParams &p, GemvGroups gr, const GemvPlan &pl, 
   if (p.N % 16 || p.K % 128 || pl.kparts > GEMV_MAX_PARTS || (p.w1 && p.n_split % 128))
     return fail(AMLA_EUNSUPPORTED, "grouped skinny GEMM: unsupported shape N=%d K=%d", p.N, p.K);
   const int MT = max_m <= 16 ? 1 : (max_m <= 32 ? 2 : 4);
-  if (gemv_lds_bytes(MT, pl.kpb, pl.rg) > pl.lds || pl.kpb > gemv_kpb_max(MT))
+  if (gemv_lds_bytes(MT, pl.kpb, pl.rg, pl.kparts) > pl.lds || pl.kpb > gemv_kpb_max(MT))
     return fail(AMLA_EINVAL, "grouped skinny GEMM: plan for a smaller M");
   gr.units = pl.groups;
   if (MT == 1) launch_grouped_mt<1>(p, gr, pl, st);
@@ -715,7 +727,7 @@ int launch_gemv_sched(const GemvParams &p, const MoeSched &s, int max_entries, i
     return fail(AMLA_EUNSUPPORTED, "scheduled skinny GEMM: unsupported shape N=%d K=%d", p.N, p.K);
   if (pl.kparts > 1 && !p.part) return fail(AMLA_EWORKSPACE, "scheduled skinny GEMM: missing partial sums");
   const int MT = max_m <= 16 ? 1 : (max_m <= 32 ? 2 : 4);
-  if (gemv_lds_bytes(MT, pl.kpb, pl.rg) > pl.lds || pl.kpb > gemv_kpb_max(MT))
+  if (gemv_lds_bytes(MT, pl.kpb, pl.rg, pl.kparts) > pl.lds || pl.kpb > gemv_kpb_max(MT))
     return fail(AMLA_EINVAL, "scheduled skinny GEMM: plan for a smaller M");
   if ((int64_t)max_entries * pl.groups > INT32_MAX) return fail(AMLA_EUNSUPPORTED, "scheduled skinny GEMM: grid");
   if (MT == 1) launch_sched_mt<1>(p, s, max_entries, pl, st);
