@@ -329,19 +329,22 @@ constexpr float REF_HEADROOM_SUM = 18446744073709551616.f;  // 2^64
 // tile's parity.  The tile loop issues one piece per score step: a burst of
 // LDS copies stalls the issuing wave for tens of cycles per copy.
 AMLA_DEV void dma_piece(const AttnParams &p, int b, int tile, int parity, int T, uint8_t *smem, uint8_t *stage,
-                        int wave, int lane, int piece) {
+                        int wave, int lane, uint32_t lane16, int piece) {
   const int t0 = tile * TT + wave * 8;
+  if (piece < 8) {
+    // one row: the clamp is on the scalar row index, every lane at lane16 = 16 * lane
+    const char *cb = reinterpret_cast<const char *>(p.ckv + (size_t)b * p.ckv_bstride);
+    const int t = min(t0 + piece, T - 1);
+    __builtin_amdgcn_global_load_lds(cb + (size_t)t * (LORA * 2) + lane16,
+                                     LDS_PTR(stage + (wave * 8 + piece) * (KROW * 2)), 16, 0, 0);
+    return;
+  }
   const int t0c = min(t0, T - 1);
   // lane-derived offsets are unsigned (scalar base + 32-bit lane offset
   // addressing) and recomputed per copy, not held across the loop
   uint32_t ln;
   asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
-  if (piece < 8) {
-    const char *cb = reinterpret_cast<const char *>(p.ckv + (size_t)b * p.ckv_bstride);
-    const int t = min(t0 + piece, T - 1);
-    __builtin_amdgcn_global_load_lds(cb + (size_t)t * (LORA * 2) + ln * 16u,
-                                     LDS_PTR(stage + (wave * 8 + piece) * (KROW * 2)), 16, 0, 0);
-  } else if (piece == 8) {
+  if (piece == 8) {
     const char *kb = reinterpret_cast<const char *>(p.kpe + (size_t)b * p.kpe_bstride) + (size_t)t0c * (ROPE * 2);
     const uint32_t row = static_cast<uint32_t>(min(t0 + static_cast<int>(ln >> 3), T - 1) - t0c);
     __builtin_amdgcn_global_load_lds(kb + row * (ROPE * 2) + (ln & 7u) * 16u, LDS_PTR(stage + K_BYTES + wave * 1024), 16,
@@ -358,7 +361,8 @@ AMLA_DEV void dma_piece(const AttnParams &p, int b, int tile, int parity, int T,
 
 AMLA_DEV void dma_tile(const AttnParams &p, int b, int tile, int T, uint8_t *smem, uint8_t *stage, int wave, int lane) {
 #pragma unroll
-  for (int piece = 0; piece < TILE_DMA; ++piece) dma_piece(p, b, tile, tile, T, smem, stage, wave, lane, piece);
+  for (int piece = 0; piece < TILE_DMA; ++piece)
+    dma_piece(p, b, tile, tile, T, smem, stage, wave, lane, static_cast<uint32_t>(lane) * 16u, piece);
 }
 
 AMLA_DEV uint32_t rot_pair(uint32_t x, float c, float s) {
@@ -494,6 +498,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   const int te = split_tile(nb, ns, split + 1);
   extern __shared__ __align__(16) uint8_t smem[];
   const int head0 = wave * 32;
+  const uint32_t lane16 = static_cast<uint32_t>(lane) * 16u;  // the copies' lane offset inside the context
 
   // query fragments (B operand: head = column l%16, K = 8*lg .. of each 32-wide step)
   bf16x8 qf[2][QKD / 32];
@@ -681,7 +686,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
         // tile is copied again (an L2 hit) into a stage nothing reads any more;
         // the table block is the parity of tile + 2, never the one the
         // preparation of tile + 1 reads
-        if (ks < TILE_DMA) dma_piece(p, b, min(tile + 2, te - 1), tile + 2, T, smem, nst, wave, lane, ks);
+        if (ks < TILE_DMA) dma_piece(p, b, min(tile + 2, te - 1), tile + 2, T, smem, nst, wave, lane, lane16, ks);
       }
       // the softmax reads sc: MFMA write -> VALU read wait states
       asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sc[0][0]), "+v"(sc[0][1]), "+v"(sc[1][0]), "+v"(sc[1][1])::"memory");
