@@ -163,12 +163,14 @@ AMLA_DEV void build_split_plan(const int32_t *__restrict__ pos, int tmax, int B,
 
 // ---------------------------------------------------------------- absorb
 
-// One workgroup per (head, 128-column quarter of the latent, group of 8
-// sequences), and workgroup (HEADS, 0, 0) writes the split plan table of a
-// batch with unequal tile counts.  Thread (dg, cc) sums rows 8*dg .. 8*dg+7 of W_UK[h] (eight
+// One workgroup per (head, 128-column quarter of the latent, group of BB
+// sequences; BB = 1, 2, 4 or 8, the smallest that holds the batch up to 8),
+// and workgroup (HEADS, 0, 0) writes the split plan table of a batch with
+// unequal tile counts.  Thread (dg, cc) sums rows 8*dg .. 8*dg+7 of W_UK[h] (eight
 // independent 8-byte loads in flight) for 8 latent columns; the 16 row groups
 // reduce through LDS.  W_UK[h] = kv_b rows h*256 .. h*256+127 lie in one
 // 128-row scale block.
+template <int BB>
 __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict__ q,  // (B, H, 192)
                                                      const uint8_t *__restrict__ wkvb,
                                                      const float *__restrict__ skvb,
@@ -176,9 +178,9 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
                                                      int B, uint16_t *__restrict__ qbuf,
                                                      const int32_t *__restrict__ pos, int tmax, int units,
                                                      int slots, int32_t *__restrict__ plan) {
-  constexpr int BB = 8;
   __shared__ float qn[BB][NOPE];
   __shared__ f32x4 red[16][BB][16][2];
+  static_assert(sizeof(red) >= (2 * 64 + 4) * sizeof(int), "the plan's scratch (batch <= 64) fits red");
   if (blockIdx.x >= HEADS) {
     if (blockIdx.x == HEADS && blockIdx.y == 0 && blockIdx.z == 0) {
       const int2 r = batch_tile_range(pos, tmax, B);
@@ -1292,9 +1294,22 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   // past HEADS return at once; a row length that is a multiple of 8 keeps the
   // quarters of head h on one XCD (workgroup i runs on XCD i mod 8), where
   // they share its query rows in L2
-  absorb_kernel<<<dim3(HEADS + 8, LORA / 128, (B + 7) / 8), 256, 0, st>>>(
-      q, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv),
-      B, qbuf, a->positions, tmax, L.units, L.slots, plan);
+  {
+    const uint8_t *wkvb = reinterpret_cast<const uint8_t *>(a->w_kv_b);
+    const uint16_t *gkv = reinterpret_cast<const uint16_t *>(a->gamma_kv);
+    if (B == 1)
+      absorb_kernel<1><<<dim3(HEADS + 8, LORA / 128, 1), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions,
+                                                                       tmax, L.units, L.slots, plan);
+    else if (B == 2)
+      absorb_kernel<2><<<dim3(HEADS + 8, LORA / 128, 1), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions,
+                                                                       tmax, L.units, L.slots, plan);
+    else if (B <= 4)
+      absorb_kernel<4><<<dim3(HEADS + 8, LORA / 128, 1), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions,
+                                                                       tmax, L.units, L.slots, plan);
+    else
+      absorb_kernel<8><<<dim3(HEADS + 8, LORA / 128, (B + 7) / 8), 256, 0, st>>>(
+          q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions, tmax, L.units, L.slots, plan);
+  }
   if ((rc = check_launch("mla absorb"))) return rc;
 
   // 5. attention over the latent cache, split over context
