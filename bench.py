@@ -143,14 +143,19 @@ def decode_stage_times(stack, caches, hidden, pos, rope, ctx, reps=2):
 def attn_traffic(B, T):
     """Measured HBM bytes per attention launch (FETCH_SIZE + WRITE_SIZE, each
     scaled by the same counters on a copy of known size), read from the
-    committed counter summary of this workload; None when there is none."""
+    committed counter summary of this workload, with the source tree the
+    counters were taken on; (None, None) when there is none.  A counter pass
+    serialises the dispatches, so it is a separate run of the same kernels,
+    not a measurement of this one."""
     import re
     path = os.path.join(ROOT, "profiles", f"attn_kernel_b{B}_ctx{T}_traffic.md")
     try:
-        m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", open(path).read())
+        text = open(path).read()
     except OSError:
-        return None
-    return int(m.group(1)) if m else None
+        return None, None
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", text)
+    c = re.search(r"source tree:\s*(\S+)", text)
+    return (int(m.group(1)) if m else None), (c.group(1) if c else None)
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -516,6 +521,7 @@ def main():
     overlap = {} if args.no_extras else overlap_extra(time_graph.last, dev)
     time_graph.last = None
     stages = decode_stage_times(stack, caches, hidden, pos, rope, T)
+    traffic, traffic_tree = attn_traffic(B, T)
     attn_bytes = B * T * ROW_BYTES
     attn_ms = stages["attention"]
     achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
@@ -569,13 +575,13 @@ def main():
         "decode_stage_ms": {k: round(v, 4) for k, v in stages.items()},
         "roofline": {"kernel": "attn_kernel (latent-cache attention, split over context)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": attn_traffic(B, T),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": attn_bytes, "avg_ms": round(attn_ms, 4),
                      "avg_ms_source": "HIP events recorded on attn_kernel's launch stream around each launch "
                                       "(eager decode of every layer, twice), mean",
-                     "traffic_source": f"profiles/attn_kernel_b{B}_ctx{T}_traffic.md: rocprofv3 --pmc FETCH_SIZE "
-                                       "and WRITE_SIZE of this workload, each scaled by the same counter on a "
-                                       "1 GiB device copy"},
+                     "traffic_source": f"committed counter summary profiles/attn_kernel_b{B}_ctx{T}_traffic.md "
+                                       f"(source tree {traffic_tree}): rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
+                                       "of this workload, each scaled by the same counter on a 1 GiB device copy"},
         **extras,
     }
     if not args.no_cpu_baseline:
