@@ -50,6 +50,8 @@ struct GemvParams {
   const float *rope_table;
   int head_dim, nope;   // QROPE
   float *part;          // fp32 partial sums of the K parts (GemvPlan::part_bytes), else unused
+  int xnorm;            // streaming GEMV only: x is the raw input and every sum of its row is multiplied
+  float eps_in;         // by rsqrt(mean(x^2) + eps_in) (the input RMSNorm folded, xg carrying its gamma)
 };
 
 struct GemvPlan {
@@ -59,9 +61,14 @@ struct GemvPlan {
   int groups;        // workgroups
   size_t lds;        // dynamic LDS bytes per workgroup
   size_t part_bytes; // fp32 partial sums (kparts * M * N * 4) when kparts > 1
+  int vec;           // 1: the streaming GEMV for one row of x (vgemv_kernel), no K parts
 };
 
 GemvPlan plan_gemv(int M, int N, int K);
+// plan_gemv, or the streaming GEMV (vec = 1) where it applies: one row of x,
+// 4096 <= K <= 16384 (K % 128 == 0), N % 8 == 0.  For launch_gemv only (the
+// grouped and scheduled launches take plan_gemv plans).
+GemvPlan plan_linear(int M, int N, int K);
 size_t gemv_lds_bytes(int MT, int kpb, int rg, int kparts);  // MT = 16-row tiles of x (1, 2 or 4)
 // Launches the skinny GEMM for M <= 64 (N % 16 == 0, K % 128 == 0, 16-byte aligned rows);
 // p.part must hold plan.part_bytes when plan.kparts > 1.

@@ -125,7 +125,7 @@ static int fp8_linear_into(const uint16_t *x, int m, int k, const uint8_t *w, co
   p.ldy = n;
   p.seq_len = 1;
   if (m > 64) return launch_gemm(p, GEMV_PLAIN, st);
-  const GemvPlan pl = plan_gemv(m, n, k);
+  const GemvPlan pl = plan_linear(m, n, k);
   p.part = part;
   return launch_gemv(p, GEMV_PLAIN, pl, st);
 }
@@ -144,7 +144,7 @@ static SwigluLayout swiglu_layout(int64_t m, int64_t k, int64_t n) {
   off = align_up(off + (size_t)m * n * 2, 256);
   size_t part = 0;
   if (m <= 64 && m > 0)
-    part = std::max(plan_gemv((int)m, (int)(2 * n), (int)k).part_bytes, plan_gemv((int)m, (int)k, (int)n).part_bytes);
+    part = std::max(plan_linear((int)m, (int)(2 * n), (int)k).part_bytes, plan_linear((int)m, (int)k, (int)n).part_bytes);
   L.part = off;
   off = align_up(off + part, 256);
   L.total = off;
@@ -227,7 +227,7 @@ int amla_swiglu(const void *x, int64_t m, int64_t k, const void *gate_w, const f
     rc = launch_gemm(a, GEMV_PLAIN, st);
     if (!rc) rc = launch_gemm(b, GEMV_PLAIN, st);
   } else {
-    const GemvPlan pl = plan_gemv((int)m, (int)(2 * n), (int)k);
+    const GemvPlan pl = plan_linear((int)m, (int)(2 * n), (int)k);
     if (pl.kparts > 1) {
       // the K-part finish and silu * up in one pass (n % 128 == 0)
       if ((rc = launch_gemv(p, GEMV_PLAIN, pl, st, false))) return rc;

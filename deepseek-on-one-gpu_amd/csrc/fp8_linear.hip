@@ -553,7 +553,7 @@ int launch_qkva_finish_norm(const GemvParams &p, int kparts, const uint16_t *gam
 }
 
 GemvPlan plan_gemv(int M, int N, int K) {
-  GemvPlan pl;
+  GemvPlan pl = {};
   const int tiles = N / 16;
   const int KB = K / 128;
   const int MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
@@ -615,6 +615,172 @@ GemvPlan plan_gemv_grouped(int M, int N, int K) {
   return pl;
 }
 
+// ---------------------------------------------------------------- streaming GEMV, one row of x
+
+// With one row of x the MFMA tiles above use 1/16 of their columns and the
+// weight stream pays for LDS staging, barriers and K-part partial sums.  Here
+// a workgroup (256 threads) owns VG_ROWS weight rows over the whole K:
+//   * thread t takes the 16-byte fp8 chunks t, t + 256, .. (NCH of them) of
+//     every row, loaded straight into registers (all VG_ROWS x NCH in flight)
+//     from one contiguous 1 KB span per wave and row;
+//   * each chunk is converted exactly to bf16 pairs and dotted with the
+//     thread's x chunk in fp32 (v_dot2_f32_bf16), then scaled by its 128x128
+//     block's scale_inv (a chunk never straddles a block), like the MFMA path;
+//   * the rows reduce over the workgroup (lane swaps inside each wave, the
+//     four waves through LDS) and two threads store the rows through the
+//     GEMV epilogue (store4), so no finishing pass is needed.
+// Optional input RMSNorm fold (p.xnorm): the workgroup holds the whole x row,
+// so it also sums x^2 and multiplies every result by rsqrt(mean(x^2) + eps_in).
+constexpr int VG_ROWS = 8;
+
+template <int CTRL>
+AMLA_DEV float vg_dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// sum over the 64 lanes of a wave, in every lane
+AMLA_DEV float vg_sum64(float v) {
+  v += vg_dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += vg_dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += vg_dpp<0x141>(v);  // row_half_mirror
+  v += vg_dpp<0x140>(v);  // row_mirror
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int NCH, int MODE>
+__global__ __launch_bounds__(256) void vgemv_kernel(GemvParams p) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * VG_ROWS;
+  const int C = p.K >> 4;  // 16-byte chunks per weight row
+  const int KB = p.K >> 7;
+  const bool seg1 = (MODE == GEMV_QKVA || p.w1) && n0 >= p.n_split;
+  const int r0 = seg1 ? n0 - p.n_split : n0;  // VG_ROWS rows inside one segment and one 128-row scale block
+  const uint8_t *wb = (seg1 ? p.w1 : p.w0) + (size_t)r0 * p.K;
+  const float *sb = (seg1 ? p.s1 : p.s0) + (size_t)(r0 >> 7) * KB;
+
+  // every chunk of the workgroup's rows in flight first
+  u32x4 w[VG_ROWS][NCH];
+#pragma unroll
+  for (int r = 0; r < VG_ROWS; ++r)
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = tid + 256 * j;
+      w[r][j] = c < C ? ldg16(wb + (size_t)r * p.K + c * 16) : u32x4{0, 0, 0, 0};
+    }
+  // this thread's chunks of x (16 bf16 each) and their block scales
+  u32x4 xa[NCH][2];
+  float sc[NCH];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = tid + 256 * j;
+    const bool ok = c < C;
+    xa[j][0] = ok ? ldg16(p.x + c * 16) : u32x4{0, 0, 0, 0};
+    xa[j][1] = ok ? ldg16(p.x + c * 16 + 8) : u32x4{0, 0, 0, 0};
+    sc[j] = ok ? sb[c >> 3] : 0.f;
+    if (p.xnorm) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          ss += lo_bf(xa[j][h][e]) * lo_bf(xa[j][h][e]) + hi_bf(xa[j][h][e]) * hi_bf(xa[j][h][e]);
+    }
+    if (p.xg && ok) {  // the GEMM takes bf16(x * g) (the folded input RMSNorm's gamma)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const u32x4 g = ldg16(p.xg + c * 16 + 8 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xa[j][h][e] = pack_bf16(lo_bf(xa[j][h][e]) * lo_bf(g[e]), hi_bf(xa[j][h][e]) * hi_bf(g[e]));
+      }
+    }
+  }
+
+  float acc[VG_ROWS];
+#pragma unroll
+  for (int r = 0; r < VG_ROWS; ++r) {
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bf16x2_t w01 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[r][j][e], 1.f, false);
+        const bf16x2_t w23 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[r][j][e], 1.f, true);
+        // bytes 4e .. 4e+3 of the chunk are elements 4e .. 4e+3: x pairs (4e, 4e+1), (4e+2, 4e+3)
+        const uint32_t x01 = xa[j][e >> 1][(e & 1) * 2], x23 = xa[j][e >> 1][(e & 1) * 2 + 1];
+        d = __builtin_amdgcn_fdot2_f32_bf16(w01, __builtin_bit_cast(bf16x2_t, x01), d, false);
+        d = __builtin_amdgcn_fdot2_f32_bf16(w23, __builtin_bit_cast(bf16x2_t, x23), d, false);
+      }
+      a = __builtin_fmaf(sc[j], d, a);
+    }
+    acc[r] = a;
+  }
+
+  __shared__ float red[4][VG_ROWS + 1];
+#pragma unroll
+  for (int r = 0; r < VG_ROWS; ++r) acc[r] = vg_sum64(acc[r]);
+  if (p.xnorm) ss = vg_sum64(ss);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < VG_ROWS; ++r) red[wave][r] = acc[r];
+    red[wave][VG_ROWS] = ss;
+  }
+  __syncthreads();
+  if (tid < VG_ROWS / 4) {
+    float rin = 1.f;
+    if (p.xnorm) rin = rsqrtf(((red[0][VG_ROWS] + red[1][VG_ROWS]) + (red[2][VG_ROWS] + red[3][VG_ROWS])) / (float)p.K +
+                           p.eps_in);
+    f32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * tid + i;
+      v[i] = ((red[0][r] + red[1][r]) + (red[2][r] + red[3][r])) * rin;
+    }
+    store4<MODE>(p, 0, n0 + 4 * tid, v);
+  }
+}
+
+template <int NCH>
+static void launch_vgemv_mode(const GemvParams &p, int mode, hipStream_t st) {
+  const unsigned groups = (unsigned)(p.N / VG_ROWS);
+  switch (mode) {
+    case GEMV_PLAIN: vgemv_kernel<NCH, GEMV_PLAIN><<<groups, 256, 0, st>>>(p); break;
+    case GEMV_RESID: vgemv_kernel<NCH, GEMV_RESID><<<groups, 256, 0, st>>>(p); break;
+    case GEMV_QKVA: vgemv_kernel<NCH, GEMV_QKVA><<<groups, 256, 0, st>>>(p); break;
+    case GEMV_F32: vgemv_kernel<NCH, GEMV_F32><<<groups, 256, 0, st>>>(p); break;
+    default: vgemv_kernel<NCH, GEMV_QROPE><<<groups, 256, 0, st>>>(p); break;
+  }
+}
+
+static bool vgemv_applies(int M, int N, int K) { return M == 1 && K % 128 == 0 && K >= 4096 && K <= 16384 && N % 8 == 0; }
+
+GemvPlan plan_linear(int M, int N, int K) {
+  if (!vgemv_applies(M, N, K)) return plan_gemv(M, N, K);
+  GemvPlan pl = {};
+  pl.kpb = K / 128;
+  pl.kparts = 1;
+  pl.rg = 1;
+  pl.groups = N / VG_ROWS;
+  pl.vec = 1;
+  return pl;
+}
+
+static int launch_vgemv(const GemvParams &p, int mode, hipStream_t st) {
+  if (!vgemv_applies(p.M, p.N, p.K) || p.ldx < p.K || (p.w1 || mode == GEMV_QKVA ? p.n_split % 128 : 0) ||
+      !aligned16(p.x) || (p.xg && !aligned16(p.xg)))
+    return fail(AMLA_EINVAL, "streaming fp8 GEMV: plan for another shape (M=%d N=%d K=%d)", p.M, p.N, p.K);
+  const int C = p.K >> 4;
+  if (C <= 256) launch_vgemv_mode<1>(p, mode, st);
+  else if (C <= 512) launch_vgemv_mode<2>(p, mode, st);
+  else launch_vgemv_mode<4>(p, mode, st);
+  return check_launch("fp8 streaming GEMV");
+}
+
 template <int MT, int MODE>
 static int launch_cfg(const GemvParams &p, const GemvPlan &pl, hipStream_t st) {
   static bool attr_set = false;  // raise the dynamic LDS limit once per process
@@ -639,6 +805,7 @@ static void launch_mt(const GemvParams &p, int mode, const GemvPlan &pl, hipStre
 }
 
 int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t st, bool finish) {
+  if (pl.vec) return launch_vgemv(p0, mode, st);
   if (p0.M < 1 || p0.M > 64) return fail(AMLA_EINVAL, "skinny fp8 GEMM needs 1 <= M <= 64 (got %d)", p0.M);
   if (p0.N % 16 || p0.K % 128)
     return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM needs N %% 16 == 0 and K %% 128 == 0 (N=%d K=%d)", p0.N, p0.K);
@@ -862,7 +1029,7 @@ int amla_fp8_block_dequant(const void *weight, const float *scale_inv, int64_t n
 
 size_t amla_fp8_linear_workspace_bytes(int64_t m, int64_t n, int64_t k) {
   if (m < 1 || m > 64 || n <= 0 || k <= 0 || n % 16 || k % 128 || n > INT32_MAX || k > INT32_MAX) return 0;
-  return plan_gemv((int)m, (int)n, (int)k).part_bytes;
+  return plan_linear((int)m, (int)n, (int)k).part_bytes;
 }
 
 int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void *weight,
@@ -892,7 +1059,7 @@ int amla_fp8_linear(const void *x, int64_t m, int64_t k, int64_t ldx, const void
   p.seq_len = 1;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (m > 64) return launch_gemm(p, GEMV_PLAIN, st);
-  const GemvPlan pl = plan_gemv((int)m, (int)n, (int)k);
+  const GemvPlan pl = plan_linear((int)m, (int)n, (int)k);
   if (pl.part_bytes) {
     if (!workspace || workspace_bytes < pl.part_bytes || !aligned16(workspace))
       return fail(AMLA_EWORKSPACE, "fp8_linear: needs %zu bytes of 16-byte aligned workspace (got %zu)", pl.part_bytes,
@@ -929,7 +1096,7 @@ int amla_fp8_linear_f32(const void *x, int64_t m, int64_t k, int64_t ldx, const 
   p.seq_len = 1;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (m > 64) return launch_gemm(p, GEMV_F32, st);
-  const GemvPlan pl = plan_gemv((int)m, (int)n, (int)k);
+  const GemvPlan pl = plan_linear((int)m, (int)n, (int)k);
   if (pl.part_bytes) {
     if (!workspace || workspace_bytes < pl.part_bytes || !aligned16(workspace))
       return fail(AMLA_EWORKSPACE, "fp8_linear_f32: needs %zu bytes of 16-byte aligned workspace (got %zu)",

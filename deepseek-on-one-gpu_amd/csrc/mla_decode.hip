@@ -1133,9 +1133,9 @@ static DecodeLayout decode_layout(const amla_mla_args &a) {
   DecodeLayout L = {};
   const int B = std::min(a.batch, DECODE_MAX_BATCH);
   const int HD = a.qk_nope + a.qk_rope;
-  L.pa = plan_gemv(B, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
-  L.pb = plan_gemv(B, a.heads * HD, a.q_lora);
-  L.po = plan_gemv(B, a.hidden, a.heads * a.v_dim);
+  L.pa = plan_linear(B, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
+  L.pb = plan_linear(B, a.heads * HD, a.q_lora);
+  L.po = plan_linear(B, a.hidden, a.heads * a.v_dim);
   // splits over the batch: one per CU, at least two tiles each for the
   // longest possible context, or one tile each while the batch holds at most
   // 64 tiles (a split's fixed cost then outweighs its second tile); the plan
@@ -1238,14 +1238,15 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   uint16_t *qbuf = reinterpret_cast<uint16_t *>(ws + L.qbuf);
 
   // 1. [input RMSNorm, layer mode] q_a | kv_a  (kv_a written raw into the
-  //    caches, inference/ops.py:136-141; forward.py:92).  With K parts the
-  //    norm is folded: the GEMM reads bf16(x * input_gamma) and the K-part
-  //    finish multiplies each sum by the row's rsqrt(mean(x^2) + eps); with a
-  //    single K part it is its own launch first.
+  //    caches, inference/ops.py:136-141; forward.py:92).  With K parts or the
+  //    streaming GEMV the norm is folded: the GEMM reads bf16(x * input_gamma)
+  //    and each sum is multiplied by the row's rsqrt(mean(x^2) + eps) (by the
+  //    K-part finish, or by the streaming GEMV itself); otherwise it is its
+  //    own launch first.
   mark(ev, 0, st);
   const uint16_t *xin = x;
   const uint16_t *gin = reinterpret_cast<const uint16_t *>(a->input_gamma);
-  const bool fold_norm = gin && L.pa.kparts > 1 && a->hidden <= 8192;
+  const bool fold_norm = gin && (L.pa.kparts > 1 || L.pa.vec) && a->hidden <= 8192;
   if (gin && !fold_norm) {
     uint16_t *xn = reinterpret_cast<uint16_t *>(ws + L.xn);
     if ((rc = launch_rms_norm(x, B, a->hidden, a->hidden, gin, a->eps, xn, a->hidden, st))) return rc;
@@ -1254,6 +1255,8 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   GemvParams pa = {};
   pa.x = xin; pa.M = B; pa.ldx = a->hidden;
   pa.xg = fold_norm ? gin : nullptr;
+  pa.xnorm = fold_norm && L.pa.vec;
+  pa.eps_in = a->eps;
   pa.w0 = reinterpret_cast<const uint8_t *>(a->w_q_a); pa.s0 = a->s_q_a;
   pa.w1 = reinterpret_cast<const uint8_t *>(a->w_kv_a); pa.s1 = a->s_kv_a;
   pa.N = a->q_lora + LORA + ROPE; pa.K = a->hidden; pa.n_split = a->q_lora;

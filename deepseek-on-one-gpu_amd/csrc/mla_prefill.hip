@@ -974,7 +974,7 @@ __global__ __launch_bounds__(F_NW * 64, 1) void flash_kernel(FlashParams p) {
 // p.part (lin_bytes) holds the K-part sums of the skinny plan or the split
 // GEMM's partial sums (PrefillLayout::lin)
 static int run_linear(const GemvParams &p, int mode, hipStream_t st, size_t lin_bytes) {
-  if (p.M <= 64) return launch_gemv(p, mode, plan_gemv(p.M, p.N, p.K), st);
+  if (p.M <= 64) return launch_gemv(p, mode, plan_linear(p.M, p.N, p.K), st);
   return launch_gemm(p, mode, st, p.part, lin_bytes);
 }
 
@@ -1003,7 +1003,7 @@ static PrefillLayout prefill_layout(const amla_mla_args &a) {
   size_t lin = 0;
   const int HDv = a.qk_nope + a.v_dim;
   auto need = [&](int m, int n, int k) {
-    lin = std::max(lin, m <= 64 ? plan_gemv(m, n, k).part_bytes : gemm_ws_bytes(m, n, k));
+    lin = std::max(lin, m <= 64 ? plan_linear(m, n, k).part_bytes : gemm_ws_bytes(m, n, k));
   };
   need((int)M, a.q_lora + a.kv_lora + a.qk_rope, a.hidden);
   need((int)M, a.heads * HD, a.q_lora);
