@@ -54,6 +54,7 @@ SIGNATURES = [
     ("amla_mla_decode", c_int, [ctypes.POINTER(MlaArgs), c_void_p]),
     ("amla_mla_prefill", c_int, [ctypes.POINTER(MlaArgs), c_void_p]),
     ("amla_mla_decode_profiled", c_int, [ctypes.POINTER(MlaArgs), c_void_p, ctypes.POINTER(c_void_p)]),
+    ("amla_mla_decode_profiled_repeat", c_int, [ctypes.POINTER(MlaArgs), c_void_p, ctypes.POINTER(c_void_p), c_int]),
     ("amla_mla_decode_noalloc", c_int, [ctypes.POINTER(MlaArgs), c_void_p]),
     ("amla_mla_decode_workspace_bytes", c_size_t, [ctypes.POINTER(MlaArgs)]),
     ("amla_mla_prefill_workspace_bytes", c_size_t, [ctypes.POINTER(MlaArgs)]),

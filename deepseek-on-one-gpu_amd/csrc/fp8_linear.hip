@@ -1005,7 +1005,7 @@ using namespace amla;
 
 extern "C" {
 
-int amla_abi_version(void) { return 103; }
+int amla_abi_version(void) { return 104; }
 
 const char *amla_last_error(void) { return g_last_error.c_str(); }
 

@@ -1196,13 +1196,13 @@ static inline void mark(hipEvent_t const *ev, int i, hipStream_t st) {
   if (ev) (void)hipEventRecord(ev[i], st);
 }
 
-static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const *ev);
+static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const *ev, int attn_repeat);
 
-static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const *ev = nullptr) {
+static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const *ev = nullptr, int attn_repeat = 1) {
   int rc = check_mla_common(a, "mla_decode");
   if (rc) return rc;
   if (a->seq_len != 1) return fail(AMLA_EINVAL, "mla_decode: seq_len must be 1 (use mla_prefill)");
-  if (a->batch <= DECODE_MAX_BATCH) return decode_chunk(a, st, ev);
+  if (a->batch <= DECODE_MAX_BATCH) return decode_chunk(a, st, ev, attn_repeat);
   // inference/ops.py:119 takes any batch: chunks of DECODE_MAX_BATCH sequences
   // in order on the stream (each chunk's launches finish before the next
   // chunk's reuse the workspace)
@@ -1217,13 +1217,15 @@ static int decode_impl(const amla_mla_args *a, hipStream_t st, hipEvent_t const 
     if (a->attn_out) c.attn_out = static_cast<char *>(a->attn_out) + (size_t)b0 * a->heads * a->v_dim * 2;
     c.ckv_cache = static_cast<char *>(a->ckv_cache) + (size_t)b0 * a->max_seq * a->kv_lora * 2;
     c.kpe_cache = static_cast<char *>(a->kpe_cache) + (size_t)b0 * a->max_seq * a->qk_rope * 2;
-    if ((rc = decode_chunk(&c, st, ev))) return rc;
+    if ((rc = decode_chunk(&c, st, ev, attn_repeat))) return rc;
   }
   return AMLA_OK;
 }
 
 // One launch sequence for at most DECODE_MAX_BATCH sequences (args checked).
-static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const *ev) {
+// attn_repeat > 1 (measurement only) launches the attention kernel that many
+// times back to back: it reads the same inputs and rewrites the same partials.
+static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const *ev, int attn_repeat) {
   int rc = AMLA_OK;
   const DecodeLayout L = decode_layout(*a);
   if (a->workspace_bytes < L.total)
@@ -1328,8 +1330,10 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   ap.eps = a->eps;
   ap.part_o = reinterpret_cast<uint16_t *>(ws + L.part_o);
   ap.part_ml = reinterpret_cast<float *>(ws + L.part_ml);
-  attn_kernel<<<dim3(L.slots), 256, ATTN_LDS, st>>>(ap);
-  if ((rc = check_launch("mla attention"))) return rc;
+  for (int r = 0; r < attn_repeat; ++r) {
+    attn_kernel<<<dim3(L.slots), 256, ATTN_LDS, st>>>(ap);
+    if ((rc = check_launch("mla attention"))) return rc;
+  }
 
   // 6. merge splits, W_UV
   mark(ev, 5, st);
@@ -1441,12 +1445,19 @@ int amla_mla_decode_noalloc(const amla_mla_args *a, void *stream) {
   return decode_impl(&b, reinterpret_cast<hipStream_t>(stream));
 }
 
-int amla_mla_decode_profiled(const amla_mla_args *a, void *stream, void *const *events) {
+int amla_mla_decode_profiled_repeat(const amla_mla_args *a, void *stream, void *const *events, int attn_repeat) {
   if (!events) return fail(AMLA_EINVAL, "mla_decode_profiled: null events");
   for (int i = 0; i <= NSTAGE; ++i)
     if (!events[i]) return fail(AMLA_EINVAL, "mla_decode_profiled: null event %d", i);
+  if (attn_repeat < 1 || attn_repeat > 64)
+    return fail(AMLA_EINVAL, "mla_decode_profiled: attention repeat %d outside 1..64", attn_repeat);
   set_attn_attr();
-  return decode_impl(a, reinterpret_cast<hipStream_t>(stream), reinterpret_cast<hipEvent_t const *>(events));
+  return decode_impl(a, reinterpret_cast<hipStream_t>(stream), reinterpret_cast<hipEvent_t const *>(events),
+                     attn_repeat);
+}
+
+int amla_mla_decode_profiled(const amla_mla_args *a, void *stream, void *const *events) {
+  return amla_mla_decode_profiled_repeat(a, stream, events, 1);
 }
 
 }  // extern "C"

@@ -148,6 +148,12 @@ int amla_mla_decode(const amla_mla_args *args, void *stream);
  * attention; split merge + W_UV; o_proj) and events[7] after the last, so a
  * benchmark can time each kernel on the stream it runs on. */
 int amla_mla_decode_profiled(const amla_mla_args *args, void *stream, void *const *events);
+/* The same hook with the attention kernel launched attn_repeat (1..64) times
+ * back to back between events[4] and events[5] (it reads the same inputs and
+ * rewrites the same partial results, so the output is unchanged): the
+ * per-launch time (events[5] - events[4]) / attn_repeat then carries only a
+ * 1/attn_repeat share of the event and dispatch overhead around one launch. */
+int amla_mla_decode_profiled_repeat(const amla_mla_args *args, void *stream, void *const *events, int attn_repeat);
 
 /* No counterpart in the reference: for callers that cannot allocate (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).

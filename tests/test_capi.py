@@ -25,7 +25,7 @@ def test_every_declared_symbol_is_exported():
     for n in names:
         assert hasattr(L, n), n
     assert {s[0] for s in _lib.SIGNATURES} == set(names)
-    assert L.amla_abi_version() == 103
+    assert L.amla_abi_version() == 104
 
 
 def test_args_struct_layout_matches_c(tmp_path):
@@ -74,6 +74,9 @@ def test_null_and_bad_arguments_fail_before_launch():
     evs[3] = None
     assert L.amla_mla_decode_profiled(ctypes.byref(a), None, evs) == -1
     assert b"null event 3" in L.amla_last_error()
+    evs[3] = p
+    assert L.amla_mla_decode_profiled_repeat(ctypes.byref(a), None, evs, 0) == -1
+    assert b"repeat" in L.amla_last_error()
     a.seq_len = 2
     assert L.amla_mla_decode(ctypes.byref(a), None) == -1      # decode needs S == 1
     # fp8_linear shape constraints
