@@ -84,6 +84,9 @@ AMLA_DEV u32x2 ldg8(const void *p) { return *reinterpret_cast<const u32x2 *>(p);
 AMLA_DEV u32x4 ldg16_nt(const void *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
 }
+AMLA_DEV u32x2 ldg8_nt(const void *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
+}
 
 AMLA_DEV bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 

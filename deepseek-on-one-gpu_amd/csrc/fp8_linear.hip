@@ -223,8 +223,9 @@ AMLA_DEV void gemv_body(const GemvParams &p, int unit, int rg, int kparts, int k
         const int cg = (cl & ~7) | ((cl ^ row) & 7);              // global chunk stored there
         const int kb = min(kb_begin + s * 4 + (cg >> 3), KB - 1);  // 128 B block (clamped: unused)
         const uint32_t off = (uint32_t)(row * p.K + kb * 128 + (cg & 7) * 16);
+        // non-temporal (aux 2): each weight byte is read once per call
         __builtin_amdgcn_global_load_lds(wb + off, (__attribute__((address_space(3))) void *)(tb + (s * 8 + i) * 1024),
-                                         16, 0, 0);
+                                         16, 0, 2);
       }
     }
   };
@@ -619,19 +620,32 @@ GemvPlan plan_gemv_grouped(int M, int N, int K) {
 
 // With one row of x the MFMA tiles above use 1/16 of their columns and the
 // weight stream pays for LDS staging, barriers and K-part partial sums.  Here
-// a workgroup (256 threads) owns VG_ROWS weight rows over the whole K:
+// a workgroup (256 threads) owns a run of rpw consecutive weight rows over the
+// whole K and streams them straight into registers, VG_R rows at a time:
 //   * thread t takes the 16-byte fp8 chunks t, t + 256, .. (NCH of them) of
-//     every row, loaded straight into registers (all VG_ROWS x NCH in flight)
-//     from one contiguous 1 KB span per wave and row;
+//     every row (one contiguous 1 KB span per wave and row);
+//   * two groups of VG_R rows are in flight: the loads of the next group are
+//     issued before the current one is computed (a register double buffer,
+//     the loop unrolled by two so that both buffers are named statically and
+//     the compiler's load counters stay exact);
+//   * the loads carry the non-temporal hint: every weight byte is read once
+//     per call, and streaming it past the caches measured 10 % faster;
 //   * each chunk is converted exactly to bf16 pairs and dotted with the
 //     thread's x chunk in fp32 (v_dot2_f32_bf16), then scaled by its 128x128
 //     block's scale_inv (a chunk never straddles a block), like the MFMA path;
-//   * the rows reduce over the workgroup (lane swaps inside each wave, the
-//     four waves through LDS) and two threads store the rows through the
-//     GEMV epilogue (store4), so no finishing pass is needed.
+//   * every row reduces over its wave by lane swaps; the four waves' sums meet
+//     in LDS once at the end, and rpw / 4 threads store four rows each through
+//     the GEMV epilogue (store4), so no finishing pass is needed.
+// A persistent grid of about 512 workgroups (two per CU) keeps the stream
+// going: the one-shot form (a workgroup per 8 rows, 1.75 rounds of the
+// machine for o_proj) measured 26.2 us against 19.4 for this one (M = 1,
+// N = 7168, K = 16384) and 7.0 against 5.2 us for q_a | kv_a (N = 2112,
+// K = 7168), bit-identical results (same chunks, same order per row).
 // Optional input RMSNorm fold (p.xnorm): the workgroup holds the whole x row,
 // so it also sums x^2 and multiplies every result by rsqrt(mean(x^2) + eps_in).
-constexpr int VG_ROWS = 8;
+constexpr int VG_R = 2;          // rows per group (a divisor of 128: a group never straddles a scale block)
+constexpr int VG_MAX_RPW = 64;   // rows per workgroup (the LDS reduction buffer)
+constexpr int VG_GRID = 512;     // target workgroups
 
 template <int CTRL>
 AMLA_DEV float vg_dpp(float v) {
@@ -649,31 +663,19 @@ AMLA_DEV float vg_sum64(float v) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// rows [blockIdx.x * rpw, + rpw) (rpw a multiple of 2 VG_R and of 4); rows
+// past N re-read the last group of the matrix (in bounds) and are not stored
 template <int NCH, int MODE>
-__global__ __launch_bounds__(256) void vgemv_kernel(GemvParams p) {
+__global__ __launch_bounds__(256, 2) void vgemv_kernel(GemvParams p, int rpw) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n0 = blockIdx.x * VG_ROWS;
+  const int nb = blockIdx.x * rpw;
   const int C = p.K >> 4;  // 16-byte chunks per weight row
   const int KB = p.K >> 7;
-  const bool seg1 = (MODE == GEMV_QKVA || p.w1) && n0 >= p.n_split;
-  const int r0 = seg1 ? n0 - p.n_split : n0;  // VG_ROWS rows inside one segment and one 128-row scale block
-  const uint8_t *wb = (seg1 ? p.w1 : p.w0) + (size_t)r0 * p.K;
-  const float *sb = (seg1 ? p.s1 : p.s0) + (size_t)(r0 >> 7) * KB;
 
-  // every chunk of the workgroup's rows in flight first
-  u32x4 w[VG_ROWS][NCH];
-#pragma unroll
-  for (int r = 0; r < VG_ROWS; ++r)
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = tid + 256 * j;
-      w[r][j] = c < C ? ldg16(wb + (size_t)r * p.K + c * 16) : u32x4{0, 0, 0, 0};
-    }
-  // this thread's chunks of x (16 bf16 each) and their block scales
+  // this thread's chunks of x (16 bf16 each)
   u32x4 xa[NCH][2];
-  float sc[NCH];
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
@@ -681,7 +683,6 @@ __global__ __launch_bounds__(256) void vgemv_kernel(GemvParams p) {
     const bool ok = c < C;
     xa[j][0] = ok ? ldg16(p.x + c * 16) : u32x4{0, 0, 0, 0};
     xa[j][1] = ok ? ldg16(p.x + c * 16 + 8) : u32x4{0, 0, 0, 0};
-    sc[j] = ok ? sb[c >> 3] : 0.f;
     if (p.xnorm) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
@@ -700,60 +701,96 @@ __global__ __launch_bounds__(256) void vgemv_kernel(GemvParams p) {
     }
   }
 
-  float acc[VG_ROWS];
+  __shared__ float red[4][VG_MAX_RPW + 1];
+  u32x4 wa[VG_R][NCH], wb[VG_R][NCH];
+  float sa[NCH], sb[NCH];
+  // the weight chunks and block scales of the group at row n0
+  auto load = [&](u32x4 (&W)[VG_R][NCH], float (&S)[NCH], int n0) __attribute__((always_inline)) {
+    const int n = min(n0, p.N - VG_R);
+    const bool seg1 = (MODE == GEMV_QKVA || p.w1) && n >= p.n_split;
+    const int r0 = seg1 ? n - p.n_split : n;
+    const uint8_t *wp = (seg1 ? p.w1 : p.w0) + (size_t)r0 * p.K;
+    const float *sp = (seg1 ? p.s1 : p.s0) + (size_t)(r0 >> 7) * KB;
 #pragma unroll
-  for (int r = 0; r < VG_ROWS; ++r) {
-    float a = 0.f;
+    for (int r = 0; r < VG_R; ++r)
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      float d = 0.f;
+      for (int j = 0; j < NCH; ++j) W[r][j] = ldg16_nt(wp + (size_t)r * p.K + min(tid + 256 * j, C - 1) * 16);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bf16x2_t w01 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[r][j][e], 1.f, false);
-        const bf16x2_t w23 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[r][j][e], 1.f, true);
-        // bytes 4e .. 4e+3 of the chunk are elements 4e .. 4e+3: x pairs (4e, 4e+1), (4e+2, 4e+3)
-        const uint32_t x01 = xa[j][e >> 1][(e & 1) * 2], x23 = xa[j][e >> 1][(e & 1) * 2 + 1];
-        d = __builtin_amdgcn_fdot2_f32_bf16(w01, __builtin_bit_cast(bf16x2_t, x01), d, false);
-        d = __builtin_amdgcn_fdot2_f32_bf16(w23, __builtin_bit_cast(bf16x2_t, x23), d, false);
+    for (int j = 0; j < NCH; ++j) S[j] = sp[min(tid + 256 * j, C - 1) >> 3];
+  };
+  // this wave's sums of the group's rows into red[wave][row - nb]
+  auto compute = [&](const u32x4 (&W)[VG_R][NCH], const float (&S)[NCH], int i0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < VG_R; ++r) {
+      float a = 0.f;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        if (tid + 256 * j >= C) continue;  // past the row (x chunks are zero there too)
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bf16x2_t w01 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(W[r][j][e], 1.f, false);
+          const bf16x2_t w23 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(W[r][j][e], 1.f, true);
+          // bytes 4e .. 4e+3 of the chunk are elements 4e .. 4e+3: x pairs (4e, 4e+1), (4e+2, 4e+3)
+          const uint32_t x01 = xa[j][e >> 1][(e & 1) * 2], x23 = xa[j][e >> 1][(e & 1) * 2 + 1];
+          d = __builtin_amdgcn_fdot2_f32_bf16(w01, __builtin_bit_cast(bf16x2_t, x01), d, false);
+          d = __builtin_amdgcn_fdot2_f32_bf16(w23, __builtin_bit_cast(bf16x2_t, x23), d, false);
+        }
+        a = __builtin_fmaf(S[j], d, a);
       }
-      a = __builtin_fmaf(sc[j], d, a);
+      a = vg_sum64(a);
+      if (lane == 0) red[wave][i0 + r] = a;
     }
-    acc[r] = a;
+  };
+  const int ng = rpw / VG_R;  // even, >= 2
+  load(wa, sa, nb);
+  for (int g = 0; g < ng - 2; g += 2) {
+    load(wb, sb, nb + (g + 1) * VG_R);
+    compute(wa, sa, g * VG_R);
+    load(wa, sa, nb + (g + 2) * VG_R);
+    compute(wb, sb, (g + 1) * VG_R);
   }
+  load(wb, sb, nb + (ng - 1) * VG_R);
+  compute(wa, sa, (ng - 2) * VG_R);
+  compute(wb, sb, (ng - 1) * VG_R);
 
-  __shared__ float red[4][VG_ROWS + 1];
-#pragma unroll
-  for (int r = 0; r < VG_ROWS; ++r) acc[r] = vg_sum64(acc[r]);
-  if (p.xnorm) ss = vg_sum64(ss);
-  if (lane == 0) {
-#pragma unroll
-    for (int r = 0; r < VG_ROWS; ++r) red[wave][r] = acc[r];
-    red[wave][VG_ROWS] = ss;
+  if (p.xnorm) {
+    ss = vg_sum64(ss);
+    if (lane == 0) red[wave][VG_MAX_RPW] = ss;
   }
   __syncthreads();
-  if (tid < VG_ROWS / 4) {
+  if (4 * tid < rpw && nb + 4 * tid < p.N) {  // N % 8 == 0: four rows are all in range or all past N
     float rin = 1.f;
-    if (p.xnorm) rin = rsqrtf(((red[0][VG_ROWS] + red[1][VG_ROWS]) + (red[2][VG_ROWS] + red[3][VG_ROWS])) / (float)p.K +
-                           p.eps_in);
+    if (p.xnorm)
+      rin = rsqrtf(((red[0][VG_MAX_RPW] + red[1][VG_MAX_RPW]) + (red[2][VG_MAX_RPW] + red[3][VG_MAX_RPW])) /
+                       (float)p.K +
+                   p.eps_in);
     f32x4 v;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * tid + i;
       v[i] = ((red[0][r] + red[1][r]) + (red[2][r] + red[3][r])) * rin;
     }
-    store4<MODE>(p, 0, n0 + 4 * tid, v);
+    store4<MODE>(p, 0, nb + 4 * tid, v);
   }
+}
+
+// rows per workgroup of the streaming GEMV: about VG_GRID workgroups
+static int vgemv_rpw(int N) {
+  const int r = (N + VG_GRID - 1) / VG_GRID;
+  return std::min(VG_MAX_RPW, std::max(2 * VG_R, (r + 3) & ~3));
 }
 
 template <int NCH>
 static void launch_vgemv_mode(const GemvParams &p, int mode, hipStream_t st) {
-  const unsigned groups = (unsigned)(p.N / VG_ROWS);
+  const int rpw = vgemv_rpw(p.N);
+  const unsigned groups = (unsigned)((p.N + rpw - 1) / rpw);
   switch (mode) {
-    case GEMV_PLAIN: vgemv_kernel<NCH, GEMV_PLAIN><<<groups, 256, 0, st>>>(p); break;
-    case GEMV_RESID: vgemv_kernel<NCH, GEMV_RESID><<<groups, 256, 0, st>>>(p); break;
-    case GEMV_QKVA: vgemv_kernel<NCH, GEMV_QKVA><<<groups, 256, 0, st>>>(p); break;
-    case GEMV_F32: vgemv_kernel<NCH, GEMV_F32><<<groups, 256, 0, st>>>(p); break;
-    default: vgemv_kernel<NCH, GEMV_QROPE><<<groups, 256, 0, st>>>(p); break;
+    case GEMV_PLAIN: vgemv_kernel<NCH, GEMV_PLAIN><<<groups, 256, 0, st>>>(p, rpw); break;
+    case GEMV_RESID: vgemv_kernel<NCH, GEMV_RESID><<<groups, 256, 0, st>>>(p, rpw); break;
+    case GEMV_QKVA: vgemv_kernel<NCH, GEMV_QKVA><<<groups, 256, 0, st>>>(p, rpw); break;
+    case GEMV_F32: vgemv_kernel<NCH, GEMV_F32><<<groups, 256, 0, st>>>(p, rpw); break;
+    default: vgemv_kernel<NCH, GEMV_QROPE><<<groups, 256, 0, st>>>(p, rpw); break;
   }
 }
 
@@ -765,7 +802,7 @@ GemvPlan plan_linear(int M, int N, int K) {
   pl.kpb = K / 128;
   pl.kparts = 1;
   pl.rg = 1;
-  pl.groups = N / VG_ROWS;
+  pl.groups = (N + vgemv_rpw(N) - 1) / vgemv_rpw(N);
   pl.vec = 1;
   return pl;
 }

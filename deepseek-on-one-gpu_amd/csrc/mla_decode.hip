@@ -196,8 +196,14 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
   const int c0 = quarter * 128 + cc * 8;  // this thread's 8 latent columns
   const uint8_t *wp = wkvb + ((size_t)h * (NOPE + VD) + dg * 8) * LORA + c0;
   u32x2 raw[8];
+  // non-temporal when this is the only workgroup reading these weight rows
+  if (gridDim.z == 1) {
 #pragma unroll
-  for (int d = 0; d < 8; ++d) raw[d] = ldg8(wp + (size_t)d * LORA);
+    for (int d = 0; d < 8; ++d) raw[d] = ldg8_nt(wp + (size_t)d * LORA);
+  } else {
+#pragma unroll
+    for (int d = 0; d < 8; ++d) raw[d] = ldg8(wp + (size_t)d * LORA);
+  }
   for (int e = tid; e < BB * NOPE; e += 256) {
     const int bb = e / NOPE, d = e % NOPE;
     qn[bb][d] = bb < nb ? bf2f(q[((size_t)(b0 + bb) * HEADS + h) * (NOPE + ROPE) + d]) : 0.f;
@@ -326,6 +332,8 @@ constexpr float REF_HEADROOM_SUM = 18446744073709551616.f;  // 2^64
 // every global_load_lds_dwordx4 writes 64 lanes x 16 B contiguously at its
 // LDS base.  Row indices are wave-uniform (scalar bases, one lane offset).
 // Rows past the context re-read row T-1 (in bounds; their scores are masked).
+// The cache rows are copied non-temporal (aux 2: each is read once per step);
+// the (cos, sin) rows, which every sequence of the batch reads, are not.
 // Piece 0..7: latent row 8w + piece; 8: the 8 rows' raw rope keys; 9, 10: the
 // (cos, sin) table rows of the 8 rows (2 x 1 KB), into the table block of the
 // tile's parity.  The tile loop issues one piece per score step: a burst of
@@ -338,7 +346,7 @@ AMLA_DEV void dma_piece(const AttnParams &p, int b, int tile, int parity, int T,
     const char *cb = reinterpret_cast<const char *>(p.ckv + (size_t)b * p.ckv_bstride);
     const int t = min(t0 + piece, T - 1);
     __builtin_amdgcn_global_load_lds(cb + (size_t)t * (LORA * 2) + lane16,
-                                     LDS_PTR(stage + (wave * 8 + piece) * (KROW * 2)), 16, 0, 0);
+                                     LDS_PTR(stage + (wave * 8 + piece) * (KROW * 2)), 16, 0, 2);
     return;
   }
   const int t0c = min(t0, T - 1);
@@ -350,7 +358,7 @@ AMLA_DEV void dma_piece(const AttnParams &p, int b, int tile, int parity, int T,
     const char *kb = reinterpret_cast<const char *>(p.kpe + (size_t)b * p.kpe_bstride) + (size_t)t0c * (ROPE * 2);
     const uint32_t row = static_cast<uint32_t>(min(t0 + static_cast<int>(ln >> 3), T - 1) - t0c);
     __builtin_amdgcn_global_load_lds(kb + row * (ROPE * 2) + (ln & 7u) * 16u, LDS_PTR(stage + K_BYTES + wave * 1024), 16,
-                                     0, 0);
+                                     0, 2);
   } else {
     const char *tb = reinterpret_cast<const char *>(p.rope_table) + (size_t)t0c * (ROPE * 4);
     const uint32_t e = static_cast<uint32_t>(piece - 9) * 64u + ln;
@@ -987,10 +995,18 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
   const int li = lane & 15, lg = lane >> 4;
   const uint8_t *wr = wkvb + ((size_t)h * (NOPE + VD) + NOPE + 32 * wave + li) * LORA + 8 * lg;
   u32x2 wa[2][LORA / 32];
+  // non-temporal when this is the only workgroup reading these weight rows
+  if (gridDim.y == 1) {
 #pragma unroll
-  for (int vt = 0; vt < 2; ++vt)
+    for (int vt = 0; vt < 2; ++vt)
 #pragma unroll
-    for (int ks = 0; ks < LORA / 32; ++ks) wa[vt][ks] = ldg8(wr + (size_t)vt * 16 * LORA + ks * 32);
+      for (int ks = 0; ks < LORA / 32; ++ks) wa[vt][ks] = ldg8_nt(wr + (size_t)vt * 16 * LORA + ks * 32);
+  } else {
+#pragma unroll
+    for (int vt = 0; vt < 2; ++vt)
+#pragma unroll
+      for (int ks = 0; ks < LORA / 32; ++ks) wa[vt][ks] = ldg8(wr + (size_t)vt * 16 * LORA + ks * 32);
+  }
 
   // ---- fast merge: wave w, sequence b0 + w.  The first 16 splits' partial
   // rows are in flight while the max and the weights are formed.
