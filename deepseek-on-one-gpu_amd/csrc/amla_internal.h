@@ -50,8 +50,8 @@ struct GemvParams {
   const float *rope_table;
   int head_dim, nope;   // QROPE
   float *part;          // fp32 partial sums of the K parts (GemvPlan::part_bytes), else unused
-  int xnorm;            // streaming GEMV only: x is the raw input and every sum of its row is multiplied
-  float eps_in;         // by rsqrt(mean(x^2) + eps_in) (the input RMSNorm folded, xg carrying its gamma)
+  int xnorm;            // streaming GEMV only: x is the raw input, projected as rms_norm(x, xg, eps_in)
+  float eps_in;         // (bf16(bf16(x * rsqrt(mean(x^2) + eps_in)) * xg), the norm's own rounding)
 };
 
 struct GemvPlan {
@@ -61,12 +61,13 @@ struct GemvPlan {
   int groups;        // workgroups
   size_t lds;        // dynamic LDS bytes per workgroup
   size_t part_bytes; // fp32 partial sums (kparts * M * N * 4) when kparts > 1
-  int vec;           // 1: the streaming GEMV for one row of x (vgemv_kernel), no K parts
+  int vec;           // streaming GEMV for one row of x, no K parts: 1 vgemv_kernel, 2 vgemv_short_kernel
 };
 
 GemvPlan plan_gemv(int M, int N, int K);
-// plan_gemv, or the streaming GEMV (vec = 1) where it applies: one row of x,
-// 4096 <= K <= 16384 (K % 128 == 0), N % 8 == 0.  For launch_gemv only (the
+// plan_gemv, or a streaming GEMV where one applies: one row of x, N % 8 == 0,
+// and 4096 <= K <= 16384 (K % 128 == 0; vec = 1) or K = 1536 (one weight
+// segment, not the cache-row epilogue; vec = 2).  For launch_gemv only (the
 // grouped and scheduled launches take plan_gemv plans).
 GemvPlan plan_linear(int M, int N, int K);
 size_t gemv_lds_bytes(int MT, int kpb, int rg, int kparts);  // MT = 16-row tiles of x (1, 2 or 4)

@@ -641,8 +641,10 @@ GemvPlan plan_gemv_grouped(int M, int N, int K) {
 // machine for o_proj) measured 26.2 us against 19.4 for this one (M = 1,
 // N = 7168, K = 16384) and 7.0 against 5.2 us for q_a | kv_a (N = 2112,
 // K = 7168), bit-identical results (same chunks, same order per row).
-// Optional input RMSNorm fold (p.xnorm): the workgroup holds the whole x row,
-// so it also sums x^2 and multiplies every result by rsqrt(mean(x^2) + eps_in).
+// Optional input RMSNorm (p.xnorm): the workgroup holds the whole x row, so
+// it normalises it exactly as rms_norm does (bf16(bf16(x * r) * xg), r =
+// rsqrt(mean(x^2) + eps_in), one LDS-only barrier) while the first weight
+// group is in flight.
 constexpr int VG_R = 2;          // rows per group (a divisor of 128: a group never straddles a scale block)
 constexpr int VG_MAX_RPW = 64;   // rows per workgroup (the LDS reduction buffer)
 constexpr int VG_GRID = 512;     // target workgroups
@@ -674,34 +676,21 @@ __global__ __launch_bounds__(256, 2) void vgemv_kernel(GemvParams p, int rpw) {
   const int C = p.K >> 4;  // 16-byte chunks per weight row
   const int KB = p.K >> 7;
 
-  // this thread's chunks of x (16 bf16 each)
-  u32x4 xa[NCH][2];
-  float ss = 0.f;
+  // this thread's chunks of x (16 bf16 each) and of xg, loaded before the
+  // weights so that waiting for them does not wait for the weight loads
+  u32x4 xa[NCH][2], ga[NCH][2];
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int c = tid + 256 * j;
     const bool ok = c < C;
     xa[j][0] = ok ? ldg16(p.x + c * 16) : u32x4{0, 0, 0, 0};
     xa[j][1] = ok ? ldg16(p.x + c * 16 + 8) : u32x4{0, 0, 0, 0};
-    if (p.xnorm) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          ss += lo_bf(xa[j][h][e]) * lo_bf(xa[j][h][e]) + hi_bf(xa[j][h][e]) * hi_bf(xa[j][h][e]);
-    }
-    if (p.xg && ok) {  // the GEMM takes bf16(x * g) (the folded input RMSNorm's gamma)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const u32x4 g = ldg16(p.xg + c * 16 + 8 * h);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          xa[j][h][e] = pack_bf16(lo_bf(xa[j][h][e]) * lo_bf(g[e]), hi_bf(xa[j][h][e]) * hi_bf(g[e]));
-      }
-    }
+    ga[j][0] = ok && p.xg ? ldg16(p.xg + c * 16) : u32x4{0, 0, 0, 0};
+    ga[j][1] = ok && p.xg ? ldg16(p.xg + c * 16 + 8) : u32x4{0, 0, 0, 0};
   }
 
-  __shared__ float red[4][VG_MAX_RPW + 1];
+  __shared__ float red[4][VG_MAX_RPW];
+  __shared__ float xss[4];
   u32x4 wa[VG_R][NCH], wb[VG_R][NCH];
   float sa[NCH], sb[NCH];
   // the weight chunks and block scales of the group at row n0
@@ -743,7 +732,42 @@ __global__ __launch_bounds__(256, 2) void vgemv_kernel(GemvParams p, int rpw) {
     }
   };
   const int ng = rpw / VG_R;  // even, >= 2
-  load(wa, sa, nb);
+  load(wa, sa, nb);  // in flight while x is prepared
+  if (p.xnorm) {
+    // rms_norm(x, xg, eps_in) of the whole row (inference/ops.py:10-12), as
+    // the row-norm kernel computes it; the barrier is LDS-only, so the weight
+    // loads above stay in flight
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          ss += lo_bf(xa[j][h][e]) * lo_bf(xa[j][h][e]) + hi_bf(xa[j][h][e]) * hi_bf(xa[j][h][e]);
+    ss = vg_sum64(ss);
+    if (lane == 0) xss[wave] = ss;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const float r = rsqrtf(((xss[0] + xss[1]) + (xss[2] + xss[3])) / (float)p.K + p.eps_in);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xa[j][h][e] = pack_bf16(round_bf16(lo_bf(xa[j][h][e]) * r) * lo_bf(ga[j][h][e]),
+                                  round_bf16(hi_bf(xa[j][h][e]) * r) * hi_bf(ga[j][h][e]));
+  } else if (p.xg) {  // the GEMM takes bf16(x * xg)
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xa[j][h][e] = pack_bf16(lo_bf(xa[j][h][e]) * lo_bf(ga[j][h][e]), hi_bf(xa[j][h][e]) * hi_bf(ga[j][h][e]));
+  }
   for (int g = 0; g < ng - 2; g += 2) {
     load(wb, sb, nb + (g + 1) * VG_R);
     compute(wa, sa, g * VG_R);
@@ -754,23 +778,144 @@ __global__ __launch_bounds__(256, 2) void vgemv_kernel(GemvParams p, int rpw) {
   compute(wa, sa, (ng - 2) * VG_R);
   compute(wb, sb, (ng - 1) * VG_R);
 
-  if (p.xnorm) {
-    ss = vg_sum64(ss);
-    if (lane == 0) red[wave][VG_MAX_RPW] = ss;
-  }
   __syncthreads();
   if (4 * tid < rpw && nb + 4 * tid < p.N) {  // N % 8 == 0: four rows are all in range or all past N
-    float rin = 1.f;
-    if (p.xnorm)
-      rin = rsqrtf(((red[0][VG_MAX_RPW] + red[1][VG_MAX_RPW]) + (red[2][VG_MAX_RPW] + red[3][VG_MAX_RPW])) /
-                       (float)p.K +
-                   p.eps_in);
     f32x4 v;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * tid + i;
-      v[i] = ((red[0][r] + red[1][r]) + (red[2][r] + red[3][r])) * rin;
+      v[i] = (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]);
     }
+    store4<MODE>(p, 0, nb + 4 * tid, v);
+  }
+}
+
+// Short rows (K = 1536, the q_b projection: 96 chunks of 16 bytes, too few
+// for 256 threads per row): each wave streams its own rows, VGS_S = 2 rows
+// (192 chunks, 3 KB contiguous) per span, lane l taking the span's chunks
+// l, l + 64, l + 128, and VGS_G spans per group, two groups in flight; the
+// rows reduce inside the wave and meet in LDS only for the epilogue's
+// four-row stores.  Each span's rows share one 128-row scale block.
+constexpr int VGS_C = 96;                    // chunks per row (K = 1536)
+constexpr int VGS_S = 2;                     // rows per span
+constexpr int VGS_CPL = VGS_S * VGS_C / 64;  // chunks per lane per span
+constexpr int VGS_G = 3;                     // spans per group
+constexpr int VGS_RPW = 4 * 2 * VGS_G * VGS_S;  // rows per workgroup: 4 waves x 2 groups
+
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void vgemv_short_kernel(GemvParams p) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nw = blockIdx.x * VGS_RPW + wave * (VGS_RPW / 4);  // this wave's first row
+  const int KB = p.K >> 7;
+  // span chunk i of this lane: row ri[i] of the span, column chunk ci[i]
+  int ri[VGS_CPL], ci[VGS_CPL];
+#pragma unroll
+  for (int i = 0; i < VGS_CPL; ++i) {
+    ri[i] = (lane + 64 * i) / VGS_C;
+    ci[i] = (lane + 64 * i) % VGS_C;
+  }
+  u32x4 xa[VGS_CPL][2], ga[VGS_CPL][2];  // x and xg chunks, loaded before the weights
+#pragma unroll
+  for (int i = 0; i < VGS_CPL; ++i) {
+    xa[i][0] = ldg16(p.x + ci[i] * 16);
+    xa[i][1] = ldg16(p.x + ci[i] * 16 + 8);
+    ga[i][0] = p.xg ? ldg16(p.xg + ci[i] * 16) : u32x4{0, 0, 0, 0};
+    ga[i][1] = p.xg ? ldg16(p.xg + ci[i] * 16 + 8) : u32x4{0, 0, 0, 0};
+  }
+  // block scales of the lane's columns in the (at most two) 128-row blocks of the wave's rows
+  const int blk0 = nw >> 7;
+  float sc0[VGS_CPL], sc1[VGS_CPL];
+  {
+    const int blk1 = min((nw + VGS_RPW / 4 - 1) >> 7, (p.N - 1) >> 7);
+#pragma unroll
+    for (int i = 0; i < VGS_CPL; ++i) {
+      sc0[i] = p.s0[(size_t)min(blk0, (p.N - 1) >> 7) * KB + (ci[i] >> 3)];
+      sc1[i] = p.s0[(size_t)blk1 * KB + (ci[i] >> 3)];
+    }
+  }
+
+  __shared__ float red[VGS_RPW];
+  u32x4 wa[VGS_G][VGS_CPL], wb[VGS_G][VGS_CPL];
+  auto load = [&](u32x4 (&W)[VGS_G][VGS_CPL], int n0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int sp = 0; sp < VGS_G; ++sp) {
+      const int n = min(n0 + sp * VGS_S, p.N - VGS_S);  // rows past N re-read the last span (not stored)
+      const uint8_t *wp = p.w0 + (size_t)n * p.K;
+#pragma unroll
+      for (int i = 0; i < VGS_CPL; ++i) W[sp][i] = ldg16_nt(wp + (lane + 64 * i) * 16);
+    }
+  };
+  auto compute = [&](const u32x4 (&W)[VGS_G][VGS_CPL], int n0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int sp = 0; sp < VGS_G; ++sp) {
+      const bool second = ((n0 + sp * VGS_S) >> 7) != blk0;  // wave-uniform
+      float a[VGS_S] = {};
+#pragma unroll
+      for (int i = 0; i < VGS_CPL; ++i) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bf16x2_t w01 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(W[sp][i][e], 1.f, false);
+          const bf16x2_t w23 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(W[sp][i][e], 1.f, true);
+          const uint32_t x01 = xa[i][e >> 1][(e & 1) * 2], x23 = xa[i][e >> 1][(e & 1) * 2 + 1];
+          d = __builtin_amdgcn_fdot2_f32_bf16(w01, __builtin_bit_cast(bf16x2_t, x01), d, false);
+          d = __builtin_amdgcn_fdot2_f32_bf16(w23, __builtin_bit_cast(bf16x2_t, x23), d, false);
+        }
+        const float v = (second ? sc1[i] : sc0[i]) * d;
+#pragma unroll
+        for (int r = 0; r < VGS_S; ++r) a[r] += ri[i] == r ? v : 0.f;
+      }
+#pragma unroll
+      for (int r = 0; r < VGS_S; ++r) {
+        const float t = vg_sum64(a[r]);
+        if (lane == 0) red[n0 + sp * VGS_S + r - blockIdx.x * VGS_RPW] = t;
+      }
+    }
+  };
+  load(wa, nw);
+  load(wb, nw + VGS_G * VGS_S);
+  // x prepared while the weights are in flight: rms_norm(x, xg, eps_in) of
+  // the whole row (inference/ops.py:10-12; each wave holds every column
+  // chunk, the span's first row once), or bf16(x * xg)
+  if (p.xnorm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < VGS_CPL; ++i)
+      if (ri[i] == 0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            ss += lo_bf(xa[i][h][e]) * lo_bf(xa[i][h][e]) + hi_bf(xa[i][h][e]) * hi_bf(xa[i][h][e]);
+      }
+    const float r = rsqrtf(vg_sum64(ss) / (float)p.K + p.eps_in);
+#pragma unroll
+    for (int i = 0; i < VGS_CPL; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xa[i][h][e] = pack_bf16(round_bf16(lo_bf(xa[i][h][e]) * r) * lo_bf(ga[i][h][e]),
+                                  round_bf16(hi_bf(xa[i][h][e]) * r) * hi_bf(ga[i][h][e]));
+  } else if (p.xg) {
+#pragma unroll
+    for (int i = 0; i < VGS_CPL; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xa[i][h][e] = pack_bf16(lo_bf(xa[i][h][e]) * lo_bf(ga[i][h][e]), hi_bf(xa[i][h][e]) * hi_bf(ga[i][h][e]));
+  }
+  compute(wa, nw);
+  compute(wb, nw + VGS_G * VGS_S);
+  __syncthreads();
+  const int nb = blockIdx.x * VGS_RPW;
+  if (4 * tid < VGS_RPW && nb + 4 * tid < p.N) {
+    f32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = red[4 * tid + i];
     store4<MODE>(p, 0, nb + 4 * tid, v);
   }
 }
@@ -795,21 +940,42 @@ static void launch_vgemv_mode(const GemvParams &p, int mode, hipStream_t st) {
 }
 
 static bool vgemv_applies(int M, int N, int K) { return M == 1 && K % 128 == 0 && K >= 4096 && K <= 16384 && N % 8 == 0; }
+static bool vgemv_short_applies(int M, int N, int K) { return M == 1 && K == VGS_C * 16 && N % 8 == 0; }
 
 GemvPlan plan_linear(int M, int N, int K) {
-  if (!vgemv_applies(M, N, K)) return plan_gemv(M, N, K);
   GemvPlan pl = {};
+  if (vgemv_applies(M, N, K)) {
+    pl.groups = (N + vgemv_rpw(N) - 1) / vgemv_rpw(N);
+    pl.vec = 1;
+  } else if (vgemv_short_applies(M, N, K)) {
+    pl.groups = (N + VGS_RPW - 1) / VGS_RPW;
+    pl.vec = 2;
+  } else {
+    return plan_gemv(M, N, K);
+  }
   pl.kpb = K / 128;
   pl.kparts = 1;
   pl.rg = 1;
-  pl.groups = (N + vgemv_rpw(N) - 1) / vgemv_rpw(N);
-  pl.vec = 1;
   return pl;
 }
 
-static int launch_vgemv(const GemvParams &p, int mode, hipStream_t st) {
-  if (!vgemv_applies(p.M, p.N, p.K) || p.ldx < p.K || (p.w1 || mode == GEMV_QKVA ? p.n_split % 128 : 0) ||
-      !aligned16(p.x) || (p.xg && !aligned16(p.xg)))
+static int launch_vgemv(const GemvParams &p, int mode, int vec, hipStream_t st) {
+  if (p.ldx < p.K || !aligned16(p.x) || (p.xg && !aligned16(p.xg)))
+    return fail(AMLA_EINVAL, "streaming fp8 GEMV: x must be 16-byte aligned rows of at least K elements");
+  if (vec == 2) {
+    // one weight segment (the row-segment and cache epilogues take the long-row kernel)
+    if (!vgemv_short_applies(p.M, p.N, p.K) || p.w1 || mode == GEMV_QKVA)
+      return fail(AMLA_EINVAL, "streaming fp8 GEMV: plan for another shape (M=%d N=%d K=%d)", p.M, p.N, p.K);
+    const unsigned groups = (unsigned)((p.N + VGS_RPW - 1) / VGS_RPW);
+    switch (mode) {
+      case GEMV_PLAIN: vgemv_short_kernel<GEMV_PLAIN><<<groups, 256, 0, st>>>(p); break;
+      case GEMV_RESID: vgemv_short_kernel<GEMV_RESID><<<groups, 256, 0, st>>>(p); break;
+      case GEMV_F32: vgemv_short_kernel<GEMV_F32><<<groups, 256, 0, st>>>(p); break;
+      default: vgemv_short_kernel<GEMV_QROPE><<<groups, 256, 0, st>>>(p); break;
+    }
+    return check_launch("fp8 streaming GEMV (short rows)");
+  }
+  if (!vgemv_applies(p.M, p.N, p.K) || (p.w1 || mode == GEMV_QKVA ? p.n_split % 128 : 0))
     return fail(AMLA_EINVAL, "streaming fp8 GEMV: plan for another shape (M=%d N=%d K=%d)", p.M, p.N, p.K);
   const int C = p.K >> 4;
   if (C <= 256) launch_vgemv_mode<1>(p, mode, st);
@@ -842,7 +1008,7 @@ static void launch_mt(const GemvParams &p, int mode, const GemvPlan &pl, hipStre
 }
 
 int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t st, bool finish) {
-  if (pl.vec) return launch_vgemv(p0, mode, st);
+  if (pl.vec) return launch_vgemv(p0, mode, pl.vec, st);
   if (p0.M < 1 || p0.M > 64) return fail(AMLA_EINVAL, "skinny fp8 GEMM needs 1 <= M <= 64 (got %d)", p0.M);
   if (p0.N % 16 || p0.K % 128)
     return fail(AMLA_EUNSUPPORTED, "skinny fp8 GEMM needs N %% 16 == 0 and K %% 128 == 0 (N=%d K=%d)", p0.N, p0.K);

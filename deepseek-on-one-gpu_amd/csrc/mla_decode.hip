@@ -14,11 +14,13 @@
 // fly, once per row instead of once per row and head.
 //
 // Launch sequence per layer:
-//   rms_norm   : input RMSNorm of hidden (layer mode only)
-//   gemv  QKVA : q_a | kv_a in K parts (fp32 partial sums)
+//   rms_norm   : input RMSNorm of hidden (layer mode only, when it cannot be
+//                folded into the next GEMV)
+//   gemv  QKVA : q_a | kv_a in K parts (fp32 partial sums), or one streaming
+//                pass for batch 1 that also writes the new cache row
 //   finish     : sums the K parts, writes the new cache row (raw latent + raw
 //                k_pe) and q_a_layernorm(q_a) (a row norm in place when the
-//                GEMV needs no K parts)
+//                GEMV needs no K parts, folded into q_b at batch 1)
 //   gemv  QROPE: q = q_a_norm W_qb^T, RoPE on the q_pe rows at pos[b]
 //   absorb     : qt = gamma_kv * W_UK^T q_nope -> qbuf (B, H, 576) with q_pe,
 //                stored in attn_kernel's fragment order; one more workgroup
@@ -1256,10 +1258,11 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   uint16_t *qbuf = reinterpret_cast<uint16_t *>(ws + L.qbuf);
 
   // 1. [input RMSNorm, layer mode] q_a | kv_a  (kv_a written raw into the
-  //    caches, inference/ops.py:136-141; forward.py:92).  With K parts or the
-  //    streaming GEMV the norm is folded: the GEMM reads bf16(x * input_gamma)
-  //    and each sum is multiplied by the row's rsqrt(mean(x^2) + eps) (by the
-  //    K-part finish, or by the streaming GEMV itself); otherwise it is its
+  //    caches, inference/ops.py:136-141; forward.py:92).  The streaming GEMV
+  //    (batch 1) normalises its x row itself, exactly as rms_norm; with K
+  //    parts the norm is folded: the GEMM reads bf16(x * input_gamma) and the
+  //    K-part finish multiplies each sum by the row's rsqrt(mean(x^2) + eps)
+  //    (one bf16 rounding fewer than the reference's); otherwise it is its
   //    own launch first.
   mark(ev, 0, st);
   const uint16_t *xin = x;
@@ -1285,13 +1288,15 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   pa.kv_lora = LORA; pa.rope = ROPE; pa.pos = a->positions; pa.seq_len = 1; pa.max_rows = a->max_seq;
   pa.part = reinterpret_cast<float *>(ws + L.lin);
   if ((rc = launch_gemv(pa, GEMV_QKVA, L.pa, st, false))) return rc;  // K parts are summed below
-  // 2. q_a_layernorm (inference/ops.py:130): fused into the K-part finish, or
-  //    a row norm in place when the GEMV needs no finishing pass
+  // 2. q_a_layernorm (inference/ops.py:130): fused into the K-part finish;
+  //    done by q_b's streaming GEMV on its x row (batch 1); else a row norm
+  //    in place
   mark(ev, 1, st);
   const uint16_t *gq = reinterpret_cast<const uint16_t *>(a->gamma_q);
+  const bool fold_qnorm = L.pa.kparts == 1 && L.pb.vec;
   if (L.pa.kparts > 1) {
     if ((rc = launch_qkva_finish_norm(pa, L.pa.kparts, gq, a->eps, st, fold_norm ? x : nullptr, a->eps))) return rc;
-  } else if ((rc = launch_rms_norm(qa, B, a->q_lora, a->q_lora, gq, a->eps, qa, a->q_lora, st))) {
+  } else if (!fold_qnorm && (rc = launch_rms_norm(qa, B, a->q_lora, a->q_lora, gq, a->eps, qa, a->q_lora, st))) {
     return rc;
   }
 
@@ -1299,6 +1304,9 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   mark(ev, 2, st);
   GemvParams pb = {};
   pb.x = qa; pb.M = B; pb.ldx = a->q_lora;
+  pb.xg = fold_qnorm ? gq : nullptr;
+  pb.xnorm = fold_qnorm;
+  pb.eps_in = a->eps;
   pb.w0 = reinterpret_cast<const uint8_t *>(a->w_q_b); pb.s0 = a->s_q_b;
   pb.N = a->heads * HD; pb.K = a->q_lora; pb.n_split = pb.N;
   pb.y = q; pb.ldy = pb.N;

@@ -88,6 +88,20 @@ def test_fp8_linear_out_dtype(name, M):
     assert torch.equal(got16.cpu(), got.cpu().to(torch.float16))
 
 
+@pytest.mark.parametrize("N,K", [(160, 1536), (208, 1536), (32, 4096), (1040, 7168), (4112, 16384)])
+def test_fp8_linear_streaming_ragged_rows(N, K):
+    """One row of x takes the streaming GEMVs (K = 1536, and 4096 <= K <= 16384): row counts
+    that leave the last workgroup's run of rows partial, and partial 128-row scale blocks."""
+    print(f"[case] fp8_linear streaming N={N} K={K}", flush=True)
+    w, s = synth.quantize_fp8_blocks(synth.randn((N, K), synth.seed_of("fp8vs", N, K), 0.02))
+    x = synth.randn((1, K), synth.seed_of("fp8vsx", N, K)).to(torch.bfloat16)
+    got = ops.fp8_linear(x.to(DEV), w.to(DEV), s.to(DEV))
+    torch.cuda.synchronize()
+    want = R.fp8_linear(x, w, s)
+    assert_parity(got, want, f"fp8_linear streaming N={N} K={K}")
+    assert_bf16_ulps(got, want, 2, f"fp8_linear streaming N={N} K={K}")
+
+
 def test_fp8_linear_repeat_is_deterministic():
     w, s = _w("o_proj")
     x = synth.randn((8, SHAPES["o_proj"][1]), 5).to(torch.bfloat16).to(DEV)
