@@ -77,12 +77,13 @@ def _check_cache(gc, rc, rows):
 
 
 def _check_layer_cache(gc, rc, hidden, gamma, aw, lo, hi):
-    """Cache rows written by the layer entry (input RMSNorm first).  Decode folds that norm into
-    the q_a|kv_a projection: it projects bf16(x * gamma) and scales the fp32 sums by the row's
-    rsqrt(mean(x^2) + eps), so the normed input is never rounded to bf16 as in
-    inference/ops.py:12.  The rows then agree with the oracle to the output tolerance (not to
-    2 bf16 ulps) and are about as close as the oracle (within 10%) to the float64 projection of the exactly
-    normed input."""
+    """Cache rows written by the layer entry (input RMSNorm first).  Decode of more than one
+    sequence folds that norm into the q_a|kv_a projection's K parts: it projects bf16(x * gamma)
+    and scales the fp32 sums by the row's rsqrt(mean(x^2) + eps), so the normed input is never
+    rounded to bf16 as in inference/ops.py:12.  The rows then agree with the oracle to the output
+    tolerance (not to 2 bf16 ulps) and are about as close as the oracle (within 10%) to the
+    float64 projection of the exactly normed input.  (One sequence normalises exactly:
+    test_layer_mode_batch1_cache_rows.)"""
     cfg = R1
     x = hidden.double()
     xn = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + cfg.rms_norm_eps) * gamma.double()
@@ -287,6 +288,16 @@ def test_layer_mode_decode_and_prefill():
         lay = _layer("mla/" + tag)
         _check_layer_cache(gc, rc, synth.make_hidden(R1, B, S, tag), lay.input_layernorm, lay.attn_weights,
                            pos, pos + S)
+
+
+def test_layer_mode_batch1_cache_rows():
+    """Layer-mode decode of one sequence: the streaming q_a|kv_a GEMV applies the input RMSNorm to
+    its x row with the reference's rounding (inference/ops.py:10-12), so the new cache row is
+    within 2 bf16 ulps of the oracle's, like the non-layer entry's."""
+    for tag, pos, max_seq in (("layerb1", 256, 264), ("layerb1b", 4095, 4104)):
+        got, want, gc, rc = _run_case(tag, 1, 1, pos, max_seq, layer_mode=True)
+        assert_parity(got, want, f"layer {tag}")
+        _check_cache(gc, rc, [(pos, pos + 1)])
 
 
 def test_prefill_row_equals_decode():
