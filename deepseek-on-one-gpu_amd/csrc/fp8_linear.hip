@@ -920,6 +920,311 @@ __global__ __launch_bounds__(256, 2) void vgemv_short_kernel(GemvParams p) {
   }
 }
 
+// ---------------------------------------------------------------- streaming GEMV, 2 .. 8 rows of x
+
+// With a few rows of x (decode batches of 2 .. 8) the skinny GEMM above stages
+// the weights through LDS and holds x in registers, which bounds a K part to
+// 1024 columns and needs a finishing pass over fp32 partial sums.  Here the
+// roles swap: x sits in LDS and the weights stream straight into registers in
+// MFMA fragment order, so every workgroup covers the whole K of its rows.
+//   * one workgroup per CU (8 waves) owns a run of rpw rows (a multiple of 4,
+//     about N / 256): 16-row MFMA tiles, the last one partial (its missing
+//     rows are not loaded and not stored);
+//   * x is copied into LDS in chunks of KC columns (one padded bf16 row per
+//     row of x); with several chunks the next one's loads are in flight while
+//     the current one is used, and a barrier per chunk swaps the two buffers;
+//   * wave (wt, wk) takes tiles wt, wt + WT, .. (TPW of them) and a contiguous
+//     run of IPW 128-wide K blocks of every chunk; lane (row l%16, group
+//     g = l/16) loads bytes 16g .. 16g+15 of every 64-byte step of its row
+//     (non-temporal: each weight byte is read once per call); the first 8
+//     bytes feed one MFMA and the next 8 another, x fragments in the same
+//     K order, so one x fragment read serves all TPW tiles;
+//   * each 128-wide block's sum is scaled by its scale_inv (the D lanes' four
+//     rows share a 128-row scale block), like the other paths;
+//   * the WK waves of a tile meet in LDS once at the end, in wave order, and
+//     the GEMV epilogue stores four rows per lane: no K parts, no finish.
+// Optional input RMSNorm (p.xnorm, one chunk only): wave m normalises row m
+// of x in LDS exactly as rms_norm does (bf16(bf16(x * r) * xg)) while the
+// first weight items are in flight; with xg and no xnorm the GEMV takes
+// bf16(x * xg).
+constexpr int XG_WAVES = 8;
+constexpr int XG_MAXM = 8;
+
+template <int TPW, int WT, int IPW, int NCH>
+struct XgShape {
+  static constexpr int WK = XG_WAVES / WT;
+  static constexpr int KC = IPW * WK * 128;  // columns of one x chunk
+  static constexpr int PITCH = KC * 2 + 16;  // bytes per x row in LDS: the 16 rows of a fragment read differ in bits 4-7
+  static constexpr int NXB = NCH > 1 ? 2 : 1;
+  static constexpr int NIT = NCH * IPW;      // 128-wide blocks per wave
+  static constexpr int XPT = KC / 512;       // 16-byte x pieces per thread and chunk (8 rows)
+  static constexpr size_t LDS = (size_t)NXB * XG_MAXM * PITCH + (size_t)XG_WAVES * TPW * 64 * 16;
+};
+
+template <int TPW, int WT, int IPW, int NCH, int D, int MODE>
+__global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
+  typedef XgShape<TPW, WT, IPW, NCH> S;
+  static_assert(D >= 1 && D <= S::NIT && TPW * WT <= 8, "items in flight within the wave's items; tiles fit one pass");
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  constexpr int WK = S::WK, KC = S::KC, PITCH = S::PITCH, NIT = S::NIT, XPT = S::XPT;
+  extern __shared__ __align__(16) uint8_t xsm[];
+  const int M = p.M;
+  f32x4 *const red = reinterpret_cast<f32x4 *>(xsm + (size_t)S::NXB * XG_MAXM * PITCH);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wt = wave % WT, wk = wave / WT;
+  const int li = lane & 15, lg = lane >> 4;
+  const int r0 = blockIdx.x * rpw;
+  const int rend = min(r0 + rpw, p.N);
+  const int KB = p.K >> 7;
+  const bool two = MODE == GEMV_QKVA || p.w1 != nullptr;
+
+  // this lane's weight row (A operand: row li of each tile; rows past the
+  // run re-read its last row, whose results are not stored) and the scale row
+  // of its output rows (D: rows 4 lg .. 4 lg + 3 of each tile).  Every load
+  // of the stream is unconditional, so the compiler's waits count exactly
+  // the items in flight.
+  const uint8_t *wrow[TPW];
+  const float *srow[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int t0 = r0 + 16 * (wt + WT * j);
+    const int rc = min(t0 + li, rend - 1);
+    const bool s1 = two && rc >= p.n_split;
+    wrow[j] = (s1 ? p.w1 : p.w0) + (size_t)(s1 ? rc - p.n_split : rc) * p.K + 16 * lg;
+    const int rd = min(t0 + 4 * lg, p.N - 1);
+    const bool d1 = two && rd >= p.n_split;
+    srow[j] = (d1 ? p.s1 : p.s0) + (size_t)((d1 ? rd - p.n_split : rd) >> 7) * KB;
+  }
+
+  // x chunk c -> registers (piece q of this thread: row q / (KC / 8), 16-byte
+  // column piece q % (KC / 8); rows past M re-read row M - 1 and are not stored)
+  u32x4 xs[XPT];
+  auto load_x = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int q = tid + 512 * i, m = min(q / (KC / 8), M - 1), c8 = q % (KC / 8);
+      xs[i] = ldg16(p.x + (size_t)m * p.ldx + (size_t)c * KC + c8 * 8);
+    }
+  };
+  auto store_x = [&](int buf) __attribute__((always_inline)) {
+    uint8_t *xb = xsm + (size_t)buf * XG_MAXM * PITCH;
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int q = tid + 512 * i, m = q / (KC / 8), c8 = q % (KC / 8);
+      *reinterpret_cast<u32x4 *>(xb + m * PITCH + c8 * 16) = xs[i];
+    }
+  };
+  // LDS-only barrier: the weight loads in flight are not waited for
+  auto lds_barrier = [&]() __attribute__((always_inline)) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // weight items: item i = block ii of chunk c, both 64-byte steps of each tile
+  u32x4 W[NIT][TPW][2];
+  float SC[NIT][TPW];
+  auto load_w = [&](int i) __attribute__((always_inline)) {
+    const int c = i / IPW, ii = i % IPW;
+    const int kb = c * (IPW * WK) + wk * IPW + ii;
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st) W[i][j][st] = ldg16_nt(wrow[j] + (size_t)kb * 128 + 64 * st);
+      SC[i][j] = srow[j][kb];
+    }
+  };
+
+  // The scheduler barriers keep every load where it is written: loads complete
+  // in issue order, so a load moved later would make the wait for an earlier
+  // one (the compiler's or the x chunk's) wait for it too.
+  // x first, then the norm weight's pieces of this lane (one chunk only;
+  // unconditional, from x when there is none), then the weights: waiting for
+  // x and xg does not wait for the weights
+  constexpr int PL = NCH == 1 ? KC / 512 : 1;  // 16-byte pieces per lane of a row
+  u32x4 g[PL];
+  load_x(0);
+  if (NCH == 1) {
+    const uint16_t *gp = p.xg ? p.xg : p.x;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) g[i] = ldg16(gp + (lane + 64 * i) * 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < D; ++i) load_w(i);
+  __builtin_amdgcn_sched_barrier(0);
+  store_x(0);
+  if (NCH == 1 && p.xg) {
+    // rms_norm(x, xg, eps_in) of each row (inference/ops.py:10-12) in place,
+    // wave m on row m, or bf16(x * xg)
+    lds_barrier();
+    if (wave < M) {
+      uint8_t *xr = xsm + wave * PITCH;
+      u32x4 v[PL];
+#pragma unroll
+      for (int i = 0; i < PL; ++i) v[i] = *reinterpret_cast<const u32x4 *>(xr + (lane + 64 * i) * 16);
+      if (p.xnorm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < PL; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ss += lo_bf(v[i][e]) * lo_bf(v[i][e]) + hi_bf(v[i][e]) * hi_bf(v[i][e]);
+        const float r = rsqrtf(vg_sum64(ss) / (float)p.K + p.eps_in);
+#pragma unroll
+        for (int i = 0; i < PL; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            v[i][e] = pack_bf16(round_bf16(lo_bf(v[i][e]) * r) * lo_bf(g[i][e]),
+                                round_bf16(hi_bf(v[i][e]) * r) * hi_bf(g[i][e]));
+      } else {
+#pragma unroll
+        for (int i = 0; i < PL; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            v[i][e] = pack_bf16(lo_bf(v[i][e]) * lo_bf(g[i][e]), hi_bf(v[i][e]) * hi_bf(g[i][e]));
+      }
+#pragma unroll
+      for (int i = 0; i < PL; ++i) *reinterpret_cast<u32x4 *>(xr + (lane + 64 * i) * 16) = v[i];
+    }
+  }
+  lds_barrier();
+  if (NCH > 1) load_x(1);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // B operand column li holds x row li % M: the columns past M repeat real
+  // rows (no conditional reads) and their sums are not stored
+  const int xrow = li % M;
+  f32x4 acc[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NIT; ++i) {
+    const int c = i / IPW, ii = i % IPW;
+    if (i + D < NIT) load_w(i + D);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t *xb = xsm + (size_t)(c % S::NXB) * XG_MAXM * PITCH + xrow * PITCH +
+                        ((wk * IPW + ii) * 128 + 16 * lg) * 2;
+    bf16x8 xf[2][2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) xf[st][h] = as_bf16x8(*reinterpret_cast<const u32x4 *>(xb + 128 * st + 16 * h));
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const u32x4 w = W[i][j][st];
+        bf16x2_t q[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          q[2 * e] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[e], 1.f, false);
+          q[2 * e + 1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[e], 1.f, true);
+        }
+        const bf16x8 a0 = {q[0][0], q[0][1], q[1][0], q[1][1], q[2][0], q[2][1], q[3][0], q[3][1]};
+        const bf16x8 a1 = {q[4][0], q[4][1], q[5][0], q[5][1], q[6][0], q[6][1], q[7][0], q[7][1]};
+        s = mfma16(a0, xf[st][0], s);
+        s = mfma16(a1, xf[st][1], s);
+      }
+      acc[j] += SC[i][j] * s;
+    }
+    if (NCH > 1 && ii == IPW - 1 && c + 1 < NCH) {
+      // chunk c done: the next one into the other buffer (free since the last
+      // barrier), then the one after that on its way
+      store_x((c + 1) % 2);
+      lds_barrier();
+      if (c + 2 < NCH) load_x(c + 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) red[(wave * TPW + j) * 64 + lane] = acc[j];
+  lds_barrier();
+  const int ntile = (rend - r0 + 15) >> 4;
+  if (tid < ntile * 64) {
+    const int tw = tid >> 6, ln = tid & 63;
+    const int wtt = tw % WT, j = tw / WT;
+    f32x4 v = red[(wtt * TPW + j) * 64 + ln];
+#pragma unroll
+    for (int k = 1; k < WK; ++k) v += red[((k * WT + wtt) * TPW + j) * 64 + ln];
+    const int m = ln & 15, n = r0 + 16 * tw + 4 * (ln >> 4);
+    if (m < M && n < rend) store4<MODE>(p, m, n, v);
+  }
+}
+
+// The shapes with an instantiation: K, tiles per wave, wave rows WT, blocks per
+// wave and chunk, chunks, items in flight; rows per workgroup fall in
+// (16 (TPW WT - 1) .. 16 TPW WT] (1 .. 16 for one tile).
+struct XgCfg {
+  int K, tpw, wt, ipw, nch, d;
+};
+constexpr XgCfg XG_CFGS[] = {
+    {16384, 2, 1, 4, 4, 4},  // o_proj (7168 x 16384): 28 rows per workgroup
+    {7168, 1, 1, 7, 1, 7},   // q_a | kv_a (2112 x 7168), q_a, kv_a: up to 16 rows
+    {1536, 3, 2, 3, 1, 3},   // q_b (24576 x 1536): 96 rows
+    {512, 1, 8, 4, 1, 4},    // kv_b (32768 x 512): 128 rows
+};
+constexpr int XG_NCFG = sizeof(XG_CFGS) / sizeof(XG_CFGS[0]);
+
+static int xgemv_rpw(int N) { return std::max(4, ((N + 255) / 256 + 3) & ~3); }
+
+static int xgemv_cfg(int M, int N, int K) {
+  if (M < 2 || M > XG_MAXM || N % 4 || K % 128) return -1;
+  const int rpw = xgemv_rpw(N);
+  for (int c = 0; c < XG_NCFG; ++c) {
+    const XgCfg &g = XG_CFGS[c];
+    const int cap = 16 * g.tpw * g.wt;
+    if (g.K == K && rpw <= cap && rpw > cap - 16 * g.wt) return c;
+  }
+  return -1;
+}
+
+template <int TPW, int WT, int IPW, int NCH, int D, int MODE>
+static void launch_xg(const GemvParams &p, int rpw, unsigned groups, hipStream_t st) {
+  static bool attr_set = false;  // raise the dynamic LDS limit once per process
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void *)xgemv_kernel<TPW, WT, IPW, NCH, D, MODE>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    attr_set = true;
+  }
+  xgemv_kernel<TPW, WT, IPW, NCH, D, MODE>
+      <<<groups, 512, XgShape<TPW, WT, IPW, NCH>::LDS, st>>>(p, rpw);
+}
+
+template <int TPW, int WT, int IPW, int NCH, int D>
+static void launch_xg_mode(const GemvParams &p, int mode, int rpw, unsigned groups, hipStream_t st) {
+  switch (mode) {
+    case GEMV_PLAIN: launch_xg<TPW, WT, IPW, NCH, D, GEMV_PLAIN>(p, rpw, groups, st); break;
+    case GEMV_RESID: launch_xg<TPW, WT, IPW, NCH, D, GEMV_RESID>(p, rpw, groups, st); break;
+    case GEMV_QKVA: launch_xg<TPW, WT, IPW, NCH, D, GEMV_QKVA>(p, rpw, groups, st); break;
+    case GEMV_F32: launch_xg<TPW, WT, IPW, NCH, D, GEMV_F32>(p, rpw, groups, st); break;
+    default: launch_xg<TPW, WT, IPW, NCH, D, GEMV_QROPE>(p, rpw, groups, st); break;
+  }
+}
+
+static int launch_xgemv(const GemvParams &p, int mode, hipStream_t st) {
+  const int c = xgemv_cfg(p.M, p.N, p.K);
+  if (c < 0) return fail(AMLA_EINVAL, "fp8 GEMV (x in LDS): plan for another shape (M=%d N=%d K=%d)", p.M, p.N, p.K);
+  if (p.ldx < p.K || p.ldx % 8 || !aligned16(p.x) || (p.xg && !aligned16(p.xg)))
+    return fail(AMLA_EINVAL, "fp8 GEMV (x in LDS): x must be 16-byte aligned rows of at least K elements");
+  if (p.xg && XG_CFGS[c].nch != 1)
+    return fail(AMLA_EUNSUPPORTED, "fp8 GEMV (x in LDS): an input norm needs K <= %d", XG_CFGS[1].K);
+  if ((mode == GEMV_QKVA || p.w1) && p.n_split % 4)
+    return fail(AMLA_EUNSUPPORTED, "fp8 GEMV (x in LDS): the first weight segment must be a multiple of 4 rows");
+  const int rpw = xgemv_rpw(p.N);
+  const unsigned groups = (unsigned)((p.N + rpw - 1) / rpw);
+  switch (c) {
+    case 0: launch_xg_mode<2, 1, 4, 4, 4>(p, mode, rpw, groups, st); break;
+    case 1: launch_xg_mode<1, 1, 7, 1, 7>(p, mode, rpw, groups, st); break;
+    case 2: launch_xg_mode<3, 2, 3, 1, 3>(p, mode, rpw, groups, st); break;
+    default: launch_xg_mode<1, 8, 4, 1, 4>(p, mode, rpw, groups, st); break;
+  }
+  return check_launch("fp8 GEMV (x in LDS)");
+}
+
 // rows per workgroup of the streaming GEMV: about VG_GRID workgroups
 static int vgemv_rpw(int N) {
   const int r = (N + VG_GRID - 1) / VG_GRID;
@@ -950,6 +1255,9 @@ GemvPlan plan_linear(int M, int N, int K) {
   } else if (vgemv_short_applies(M, N, K)) {
     pl.groups = (N + VGS_RPW - 1) / VGS_RPW;
     pl.vec = 2;
+  } else if (xgemv_cfg(M, N, K) >= 0) {
+    pl.groups = (N + xgemv_rpw(N) - 1) / xgemv_rpw(N);
+    pl.vec = 3;
   } else {
     return plan_gemv(M, N, K);
   }
@@ -960,6 +1268,7 @@ GemvPlan plan_linear(int M, int N, int K) {
 }
 
 static int launch_vgemv(const GemvParams &p, int mode, int vec, hipStream_t st) {
+  if (vec == 3) return launch_xgemv(p, mode, st);
   if (p.ldx < p.K || !aligned16(p.x) || (p.xg && !aligned16(p.xg)))
     return fail(AMLA_EINVAL, "streaming fp8 GEMV: x must be 16-byte aligned rows of at least K elements");
   if (vec == 2) {

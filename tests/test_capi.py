@@ -83,18 +83,21 @@ def test_null_and_bad_arguments_fail_before_launch():
     assert L.amla_fp8_linear(p, 1, 100, 100, p, p, 16, p, 16, None, 0, None) == -3
     assert L.amla_fp8_linear(p, 1, 128, 64, p, p, 16, p, 16, None, 0, None) == -1
     # a K that needs partial sums, without workspace: rejected before launch
-    assert L.amla_fp8_linear(p, 8, 16384, 16384, p, p, 7168, p, 7168, None, 0, None) == -2
+    assert L.amla_fp8_linear(p, 16, 16384, 16384, p, p, 7168, p, 7168, None, 0, None) == -2
     assert b"workspace" in L.amla_last_error()
-    # one row of x takes the streaming GEMV over the whole K: no workspace
+    # one row of x takes the streaming GEMV over the whole K, 2-8 rows at the projection shapes
+    # the GEMV with x in LDS: no workspace; 9-64 rows the skinny GEMM's K parts
     assert L.amla_fp8_linear_workspace_bytes(1, 7168, 16384) == 0
-    assert L.amla_fp8_linear_workspace_bytes(8, 7168, 16384) > 0
+    assert L.amla_fp8_linear_workspace_bytes(8, 7168, 16384) == 0
+    assert L.amla_fp8_linear_workspace_bytes(8, 2112, 7168) == 0
+    assert L.amla_fp8_linear_workspace_bytes(16, 7168, 16384) > 0
 
 
 def test_workspace_queries():
     L = _lib.lib()
-    # wo at M=8: K = 16384 is split into parts whose fp32 sums need workspace
-    n = L.amla_fp8_linear_workspace_bytes(8, 7168, 16384)
-    assert n > 0 and n % (8 * 7168 * 4) == 0
+    # wo at M=16: K = 16384 is split into parts whose fp32 sums need workspace
+    n = L.amla_fp8_linear_workspace_bytes(16, 7168, 16384)
+    assert n > 0 and n % (16 * 7168 * 4) == 0
     assert L.amla_fp8_linear_workspace_bytes(8, 24576, 1536) == 0     # one K part
     assert L.amla_fp8_linear_workspace_bytes(4096, 24576, 1536) == 0   # the large-M GEMM needs none
     a = _lib.MlaArgs()

@@ -43,9 +43,10 @@ def test_dequant_r1_weights_bit_exact(name):
 
 
 @pytest.mark.parametrize("name", list(SHAPES))
-@pytest.mark.parametrize("M", [1, 8, 17, 32, 64])
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 17, 32, 64])
 def test_fp8_linear_r1_shapes(name, M):
-    """M 1-16 and 17-32 hold x in registers (one and two 16-row tiles), 33-64 stage it in LDS."""
+    """M = 1 takes the streaming GEMVs, 2-8 the GEMV with x in LDS at these shapes (masked
+    columns past M), 9-64 the skinny GEMM (one, two or four 16-row x tiles in registers)."""
     print(f"[case] fp8_linear {name} M={M}", flush=True)
     w, s = _w(name)
     x = synth.randn((M, SHAPES[name][1]), synth.seed_of("fp8x", name, M)).to(torch.bfloat16)

@@ -300,6 +300,16 @@ def test_layer_mode_batch1_cache_rows():
         _check_cache(gc, rc, [(pos, pos + 1)])
 
 
+def test_layer_mode_batch8_cache_rows():
+    """Layer-mode decode of 2-8 sequences: the q_a|kv_a GEMV with x in LDS normalises each x row
+    with the reference's rounding (inference/ops.py:10-12) and q_b's normalises q_a, so the new
+    cache rows are within 2 bf16 ulps of the oracle's."""
+    for tag, B, pos, max_seq in (("layerb8", 8, 300, 304), ("layerb3", 3, 1000, 1008)):
+        got, want, gc, rc = _run_case(tag, B, 1, pos, max_seq, layer_mode=True)
+        assert_parity(got, want, f"layer {tag}")
+        _check_cache(gc, rc, [(pos, pos + 1)] * B)
+
+
 def test_prefill_row_equals_decode():
     """Prefill of S tokens, row S-1 == prefill of S-1 tokens followed by a decode step."""
     lay = _layer("mla/consistency")
