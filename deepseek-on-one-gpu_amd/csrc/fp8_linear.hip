@@ -958,7 +958,8 @@ struct XgShape {
   static constexpr int NXB = NCH > 1 ? 2 : 1;
   static constexpr int NIT = NCH * IPW;      // 128-wide blocks per wave
   static constexpr int XPT = KC / 512;       // 16-byte x pieces per thread and chunk (8 rows)
-  static constexpr size_t LDS = (size_t)NXB * XG_MAXM * PITCH + (size_t)XG_WAVES * TPW * 64 * 16;
+  static constexpr size_t GAM = NCH == 1 ? (size_t)KC * 2 : 0;  // the norm weight (one chunk only)
+  static constexpr size_t LDS = (size_t)NXB * XG_MAXM * PITCH + GAM + (size_t)XG_WAVES * TPW * 64 * 16;
 };
 
 template <int TPW, int WT, int IPW, int NCH, int D, int MODE>
@@ -969,7 +970,8 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
   constexpr int WK = S::WK, KC = S::KC, PITCH = S::PITCH, NIT = S::NIT, XPT = S::XPT;
   extern __shared__ __align__(16) uint8_t xsm[];
   const int M = p.M;
-  f32x4 *const red = reinterpret_cast<f32x4 *>(xsm + (size_t)S::NXB * XG_MAXM * PITCH);
+  uint8_t *const gsm = xsm + (size_t)S::NXB * XG_MAXM * PITCH;  // norm weight, bf16
+  f32x4 *const red = reinterpret_cast<f32x4 *>(gsm + S::GAM);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -980,19 +982,29 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
   const int KB = p.K >> 7;
   const bool two = MODE == GEMV_QKVA || p.w1 != nullptr;
 
-  // this lane's weight row (A operand: row li of each tile; rows past the
-  // run re-read its last row, whose results are not stored) and the scale row
-  // of its output rows (D: rows 4 lg .. 4 lg + 3 of each tile).  Every load
-  // of the stream is unconditional, so the compiler's waits count exactly
-  // the items in flight.
-  const uint8_t *wrow[TPW];
+  // Weight loads read whole 128-byte lines: for each tile and 128-wide block
+  // one load covers rows 0-7 and one rows 8-15, lane l taking row l & 7 and
+  // 16-byte chunk cl = ((l >> 4) & 1) + 2 (l >> 5) + 4 ((l >> 3) & 1) of the
+  // block (eight lanes per row).  One lane swap (lanes l and l ^ 8, selected
+  // by bit 3) turns the pair into the MFMA fragment order: lane (row l % 16,
+  // group l / 16) with chunks g and 4 + g.  Rows past the run re-read its last
+  // row (the same addresses: no extra traffic; their results are not stored).
+  // The scale row is that of the output rows (D: rows 4 lg .. 4 lg + 3 of each
+  // tile).  Every load of the stream is unconditional, so the compiler's waits
+  // count exactly the items in flight.
+  const int cl = ((lane >> 4) & 1) + 2 * (lane >> 5) + 4 * ((lane >> 3) & 1);
+  const bool hi8 = (lane >> 3) & 1;
+  const uint8_t *wrow[TPW][2];
   const float *srow[TPW];
 #pragma unroll
   for (int j = 0; j < TPW; ++j) {
     const int t0 = r0 + 16 * (wt + WT * j);
-    const int rc = min(t0 + li, rend - 1);
-    const bool s1 = two && rc >= p.n_split;
-    wrow[j] = (s1 ? p.w1 : p.w0) + (size_t)(s1 ? rc - p.n_split : rc) * p.K + 16 * lg;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int rc = min(t0 + 8 * hf + (lane & 7), rend - 1);
+      const bool s1 = two && rc >= p.n_split;
+      wrow[j][hf] = (s1 ? p.w1 : p.w0) + (size_t)(s1 ? rc - p.n_split : rc) * p.K + 16 * cl;
+    }
     const int rd = min(t0 + 4 * lg, p.N - 1);
     const bool d1 = two && rd >= p.n_split;
     srow[j] = (d1 ? p.s1 : p.s0) + (size_t)((d1 ? rd - p.n_split : rd) >> 7) * KB;
@@ -1032,7 +1044,7 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
 #pragma unroll
-      for (int st = 0; st < 2; ++st) W[i][j][st] = ldg16_nt(wrow[j] + (size_t)kb * 128 + 64 * st);
+      for (int hf = 0; hf < 2; ++hf) W[i][j][hf] = ldg16_nt(wrow[j][hf] + (size_t)kb * 128);
       SC[i][j] = srow[j][kb];
     }
   };
@@ -1040,53 +1052,58 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
   // The scheduler barriers keep every load where it is written: loads complete
   // in issue order, so a load moved later would make the wait for an earlier
   // one (the compiler's or the x chunk's) wait for it too.
-  // x first, then the norm weight's pieces of this lane (one chunk only;
-  // unconditional, from x when there is none), then the weights: waiting for
-  // x and xg does not wait for the weights
-  constexpr int PL = NCH == 1 ? KC / 512 : 1;  // 16-byte pieces per lane of a row
-  u32x4 g[PL];
+  // x first, then the norm weight (one chunk only; unconditional, from x when
+  // there is none; staged in LDS), then the weights: waiting for x and xg does
+  // not wait for the weights
+  constexpr int PL = KC / 512;                    // 16-byte pieces per lane of a row
+  constexpr int GPT = (KC / 8 + 511) / 512;       // 16-byte norm weight pieces per thread
+  u32x4 gs[GPT];
   load_x(0);
   if (NCH == 1) {
     const uint16_t *gp = p.xg ? p.xg : p.x;
 #pragma unroll
-    for (int i = 0; i < PL; ++i) g[i] = ldg16(gp + (lane + 64 * i) * 8);
+    for (int i = 0; i < GPT; ++i) gs[i] = ldg16(gp + min(tid + 512 * i, KC / 8 - 1) * 8);
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 0; i < D; ++i) load_w(i);
   __builtin_amdgcn_sched_barrier(0);
   store_x(0);
+  if (NCH == 1) {
+#pragma unroll
+    for (int i = 0; i < GPT; ++i)
+      if (tid + 512 * i < KC / 8) *reinterpret_cast<u32x4 *>(gsm + (tid + 512 * i) * 16) = gs[i];
+  }
   if (NCH == 1 && p.xg) {
     // rms_norm(x, xg, eps_in) of each row (inference/ops.py:10-12) in place,
     // wave m on row m, or bf16(x * xg)
     lds_barrier();
     if (wave < M) {
       uint8_t *xr = xsm + wave * PITCH;
-      u32x4 v[PL];
-#pragma unroll
-      for (int i = 0; i < PL; ++i) v[i] = *reinterpret_cast<const u32x4 *>(xr + (lane + 64 * i) * 16);
+      // two passes over the row in LDS (few registers while the weights are
+      // in flight): the sum of squares, then bf16(bf16(x * r) * xg); without
+      // the norm r = 1 and bf16(x * 1) = x
+      float r = 1.f;
       if (p.xnorm) {
         float ss = 0.f;
 #pragma unroll
-        for (int i = 0; i < PL; ++i)
+        for (int i = 0; i < PL; ++i) {
+          const u32x4 v = *reinterpret_cast<const u32x4 *>(xr + (lane + 64 * i) * 16);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) ss += lo_bf(v[i][e]) * lo_bf(v[i][e]) + hi_bf(v[i][e]) * hi_bf(v[i][e]);
-        const float r = rsqrtf(vg_sum64(ss) / (float)p.K + p.eps_in);
-#pragma unroll
-        for (int i = 0; i < PL; ++i)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            v[i][e] = pack_bf16(round_bf16(lo_bf(v[i][e]) * r) * lo_bf(g[i][e]),
-                                round_bf16(hi_bf(v[i][e]) * r) * hi_bf(g[i][e]));
-      } else {
-#pragma unroll
-        for (int i = 0; i < PL; ++i)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            v[i][e] = pack_bf16(lo_bf(v[i][e]) * lo_bf(g[i][e]), hi_bf(v[i][e]) * hi_bf(g[i][e]));
+          for (int e = 0; e < 4; ++e) ss += lo_bf(v[e]) * lo_bf(v[e]) + hi_bf(v[e]) * hi_bf(v[e]);
+        }
+        r = rsqrtf(vg_sum64(ss) / (float)p.K + p.eps_in);
       }
 #pragma unroll
-      for (int i = 0; i < PL; ++i) *reinterpret_cast<u32x4 *>(xr + (lane + 64 * i) * 16) = v[i];
+      for (int i = 0; i < PL; ++i) {
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(xr + (lane + 64 * i) * 16);
+        const u32x4 g = *reinterpret_cast<const u32x4 *>(gsm + (lane + 64 * i) * 16);
+        u32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = pack_bf16(round_bf16(lo_bf(v[e]) * r) * lo_bf(g[e]), round_bf16(hi_bf(v[e]) * r) * hi_bf(g[e]));
+        *reinterpret_cast<u32x4 *>(xr + (lane + 64 * i) * 16) = y;
+      }
     }
   }
   lds_barrier();
@@ -1113,10 +1130,20 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
       for (int h = 0; h < 2; ++h) xf[st][h] = as_bf16x8(*reinterpret_cast<const u32x4 *>(xb + 128 * st + 16 * h));
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
+      // rows 0-7 | rows 8-15 -> fragment order: step 0 (chunks 0-3), step 1 (4-7)
+      u32x4 wf[2];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t x0 = W[i][j][0][e], x1 = W[i][j][1][e];
+        const uint32_t r0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x0, 0x128, 0xf, 0xf, false);  // row_ror:8
+        const uint32_t r1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x1, 0x128, 0xf, 0xf, false);
+        wf[0][e] = hi8 ? r1 : x0;
+        wf[1][e] = hi8 ? x1 : r0;
+      }
       f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
-        const u32x4 w = W[i][j][st];
+        const u32x4 w = wf[st];
         bf16x2_t q[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
