@@ -958,8 +958,16 @@ struct XgShape {
   static constexpr int NXB = NCH > 1 ? 2 : 1;
   static constexpr int NIT = NCH * IPW;      // 128-wide blocks per wave
   static constexpr int XPT = KC / 512;       // 16-byte x pieces per thread and chunk (8 rows)
+  // several chunks with one tile group: each wave reads only its own columns
+  // of x (IPW blocks per chunk), so each stages them itself in its own two
+  // buffers and no barrier is needed between chunks
+  static constexpr bool XWAVE = NCH > 1 && WT == 1;
+  static constexpr int WSLICE = IPW * 128;       // columns of a wave's slice of a chunk
+  static constexpr int WPITCH = WSLICE * 2 + 16;  // bytes per x row of a slice
+  static constexpr int XWP = WSLICE / 64;         // 16-byte pieces per lane and slice (8 rows)
+  static constexpr size_t XLDS = XWAVE ? (size_t)XG_WAVES * 2 * XG_MAXM * WPITCH : (size_t)NXB * XG_MAXM * PITCH;
   static constexpr size_t GAM = NCH == 1 ? (size_t)KC * 2 : 0;  // the norm weight (one chunk only)
-  static constexpr size_t LDS = (size_t)NXB * XG_MAXM * PITCH + GAM + (size_t)XG_WAVES * TPW * 64 * 16;
+  static constexpr size_t LDS = XLDS + GAM + (size_t)XG_WAVES * TPW * 64 * 16;
 };
 
 template <int TPW, int WT, int IPW, int NCH, int D, int MODE>
@@ -970,7 +978,7 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
   constexpr int WK = S::WK, KC = S::KC, PITCH = S::PITCH, NIT = S::NIT, XPT = S::XPT;
   extern __shared__ __align__(16) uint8_t xsm[];
   const int M = p.M;
-  uint8_t *const gsm = xsm + (size_t)S::NXB * XG_MAXM * PITCH;  // norm weight, bf16
+  uint8_t *const gsm = xsm + S::XLDS;  // norm weight, bf16
   f32x4 *const red = reinterpret_cast<f32x4 *>(gsm + S::GAM);
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1028,6 +1036,24 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
       *reinterpret_cast<u32x4 *>(xb + m * PITCH + c8 * 16) = xs[i];
     }
   };
+  // a wave's own slice of chunk c (XWAVE): rows past M re-read row M - 1
+  constexpr int WSLICE = S::WSLICE, WPITCH = S::WPITCH, XWP = S::XWP;
+  u32x4 xw[S::XWAVE ? XWP : 1];
+  auto load_xw = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < XWP; ++i) {
+      const int q = lane + 64 * i, m = min(q / (WSLICE / 8), M - 1), c8 = q % (WSLICE / 8);
+      xw[i] = ldg16(p.x + (size_t)m * p.ldx + (size_t)c * KC + wk * WSLICE + c8 * 8);
+    }
+  };
+  auto store_xw = [&](int buf) __attribute__((always_inline)) {
+    uint8_t *xb = xsm + (size_t)((wave * 2 + buf) * XG_MAXM) * WPITCH;
+#pragma unroll
+    for (int i = 0; i < XWP; ++i) {
+      const int q = lane + 64 * i, m = q / (WSLICE / 8), c8 = q % (WSLICE / 8);
+      *reinterpret_cast<u32x4 *>(xb + m * WPITCH + c8 * 16) = xw[i];
+    }
+  };
   // LDS-only barrier: the weight loads in flight are not waited for
   auto lds_barrier = [&]() __attribute__((always_inline)) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1058,7 +1084,8 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
   constexpr int PL = KC / 512;                    // 16-byte pieces per lane of a row
   constexpr int GPT = (KC / 8 + 511) / 512;       // 16-byte norm weight pieces per thread
   u32x4 gs[GPT];
-  load_x(0);
+  if constexpr (S::XWAVE) load_xw(0);
+  else load_x(0);
   if (NCH == 1) {
     const uint16_t *gp = p.xg ? p.xg : p.x;
 #pragma unroll
@@ -1068,7 +1095,8 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
 #pragma unroll
   for (int i = 0; i < D; ++i) load_w(i);
   __builtin_amdgcn_sched_barrier(0);
-  store_x(0);
+  if constexpr (S::XWAVE) store_xw(0);  // this wave's own reads follow in order: no barrier
+  else store_x(0);
   if (NCH == 1) {
 #pragma unroll
     for (int i = 0; i < GPT; ++i)
@@ -1106,8 +1134,12 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
       }
     }
   }
-  lds_barrier();
-  if (NCH > 1) load_x(1);
+  if constexpr (S::XWAVE) {
+    load_xw(1);
+  } else {
+    lds_barrier();
+    if (NCH > 1) load_x(1);
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // B operand column li holds x row li % M: the columns past M repeat real
@@ -1121,8 +1153,9 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
     const int c = i / IPW, ii = i % IPW;
     if (i + D < NIT) load_w(i + D);
     __builtin_amdgcn_sched_barrier(0);
-    const uint8_t *xb = xsm + (size_t)(c % S::NXB) * XG_MAXM * PITCH + xrow * PITCH +
-                        ((wk * IPW + ii) * 128 + 16 * lg) * 2;
+    const uint8_t *xb = S::XWAVE ? xsm + (size_t)((wave * 2 + c % 2) * XG_MAXM + xrow) * WPITCH + (ii * 128 + 16 * lg) * 2
+                                 : xsm + (size_t)(c % S::NXB) * XG_MAXM * PITCH + xrow * PITCH +
+                                       ((wk * IPW + ii) * 128 + 16 * lg) * 2;
     bf16x8 xf[2][2];
 #pragma unroll
     for (int st = 0; st < 2; ++st)
@@ -1160,9 +1193,14 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
     if (NCH > 1 && ii == IPW - 1 && c + 1 < NCH) {
       // chunk c done: the next one into the other buffer (free since the last
       // barrier), then the one after that on its way
-      store_x((c + 1) % 2);
-      lds_barrier();
-      if (c + 2 < NCH) load_x(c + 2);
+      if constexpr (S::XWAVE) {
+        store_xw((c + 1) % 2);  // the buffer of chunk c - 1, which this wave has finished
+        if (c + 2 < NCH) load_xw(c + 2);
+      } else {
+        store_x((c + 1) % 2);
+        lds_barrier();
+        if (c + 2 < NCH) load_x(c + 2);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
