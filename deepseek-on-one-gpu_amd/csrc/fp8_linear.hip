@@ -930,15 +930,18 @@ __global__ __launch_bounds__(256, 2) void vgemv_short_kernel(GemvParams p) {
 //   * one workgroup per CU (8 waves) owns a run of rpw rows (a multiple of 4,
 //     about N / 256): 16-row MFMA tiles, the last one partial (its missing
 //     rows are not loaded and not stored);
-//   * x is copied into LDS in chunks of KC columns (one padded bf16 row per
-//     row of x); with several chunks the next one's loads are in flight while
-//     the current one is used, and a barrier per chunk swaps the two buffers;
+//   * x is copied into LDS (one padded bf16 row per row of x) whole, or in
+//     chunks of KC columns when it does not fit: then each wave stages only
+//     the columns it reads, in two buffers of its own (the next chunk's loads
+//     in flight while the current one is used), so no barrier is needed;
 //   * wave (wt, wk) takes tiles wt, wt + WT, .. (TPW of them) and a contiguous
-//     run of IPW 128-wide K blocks of every chunk; lane (row l%16, group
-//     g = l/16) loads bytes 16g .. 16g+15 of every 64-byte step of its row
-//     (non-temporal: each weight byte is read once per call); the first 8
-//     bytes feed one MFMA and the next 8 another, x fragments in the same
-//     K order, so one x fragment read serves all TPW tiles;
+//     run of IPW 128-wide K blocks of every chunk; the weights are read in
+//     whole 128-byte lines (eight rows per load, non-temporal: each weight
+//     byte is read once per call) and one lane swap puts them in the MFMA
+//     fragment order, lane (row l%16, group g = l/16) holding bytes 16g ..
+//     16g+15 and 64+16g .. of the block; the first 8 bytes of each feed one
+//     MFMA and the next 8 another, x fragments in the same K order, so one x
+//     fragment read serves all TPW tiles;
 //   * each 128-wide block's sum is scaled by its scale_inv (the D lanes' four
 //     rows share a 128-row scale block), like the other paths;
 //   * the WK waves of a tile meet in LDS once at the end, in wave order, and

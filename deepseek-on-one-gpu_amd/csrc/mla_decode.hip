@@ -167,8 +167,11 @@ AMLA_DEV void build_split_plan(const int32_t *__restrict__ pos, int tmax, int B,
 
 // One workgroup per (head, 128-column quarter of the latent, group of BB
 // sequences; BB = 1, 2, 4 or 8, the smallest that holds the batch up to 8),
-// and workgroup (HEADS, 0, 0) writes the split plan table of a batch with
-// unequal tile counts.  Thread (dg, cc) sums rows 8*dg .. 8*dg+7 of W_UK[h] (eight
+// and workgroup (0, 0, 0) also writes the split plan table of a batch with
+// unequal tile counts.  The grid, 512 workgroups up to batch 8, is one round
+// of two workgroups per CU; the quarters of head h share its XCD (workgroup
+// i runs on XCD i mod 8 and HEADS is a multiple of 8), where they share its
+// query rows in L2.  Thread (dg, cc) sums rows 8*dg .. 8*dg+7 of W_UK[h] (eight
 // independent 8-byte loads in flight) for 8 latent columns; the 16 row groups
 // reduce through LDS.  W_UK[h] = kv_b rows h*256 .. h*256+127 lie in one
 // 128-row scale block.
@@ -183,12 +186,14 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
   __shared__ float qn[BB][NOPE];
   __shared__ f32x4 red[16][BB][16][2];
   static_assert(sizeof(red) >= (2 * 64 + 4) * sizeof(int), "the plan's scratch (batch <= 64) fits red");
-  if (blockIdx.x >= HEADS) {
-    if (blockIdx.x == HEADS && blockIdx.y == 0 && blockIdx.z == 0) {
-      const int2 r = batch_tile_range(pos, tmax, B);
-      if (r.x != r.y) build_split_plan(pos, tmax, B, units, slots, plan, reinterpret_cast<int *>(&red[0][0][0][0]));
+  if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {
+    // the first workgroup also writes the split plan (its scratch is red,
+    // rewritten below after the barrier)
+    const int2 r = batch_tile_range(pos, tmax, B);
+    if (r.x != r.y) {
+      build_split_plan(pos, tmax, B, units, slots, plan, reinterpret_cast<int *>(&red[0][0][0][0]));
+      __syncthreads();
     }
-    return;
   }
   const int h = blockIdx.x, quarter = blockIdx.y;
   const int b0 = blockIdx.z * BB;
@@ -1319,24 +1324,20 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   mark(ev, 3, st);
   int32_t *plan = reinterpret_cast<int32_t *>(ws + L.plan);
   const int tmax = mla_context_bound(*a);
-  // x = HEADS + 8: workgroup (HEADS, 0, 0) writes the plan table, the others
-  // past HEADS return at once; a row length that is a multiple of 8 keeps the
-  // quarters of head h on one XCD (workgroup i runs on XCD i mod 8), where
-  // they share its query rows in L2
   {
     const uint8_t *wkvb = reinterpret_cast<const uint8_t *>(a->w_kv_b);
     const uint16_t *gkv = reinterpret_cast<const uint16_t *>(a->gamma_kv);
     if (B == 1)
-      absorb_kernel<1><<<dim3(HEADS + 8, LORA / 128, 1), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions,
+      absorb_kernel<1><<<dim3(HEADS, LORA / 128, 1), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions,
                                                                        tmax, L.units, L.slots, plan);
     else if (B == 2)
-      absorb_kernel<2><<<dim3(HEADS + 8, LORA / 128, 1), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions,
+      absorb_kernel<2><<<dim3(HEADS, LORA / 128, 1), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions,
                                                                        tmax, L.units, L.slots, plan);
     else if (B <= 4)
-      absorb_kernel<4><<<dim3(HEADS + 8, LORA / 128, 1), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions,
+      absorb_kernel<4><<<dim3(HEADS, LORA / 128, 1), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions,
                                                                        tmax, L.units, L.slots, plan);
     else
-      absorb_kernel<8><<<dim3(HEADS + 8, LORA / 128, (B + 7) / 8), 256, 0, st>>>(
+      absorb_kernel<8><<<dim3(HEADS, LORA / 128, (B + 7) / 8), 256, 0, st>>>(
           q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions, tmax, L.units, L.slots, plan);
   }
   if ((rc = check_launch("mla absorb"))) return rc;
