@@ -165,13 +165,12 @@ AMLA_DEV void build_split_plan(const int32_t *__restrict__ pos, int tmax, int B,
 
 // ---------------------------------------------------------------- absorb
 
-// One workgroup per (head, 128-column quarter of the latent, group of BB
-// sequences; BB = 1, 2, 4 or 8, the smallest that holds the batch up to 8),
-// and workgroup (0, 0, 0) also writes the split plan table of a batch with
-// unequal tile counts.  The grid, 512 workgroups up to batch 8, is one round
-// of two workgroups per CU; the quarters of head h share its XCD (workgroup
-// i runs on XCD i mod 8 and HEADS is a multiple of 8), where they share its
-// query rows in L2.  Thread (dg, cc) sums rows 8*dg .. 8*dg+7 of W_UK[h] (eight
+// Batches of more than 8 (absorb_mfma_kernel below takes up to 8): one
+// workgroup per (head, 128-column quarter of the latent, group of BB = 8
+// sequences), and workgroup (0, 0, 0) also writes the split plan table of a
+// batch with unequal tile counts; the quarters of head h share its XCD
+// (workgroup i runs on XCD i mod 8 and HEADS is a multiple of 8), where they
+// share its query rows in L2.  Thread (dg, cc) sums rows 8*dg .. 8*dg+7 of W_UK[h] (eight
 // independent 8-byte loads in flight) for 8 latent columns; the 16 row groups
 // reduce through LDS.  W_UK[h] = kv_b rows h*256 .. h*256+127 lie in one
 // 128-row scale block.
@@ -260,6 +259,103 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
           *reinterpret_cast<const uint32_t *>(q + ((size_t)(b0 + bb) * HEADS + h) * (NOPE + ROPE) + NOPE + j);
       *reinterpret_cast<uint32_t *>(qbuf + qfrag_index(b0 + bb, h, LORA + j)) = v;
     }
+  }
+}
+
+// Batches of up to 8: the same product by 16x16x32 MFMAs.  Workgroup (h, q)
+// (4 waves) stages the quarter W_UK[h][:, 128q .. +127] (16 KB) and the
+// sequences' q_nope rows in LDS; wave w computes latent columns 32w .. +31 of
+// it: A = q_nope (sequences x d; fragment columns past B repeat real rows),
+// B = W_UK (d x latent column) by the 8-bit transpose read (lane L of a
+// 16-lane group receives column L of the eight rows its group addresses),
+// fp8 -> bf16 exactly; qt = gamma_kv * s_UK * sum, through LDS into 16-byte
+// stores of the fragment-ordered query.  Workgroup (0, 0) also writes the
+// split plan.
+constexpr int AB_WPITCH = 128 + 16;      // bytes per W_UK quarter row in LDS (fp8)
+constexpr int AB_NPITCH = NOPE * 2 + 16;  // bytes per q_nope row (bf16)
+constexpr int AB_OPITCH = 128 * 2 + 16;   // bytes per output row (bf16)
+
+__global__ __launch_bounds__(256) void absorb_mfma_kernel(const uint16_t *__restrict__ q,  // (B, H, 192)
+                                                          const uint8_t *__restrict__ wkvb,
+                                                          const float *__restrict__ skvb,
+                                                          const uint16_t *__restrict__ gamma, int B,
+                                                          uint16_t *__restrict__ qbuf,
+                                                          const int32_t *__restrict__ pos, int tmax, int units,
+                                                          int slots, int32_t *__restrict__ plan) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  __shared__ __align__(16) uint8_t wsm[NOPE * AB_WPITCH];
+  __shared__ __align__(16) uint8_t nsm[8 * AB_NPITCH];
+  __shared__ __align__(16) uint8_t osm[8 * AB_OPITCH];
+  const int h = blockIdx.x, quarter = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  if (h == 0 && quarter == 0) {
+    const int2 r = batch_tile_range(pos, tmax, B);
+    if (r.x != r.y) {
+      // the plan's scratch (2 B + 4 ints) is wsm, written below after the barrier
+      build_split_plan(pos, tmax, B, units, slots, plan, reinterpret_cast<int *>(wsm));
+      __syncthreads();
+    }
+  }
+  // W_UK quarter: 128 rows x 128 bytes, four 16-byte pieces per thread
+  // (non-temporal: read once); q_nope rows (rows past B re-read row B - 1)
+  const uint8_t *wq = wkvb + (size_t)h * (NOPE + VD) * LORA + quarter * 128;
+  u32x4 wv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = tid + 256 * i;
+    wv[i] = ldg16_nt(wq + (size_t)(p >> 3) * LORA + (p & 7) * 16);
+  }
+  u32x4 nv = {0, 0, 0, 0};
+  if (tid < 8 * 16) nv = ldg16(q + ((size_t)min(tid >> 4, B - 1) * HEADS + h) * (NOPE + ROPE) + (tid & 15) * 8);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = tid + 256 * i;
+    *reinterpret_cast<u32x4 *>(wsm + (p >> 3) * AB_WPITCH + (p & 7) * 16) = wv[i];
+  }
+  if (tid < 8 * 16) *reinterpret_cast<u32x4 *>(nsm + (tid >> 4) * AB_NPITCH + (tid & 15) * 16) = nv;
+  __syncthreads();
+
+  const int xrow = li % B;  // B <= 8
+  bf16x8 a[NOPE / 32];
+#pragma unroll
+  for (int ks = 0; ks < NOPE / 32; ++ks)
+    a[ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(nsm + xrow * AB_NPITCH + (32 * ks + 8 * lg) * 2));
+  const float sc = skvb[(size_t)(2 * h) * (LORA / 128) + quarter];
+#pragma unroll
+  for (int cbi = 0; cbi < 2; ++cbi) {
+    const int cb = 2 * wave + cbi;
+    f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < NOPE / 32; ++ks) {
+      const uint8_t *ap = wsm + (32 * ks + 8 * lg + (li >> 1)) * AB_WPITCH + 16 * cb + 8 * (li & 1);
+      const v2i w2 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i *)ap);
+      const bf16x2_t c0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w2.x, 1.f, false);
+      const bf16x2_t c1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w2.x, 1.f, true);
+      const bf16x2_t c2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w2.y, 1.f, false);
+      const bf16x2_t c3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w2.y, 1.f, true);
+      const bf16x8 bw = {c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
+      d4 = mfma16(a[ks], bw, d4);
+    }
+    // D: latent column 16 cb + li of the quarter, sequences 4 lg .. 4 lg + 3
+    const int c = 16 * cb + li;
+    const float g = bf2f(gamma[quarter * 128 + c]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (4 * lg + e < B) *reinterpret_cast<uint16_t *>(osm + (4 * lg + e) * AB_OPITCH + c * 2) = f2bf(d4[e] * sc * g);
+  }
+  __syncthreads();
+  if (tid < B * 16) {
+    const int m = tid >> 4, c8 = tid & 15;
+    *reinterpret_cast<u32x4 *>(qbuf + qfrag_index(m, h, quarter * 128 + c8 * 8)) =
+        *reinterpret_cast<const u32x4 *>(osm + m * AB_OPITCH + c8 * 16);
+  }
+  // rope half of the query: copied next to the absorbed latent query
+  if (quarter == 0 && tid < B * (ROPE / 2)) {
+    const int m = tid / (ROPE / 2), j = (tid % (ROPE / 2)) * 2;
+    const uint32_t v = *reinterpret_cast<const uint32_t *>(q + ((size_t)m * HEADS + h) * (NOPE + ROPE) + NOPE + j);
+    *reinterpret_cast<uint32_t *>(qbuf + qfrag_index(m, h, LORA + j)) = v;
   }
 }
 
@@ -1327,15 +1423,9 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   {
     const uint8_t *wkvb = reinterpret_cast<const uint8_t *>(a->w_kv_b);
     const uint16_t *gkv = reinterpret_cast<const uint16_t *>(a->gamma_kv);
-    if (B == 1)
-      absorb_kernel<1><<<dim3(HEADS, LORA / 128, 1), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions,
-                                                                       tmax, L.units, L.slots, plan);
-    else if (B == 2)
-      absorb_kernel<2><<<dim3(HEADS, LORA / 128, 1), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions,
-                                                                       tmax, L.units, L.slots, plan);
-    else if (B <= 4)
-      absorb_kernel<4><<<dim3(HEADS, LORA / 128, 1), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions,
-                                                                       tmax, L.units, L.slots, plan);
+    if (B <= 8)
+      absorb_mfma_kernel<<<dim3(HEADS, LORA / 128), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions, tmax,
+                                                            L.units, L.slots, plan);
     else
       absorb_kernel<8><<<dim3(HEADS, LORA / 128, (B + 7) / 8), 256, 0, st>>>(
           q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions, tmax, L.units, L.slots, plan);
