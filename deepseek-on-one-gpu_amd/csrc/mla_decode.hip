@@ -993,25 +993,32 @@ constexpr size_t ATTN_LDS = ATTN_LDS_BYTES;
 // ---------------------------------------------------------------- combine + W_UV
 
 AMLA_DEV float block_reduce(float v, float *red, bool is_max) {
+  // 512 threads (8 waves), in wave order
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   v = is_max ? wave_max(v) : wave_sum(v);
   __syncthreads();
   if (lane == 0) red[wave] = v;
   __syncthreads();
-  return is_max ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) : (red[0] + red[1]) + (red[2] + red[3]);
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < 8; ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+  return r;
 }
 
 // Exact online-softmax recomputation of one (split, head) in fp32, used only
 // for heads attn_kernel flagged (a sum of p = 2^(s - m_ref) at or above 2^64:
-// scores far above the split's reference max).  Thread tid owns latent columns 2*tid and 2*tid+1.
+// scores far above the split's reference max).  Thread tid < 256 owns latent
+// columns 2*tid and 2*tid+1 and one row of each 256-row block; the other
+// threads of the 512 take part in the reductions only.
 AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, const SeqSplits &sp, int split, float *qs,
                               float *ps, float *red, float &m_out, float &l_out, float &o0, float &o1) {
   const int tid = threadIdx.x;
+  const bool act = tid < 256;
   const int T = min(p.pos[b] + 1, p.tmax);
   const int t0 = split_tile(sp.ntiles, sp.count, split) * TT;
   const int t1 = min(split_tile(sp.ntiles, sp.count, split + 1) * TT, T);
   __syncthreads();
-  for (int c = tid; c < QKD; c += 256) qs[c] = bf2f(p.qbuf[qfrag_index(b, h, c)]);
+  for (int c = tid; c < QKD; c += 512) qs[c] = bf2f(p.qbuf[qfrag_index(b, h, c)]);
   __syncthreads();
   const uint16_t *cb = p.ckv + (size_t)b * p.ckv_bstride;
   const uint16_t *kb = p.kpe + (size_t)b * p.kpe_bstride;
@@ -1019,7 +1026,7 @@ AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, const SeqSplits
   for (int c0 = t0; c0 < t1; c0 += 256) {
     const int t = c0 + tid;
     float sv = -INFINITY, rt = 0.f;
-    if (t < t1) {
+    if (act && t < t1) {
       const uint16_t *row = cb + (size_t)t * LORA;
       float ss = 0.f, dl = 0.f;
       for (int c = 0; c < LORA; ++c) {
@@ -1042,18 +1049,20 @@ AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, const SeqSplits
     const float Mn = fmaxf(M, mc);
     const float f = (M == -INFINITY) ? 0.f : exp2f(M - Mn);
     const float pe = (sv == -INFINITY) ? 0.f : exp2f(sv - Mn);
-    ps[tid] = pe * rt;
+    if (act) ps[tid] = pe * rt;
     const float ls = block_reduce(pe, red, false);
     L = L * f + ls;
     a0 *= f;
     a1 *= f;
     M = Mn;
     const int n = min(256, t1 - c0);
-    for (int j = 0; j < n; ++j) {
-      const float w = ps[j];
-      const uint32_t pr = reinterpret_cast<const uint32_t *>(cb + (size_t)(c0 + j) * LORA)[tid];  // columns 2tid, 2tid+1
-      a0 += w * lo_bf(pr);
-      a1 += w * hi_bf(pr);
+    if (act) {
+      for (int j = 0; j < n; ++j) {
+        const float w = ps[j];
+        const uint32_t pr = reinterpret_cast<const uint32_t *>(cb + (size_t)(c0 + j) * LORA)[tid];  // columns 2tid, 2tid+1
+        a0 += w * lo_bf(pr);
+        a1 += w * hi_bf(pr);
+      }
     }
     __syncthreads();
   }
@@ -1063,65 +1072,75 @@ AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, const SeqSplits
   o1 = a1;
 }
 
-// Grid (H, ceil(B / 4)): workgroup (h, g) finishes sequences 4g .. 4g+3 of
-// head h, so W_UV[h] is read once per four sequences.
-//   wave w merges the splits of sequence 4g + w (lane: latent columns
-//     8l .. 8l+7, one 16-byte load per split), online max over the splits;
+// Grid (H, ceil(B / 4)), 512 threads: workgroup (h, g) finishes sequences
+// 4g .. 4g+3 of head h, so W_UV[h] is read once per four sequences.
+//   waves 2j and 2j+1 merge the splits of sequence 4g + j, the first half of
+//     the splits and the second (lane: latent columns 8l .. 8l+7, one 16-byte
+//     load per split, up to XB splits in flight): both take the max over all
+//     the splits, each sums its half with exp2(m_s - M), and the second hands
+//     its sums to the first through LDS (fixed order);
 //   a sequence with a flagged split is merged by the whole workgroup with
 //     exact recomputation of the flagged splits (rare);
 //   lat = O / l times kv_a_layernorm gamma and W_UV's block scale, as bf16;
 //   out[b][v] = W_UV[h][v] . lat[b] by 16x16x32 MFMAs: A = W_UV rows (fp8
 //     converted exactly), B = lat of the four sequences (columns 4.. zero);
-//     wave w produces rows v = 32w .. 32w+31.
-__global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const uint8_t *__restrict__ wkvb,
+//     wave w produces rows v = 16w .. 16w+15.
+__global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const uint8_t *__restrict__ wkvb,
                                                          const float *__restrict__ skvb,
                                                          const uint16_t *__restrict__ gamma, int B,
                                                          uint16_t *__restrict__ attn) {
-  constexpr int SQ = 4;     // sequences per workgroup
+  constexpr int SQ = 4;           // sequences per workgroup
+  constexpr int XB = 16;          // splits in flight per wave (a batch)
+  constexpr int WMAX = 128;       // weights per wave: half of at most 256 splits, a whole number of batches
   constexpr int LROW = LORA + 8;  // bf16 per lat row in LDS (16 B pad)
   const int h = blockIdx.x, b0 = blockIdx.y * SQ;
   const int nb = min(SQ, B - b0);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   __shared__ __align__(16) uint16_t latb[SQ][LROW];
-  __shared__ float wsp[SQ][256 + 16];
+  __shared__ float wsp[8][WMAX];
+  __shared__ float xacc[SQ][8][64];  // second half's sums, [column e][lane]
+  __shared__ float xl[SQ];
   __shared__ float qs[QKD];
   __shared__ float ps[256];
-  __shared__ float red[4];
+  __shared__ float red[8];
   __shared__ int s_flag[SQ];
   float bsc[4];  // W_UV block scales of the four 128-column blocks
 #pragma unroll
   for (int q = 0; q < 4; ++q) bsc[q] = skvb[(size_t)(2 * h + 1) * (LORA / 128) + q];
 
-  // W_UV rows of this wave (rows v = 32w .. 32w+31, 8 bytes per lane and K
+  // W_UV rows of this wave (rows v = 16w .. 16w+15, 8 bytes per lane and K
   // step) are loaded first: nothing they feed depends on the merge
   const int li = lane & 15, lg = lane >> 4;
-  const uint8_t *wr = wkvb + ((size_t)h * (NOPE + VD) + NOPE + 32 * wave + li) * LORA + 8 * lg;
-  u32x2 wa[2][LORA / 32];
+  const uint8_t *wr = wkvb + ((size_t)h * (NOPE + VD) + NOPE + 16 * wave + li) * LORA + 8 * lg;
+  u32x2 wa[LORA / 32];
   // non-temporal when this is the only workgroup reading these weight rows
   if (gridDim.y == 1) {
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt)
-#pragma unroll
-      for (int ks = 0; ks < LORA / 32; ++ks) wa[vt][ks] = ldg8_nt(wr + (size_t)vt * 16 * LORA + ks * 32);
+    for (int ks = 0; ks < LORA / 32; ++ks) wa[ks] = ldg8_nt(wr + ks * 32);
   } else {
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt)
-#pragma unroll
-      for (int ks = 0; ks < LORA / 32; ++ks) wa[vt][ks] = ldg8(wr + (size_t)vt * 16 * LORA + ks * 32);
+    for (int ks = 0; ks < LORA / 32; ++ks) wa[ks] = ldg8(wr + ks * 32);
   }
 
-  // ---- fast merge: wave w, sequence b0 + w.  The first 16 splits' partial
-  // rows are in flight while the max and the weights are formed.
-  if (wave < nb) {
-    const SeqSplits sp = seq_splits(ap, b0 + wave);
+  // ---- fast merge: wave w, sequence b0 + w / 2, half w % 2 of its splits.
+  // The first batch of partial rows is in flight while the max and the
+  // weights are formed.
+  const int sw = wave >> 1, hf = wave & 1;
+  bool flagged = false;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float L = 0.f;
+  if (sw < nb) {
+    const SeqSplits sp = seq_splits(ap, b0 + sw);
     const size_t base = (size_t)sp.first * HEADS + h;
     const u32x4 *po = reinterpret_cast<const u32x4 *>(ap.part_o + base * LORA) + lane;
     const size_t stride = (size_t)HEADS * LORA / 8;
     const int nsp = sp.count;
-    u32x4 v[16];
+    const int half = (nsp + 1) >> 1;
+    const int s0 = hf ? half : 0, s1 = hf ? nsp : half;  // this wave's splits [s0, s1)
+    u32x4 v[XB];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = po[(size_t)min(j, nsp - 1) * stride];
+    for (int j = 0; j < XB; ++j) v[j] = po[(size_t)min(s0 + j, nsp - 1) * stride];
     float mloc = -INFINITY;
     bool badl = false;
     for (int s = lane; s < nsp; s += 64) {
@@ -1129,66 +1148,76 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
       badl = badl || ap.part_ml[(base + (size_t)s * HEADS) * 2 + 1] < 0.f;
     }
     const float M = wave_max(mloc);
-    const bool flagged = __builtin_amdgcn_ballot_w64(badl) != 0;
-    if (lane == 0) s_flag[wave] = flagged;
+    flagged = __builtin_amdgcn_ballot_w64(badl) != 0;
+    if (lane == 0 && hf == 0) s_flag[sw] = flagged;
     if (!flagged) {
-      // weights, zero past the last split up to a multiple of 16
+      // weights of this half, zero past its last split up to a whole batch
       float lloc = 0.f;
-      const int nsp16 = (nsp + 15) & ~15;
-      for (int s = lane; s < nsp16; s += 64) {
+      const int nw = ((s1 - s0 + XB - 1) / XB) * XB;
+      for (int k = lane; k < nw; k += 64) {
         float w = 0.f;
-        if (s < nsp) {
-          const float ms = ap.part_ml[(base + (size_t)s * HEADS) * 2];
+        if (s0 + k < s1) {
+          const size_t row = base + (size_t)(s0 + k) * HEADS;
+          const float ms = ap.part_ml[row * 2];
           w = ms == -INFINITY ? 0.f : exp2f(ms - M);
-          lloc += w * ap.part_ml[(base + (size_t)s * HEADS) * 2 + 1];
+          lloc += w * ap.part_ml[row * 2 + 1];
         }
-        wsp[wave][s] = w;
+        wsp[wave][k] = w;
       }
-      const float L = wave_sum(lloc);
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int s = 0; s < nsp; s += 16) {
+      L = wave_sum(lloc);
+      for (int k = 0; k < s1 - s0; k += XB) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float w = wsp[wave][s + j];
+        for (int j = 0; j < XB; ++j) {
+          const float w = wsp[wave][k + j];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             acc[2 * e] += w * lo_bf(v[j][e]);
             acc[2 * e + 1] += w * hi_bf(v[j][e]);
           }
         }
-        if (s + 16 < nsp) {
+        if (k + XB < s1 - s0) {
 #pragma unroll
-          for (int j = 0; j < 16; ++j) v[j] = po[(size_t)min(s + 16 + j, nsp - 1) * stride];
+          for (int j = 0; j < XB; ++j) v[j] = po[(size_t)min(s0 + k + XB + j, nsp - 1) * stride];
         }
       }
-      const float inv = 1.f / L;
-      const float sc = bsc[(8 * lane) / 128];
-      const u32x4 gm = *reinterpret_cast<const u32x4 *>(gamma + 8 * lane);
-      u32x4 o;
+      if (hf == 1) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o[e] = pack_bf16(acc[2 * e] * inv * lo_bf(gm[e]) * sc, acc[2 * e + 1] * inv * hi_bf(gm[e]) * sc);
-      *reinterpret_cast<u32x4 *>(&latb[wave][8 * lane]) = o;
+        for (int e = 0; e < 8; ++e) xacc[sw][e][lane] = acc[e];
+        if (lane == 0) xl[sw] = L;
+      }
     }
-  } else if (wave < SQ && lane == 0) {
-    s_flag[wave] = 0;
+  } else if (hf == 0 && lane == 0) {
+    s_flag[sw] = 0;
+  }
+  __syncthreads();
+  if (sw < nb && hf == 0 && !flagged) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += xacc[sw][e][lane];
+    const float inv = 1.f / (L + xl[sw]);
+    const float sc = bsc[(8 * lane) / 128];
+    const u32x4 gm = *reinterpret_cast<const u32x4 *>(gamma + 8 * lane);
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = pack_bf16(acc[2 * e] * inv * lo_bf(gm[e]) * sc, acc[2 * e + 1] * inv * hi_bf(gm[e]) * sc);
+    *reinterpret_cast<u32x4 *>(&latb[sw][8 * lane]) = o;
   }
   __syncthreads();
 
   // ---- rare path: sequences with a flagged split, merged by the whole
-  // workgroup (thread tid: latent columns 2 tid, 2 tid + 1)
+  // workgroup (thread tid < 256: latent columns 2 tid, 2 tid + 1)
   for (int bb = 0; bb < nb; ++bb) {
     if (!s_flag[bb]) continue;
     const int b = b0 + bb;
     const SeqSplits sp = seq_splits(ap, b);
     const size_t base = (size_t)sp.first * HEADS + h;
-    float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
+    float M = -INFINITY, Ls = 0.f, a0 = 0.f, a1 = 0.f;
     for (int s = 0; s < sp.count; ++s) {
       const size_t row = base + (size_t)s * HEADS;
-      float m1 = ap.part_ml[row * 2], l1 = ap.part_ml[row * 2 + 1], o0, o1;
+      float m1 = ap.part_ml[row * 2], l1 = ap.part_ml[row * 2 + 1], o0 = 0.f, o1 = 0.f;
       if (l1 < 0.f) {
         recompute_split(ap, b, h, sp, s, qs, ps, red, m1, l1, o0, o1);
-      } else {
+      } else if (tid < 256) {
         const uint32_t v = reinterpret_cast<const uint32_t *>(ap.part_o + row * LORA)[tid];
         o0 = lo_bf(v);
         o1 = hi_bf(v);
@@ -1199,40 +1228,37 @@ __global__ __launch_bounds__(256) void combine_uv_kernel(AttnParams ap, const ui
       const float fn = exp2f(m1 - Mn);
       a0 = a0 * fo + o0 * fn;
       a1 = a1 * fo + o1 * fn;
-      L = L * fo + l1 * fn;
+      Ls = Ls * fo + l1 * fn;
       M = Mn;
     }
-    const float inv = 1.f / L;
-    const float sc = bsc[(2 * tid) / 128];
-    const uint32_t gm = reinterpret_cast<const uint32_t *>(gamma)[tid];
-    reinterpret_cast<uint32_t *>(&latb[bb][0])[tid] = pack_bf16(a0 * inv * lo_bf(gm) * sc, a1 * inv * hi_bf(gm) * sc);
+    if (tid < 256) {
+      const float inv = 1.f / Ls;
+      const float sc = bsc[(2 * tid) / 128];
+      const uint32_t gm = reinterpret_cast<const uint32_t *>(gamma)[tid];
+      reinterpret_cast<uint32_t *>(&latb[bb][0])[tid] = pack_bf16(a0 * inv * lo_bf(gm) * sc, a1 * inv * hi_bf(gm) * sc);
+    }
     __syncthreads();
   }
 
-  // ---- out = W_UV[h] . lat: wave w, rows 32w .. 32w+31 (two 16-row tiles), 16 K steps of 32
-  f32x4 c[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  // ---- out = W_UV[h] . lat: wave w, rows 16w .. 16w+15, 16 K steps of 32
+  f32x4 c = {0.f, 0.f, 0.f, 0.f};
   const bool bvalid = li < nb;
   const uint16_t *lr = &latb[bvalid ? li : 0][8 * lg];
 #pragma unroll
   for (int ks = 0; ks < LORA / 32; ++ks) {
     const u32x4 bl = bvalid ? *reinterpret_cast<const u32x4 *>(lr + ks * 32) : u32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt) {
-      typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-      const bf16x2_t c0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[vt][ks].x, 1.f, false);
-      const bf16x2_t c1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[vt][ks].x, 1.f, true);
-      const bf16x2_t c2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[vt][ks].y, 1.f, false);
-      const bf16x2_t c3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[vt][ks].y, 1.f, true);
-      const bf16x8 a = {c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
-      c[vt] = mfma16(a, as_bf16x8(bl), c[vt]);
-    }
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t c0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[ks].x, 1.f, false);
+    const bf16x2_t c1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[ks].x, 1.f, true);
+    const bf16x2_t c2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[ks].y, 1.f, false);
+    const bf16x2_t c3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[ks].y, 1.f, true);
+    const bf16x8 a = {c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
+    c = mfma16(a, as_bf16x8(bl), c);
   }
-  // C: lane holds sequence b0 + li, rows v = 16 vt + 4 lg .. +3 of the wave's 32
+  // C: lane holds sequence b0 + li, rows v = 16w + 4 lg .. +3
   if (bvalid) {
-    uint16_t *dst = attn + (size_t)(b0 + li) * HEADS * VD + h * VD + 32 * wave + 4 * lg;
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt)
-      *reinterpret_cast<u32x2 *>(dst + 16 * vt) = u32x2{pack_bf16(c[vt].x, c[vt].y), pack_bf16(c[vt].z, c[vt].w)};
+    uint16_t *dst = attn + (size_t)(b0 + li) * HEADS * VD + h * VD + 16 * wave + 4 * lg;
+    *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf16(c.x, c.y), pack_bf16(c.z, c.w)};
   }
 }
 
@@ -1453,7 +1479,7 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   // 6. merge splits, W_UV
   mark(ev, 5, st);
   uint16_t *attn = reinterpret_cast<uint16_t *>(a->attn_out ? a->attn_out : ws + L.attn);
-  combine_uv_kernel<<<dim3(HEADS, (B + 3) / 4), 256, 0, st>>>(ap, reinterpret_cast<const uint8_t *>(a->w_kv_b),
+  combine_uv_kernel<<<dim3(HEADS, (B + 3) / 4), 512, 0, st>>>(ap, reinterpret_cast<const uint8_t *>(a->w_kv_b),
                                                               a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv),
                                                               B, attn);
   if ((rc = check_launch("mla combine"))) return rc;
