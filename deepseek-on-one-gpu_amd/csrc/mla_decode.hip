@@ -165,132 +165,40 @@ AMLA_DEV void build_split_plan(const int32_t *__restrict__ pos, int tmax, int B,
 
 // ---------------------------------------------------------------- absorb
 
-// Batches of more than 8 (absorb_mfma_kernel below takes up to 8): one
-// workgroup per (head, 128-column quarter of the latent, group of BB = 8
-// sequences), and workgroup (0, 0, 0) also writes the split plan table of a
-// batch with unequal tile counts; the quarters of head h share its XCD
-// (workgroup i runs on XCD i mod 8 and HEADS is a multiple of 8), where they
-// share its query rows in L2.  Thread (dg, cc) sums rows 8*dg .. 8*dg+7 of W_UK[h] (eight
-// independent 8-byte loads in flight) for 8 latent columns; the 16 row groups
-// reduce through LDS.  W_UK[h] = kv_b rows h*256 .. h*256+127 lie in one
-// 128-row scale block.
-template <int BB>
-__global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict__ q,  // (B, H, 192)
-                                                     const uint8_t *__restrict__ wkvb,
-                                                     const float *__restrict__ skvb,
-                                                     const uint16_t *__restrict__ gamma,
-                                                     int B, uint16_t *__restrict__ qbuf,
-                                                     const int32_t *__restrict__ pos, int tmax, int units,
-                                                     int slots, int32_t *__restrict__ plan) {
-  __shared__ float qn[BB][NOPE];
-  __shared__ f32x4 red[16][BB][16][2];
-  static_assert(sizeof(red) >= (2 * 64 + 4) * sizeof(int), "the plan's scratch (batch <= 64) fits red");
-  if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {
-    // the first workgroup also writes the split plan (its scratch is red,
-    // rewritten below after the barrier)
-    const int2 r = batch_tile_range(pos, tmax, B);
-    if (r.x != r.y) {
-      build_split_plan(pos, tmax, B, units, slots, plan, reinterpret_cast<int *>(&red[0][0][0][0]));
-      __syncthreads();
-    }
-  }
-  const int h = blockIdx.x, quarter = blockIdx.y;
-  const int b0 = blockIdx.z * BB;
-  const int nb = min(BB, B - b0);
-  const int tid = threadIdx.x;
-  const int cc = tid & 15, dg = tid >> 4;
-  const int c0 = quarter * 128 + cc * 8;  // this thread's 8 latent columns
-  const uint8_t *wp = wkvb + ((size_t)h * (NOPE + VD) + dg * 8) * LORA + c0;
-  u32x2 raw[8];
-  // non-temporal when this is the only workgroup reading these weight rows
-  if (gridDim.z == 1) {
-#pragma unroll
-    for (int d = 0; d < 8; ++d) raw[d] = ldg8_nt(wp + (size_t)d * LORA);
-  } else {
-#pragma unroll
-    for (int d = 0; d < 8; ++d) raw[d] = ldg8(wp + (size_t)d * LORA);
-  }
-  for (int e = tid; e < BB * NOPE; e += 256) {
-    const int bb = e / NOPE, d = e % NOPE;
-    qn[bb][d] = bb < nb ? bf2f(q[((size_t)(b0 + bb) * HEADS + h) * (NOPE + ROPE) + d]) : 0.f;
-  }
-  __syncthreads();
-  f32x4 acc[BB][2];
-#pragma unroll
-  for (int bb = 0; bb < BB; ++bb) acc[bb][0] = acc[bb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int d = 0; d < 8; ++d) {
-    const f32x2 w01 = fp8x2_to_f32<false>(raw[d].x), w23 = fp8x2_to_f32<true>(raw[d].x);
-    const f32x2 w45 = fp8x2_to_f32<false>(raw[d].y), w67 = fp8x2_to_f32<true>(raw[d].y);
-    const f32x4 wa = {w01.x, w01.y, w23.x, w23.y}, wb = {w45.x, w45.y, w67.x, w67.y};
-#pragma unroll
-    for (int bb = 0; bb < BB; ++bb) {
-      const float qv = qn[bb][dg * 8 + d];
-      acc[bb][0] += qv * wa;
-      acc[bb][1] += qv * wb;
-    }
-  }
-#pragma unroll
-  for (int bb = 0; bb < BB; ++bb) {
-    red[dg][bb][cc][0] = acc[bb][0];
-    red[dg][bb][cc][1] = acc[bb][1];
-  }
-  __syncthreads();
-  // one thread per (sequence, column group, half): sum the 16 row groups in order
-  {
-    const int bb = tid >> 5, c16 = (tid >> 1) & 15, half = tid & 1;
-    if (bb < nb) {
-      f32x4 v = red[0][bb][c16][half];
-#pragma unroll
-      for (int g = 1; g < 16; ++g) v += red[g][bb][c16][half];
-      const int c = quarter * 128 + c16 * 8 + half * 4;
-      const float sc = skvb[(size_t)(2 * h) * (LORA / 128) + quarter];
-      const u32x2 gm = *reinterpret_cast<const u32x2 *>(gamma + c);
-      u32x2 o = {pack_bf16(v.x * sc * lo_bf(gm.x), v.y * sc * hi_bf(gm.x)),
-                 pack_bf16(v.z * sc * lo_bf(gm.y), v.w * sc * hi_bf(gm.y))};
-      *reinterpret_cast<u32x2 *>(qbuf + qfrag_index(b0 + bb, h, c)) = o;  // 4 columns in one 8-column group
-    }
-  }
-  // rope half of the query: copied next to the absorbed latent query
-  if (quarter == 0) {
-    for (int e = tid; e < nb * (ROPE / 2); e += 256) {
-      const int bb = e / (ROPE / 2), j = (e % (ROPE / 2)) * 2;
-      const uint32_t v =
-          *reinterpret_cast<const uint32_t *>(q + ((size_t)(b0 + bb) * HEADS + h) * (NOPE + ROPE) + NOPE + j);
-      *reinterpret_cast<uint32_t *>(qbuf + qfrag_index(b0 + bb, h, LORA + j)) = v;
-    }
-  }
-}
-
-// Batches of up to 8: the same product by 16x16x32 MFMAs.  Workgroup (h, q)
-// (4 waves) stages the quarter W_UK[h][:, 128q .. +127] (16 KB) and the
-// sequences' q_nope rows in LDS; wave w computes latent columns 32w .. +31 of
-// it: A = q_nope (sequences x d; fragment columns past B repeat real rows),
-// B = W_UK (d x latent column) by the 8-bit transpose read (lane L of a
-// 16-lane group receives column L of the eight rows its group addresses),
-// fp8 -> bf16 exactly; qt = gamma_kv * s_UK * sum, through LDS into 16-byte
-// stores of the fragment-ordered query.  Workgroup (0, 0) also writes the
-// split plan.
-constexpr int AB_WPITCH = 128 + 16;      // bytes per W_UK quarter row in LDS (fp8)
+// One workgroup (4 waves) per (head h, 128-column quarter q of the latent,
+// group of 16 sequences): it stages the quarter W_UK[h][:, 128q .. +127]
+// (16 KB, W_UK[h] = kv_b rows h*256 .. h*256+127, one 128-row scale block)
+// and the group's q_nope rows in LDS; wave w computes latent columns
+// 32w .. +31 of it by 16x16x32 MFMAs: A = q_nope (sequences x d; rows past
+// the batch repeat real rows and are not stored), B = W_UK (d x latent
+// column) by the 8-bit transpose read (lane L of a 16-lane group receives
+// column L of the eight rows its group addresses), fp8 -> bf16 exactly;
+// qt = gamma_kv * s_UK * sum, through LDS into 16-byte stores of the
+// fragment-ordered query.  Workgroup (0, 0, 0) also writes the split plan
+// table of a batch with unequal tile counts.
+constexpr int AB_SEQ = 16;                // sequences per workgroup (the MFMA's 16 rows)
+constexpr int AB_WPITCH = 128 + 16;       // bytes per W_UK quarter row in LDS (fp8)
 constexpr int AB_NPITCH = NOPE * 2 + 16;  // bytes per q_nope row (bf16)
 constexpr int AB_OPITCH = 128 * 2 + 16;   // bytes per output row (bf16)
 
-__global__ __launch_bounds__(256) void absorb_mfma_kernel(const uint16_t *__restrict__ q,  // (B, H, 192)
-                                                          const uint8_t *__restrict__ wkvb,
-                                                          const float *__restrict__ skvb,
-                                                          const uint16_t *__restrict__ gamma, int B,
-                                                          uint16_t *__restrict__ qbuf,
-                                                          const int32_t *__restrict__ pos, int tmax, int units,
-                                                          int slots, int32_t *__restrict__ plan) {
+__global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict__ q,  // (B, H, 192)
+                                                     const uint8_t *__restrict__ wkvb,
+                                                     const float *__restrict__ skvb,
+                                                     const uint16_t *__restrict__ gamma, int B,
+                                                     uint16_t *__restrict__ qbuf,
+                                                     const int32_t *__restrict__ pos, int tmax, int units,
+                                                     int slots, int32_t *__restrict__ plan) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   typedef int v2i __attribute__((ext_vector_type(2)));
   __shared__ __align__(16) uint8_t wsm[NOPE * AB_WPITCH];
-  __shared__ __align__(16) uint8_t nsm[8 * AB_NPITCH];
-  __shared__ __align__(16) uint8_t osm[8 * AB_OPITCH];
-  const int h = blockIdx.x, quarter = blockIdx.y;
+  __shared__ __align__(16) uint8_t nsm[AB_SEQ * AB_NPITCH];
+  __shared__ __align__(16) uint8_t osm[AB_SEQ * AB_OPITCH];
+  static_assert(sizeof(wsm) >= (2 * 64 + 8) * sizeof(int), "the plan's scratch (batch <= 64) fits wsm");
+  const int h = blockIdx.x, quarter = blockIdx.y, b0 = blockIdx.z * AB_SEQ;
+  const int nb = min(AB_SEQ, B - b0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  if (h == 0 && quarter == 0) {
+  if (h == 0 && quarter == 0 && blockIdx.z == 0) {
     const int2 r = batch_tile_range(pos, tmax, B);
     if (r.x != r.y) {
       // the plan's scratch (2 B + 4 ints) is wsm, written below after the barrier
@@ -299,29 +207,37 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const uint16_t *__rest
     }
   }
   // W_UK quarter: 128 rows x 128 bytes, four 16-byte pieces per thread
-  // (non-temporal: read once); q_nope rows (rows past B re-read row B - 1)
+  // (non-temporal when this is the only group of sequences reading it);
+  // q_nope rows, one 16-byte piece per thread (rows past the batch re-read
+  // its last row)
   const uint8_t *wq = wkvb + (size_t)h * (NOPE + VD) * LORA + quarter * 128;
   u32x4 wv[4];
+  if (gridDim.z == 1) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int p = tid + 256 * i;
-    wv[i] = ldg16_nt(wq + (size_t)(p >> 3) * LORA + (p & 7) * 16);
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + 256 * i;
+      wv[i] = ldg16_nt(wq + (size_t)(p >> 3) * LORA + (p & 7) * 16);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + 256 * i;
+      wv[i] = ldg16(wq + (size_t)(p >> 3) * LORA + (p & 7) * 16);
+    }
   }
-  u32x4 nv = {0, 0, 0, 0};
-  if (tid < 8 * 16) nv = ldg16(q + ((size_t)min(tid >> 4, B - 1) * HEADS + h) * (NOPE + ROPE) + (tid & 15) * 8);
+  const u32x4 nv = ldg16(q + ((size_t)(b0 + min(tid >> 4, nb - 1)) * HEADS + h) * (NOPE + ROPE) + (tid & 15) * 8);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int p = tid + 256 * i;
     *reinterpret_cast<u32x4 *>(wsm + (p >> 3) * AB_WPITCH + (p & 7) * 16) = wv[i];
   }
-  if (tid < 8 * 16) *reinterpret_cast<u32x4 *>(nsm + (tid >> 4) * AB_NPITCH + (tid & 15) * 16) = nv;
+  *reinterpret_cast<u32x4 *>(nsm + (tid >> 4) * AB_NPITCH + (tid & 15) * 16) = nv;
   __syncthreads();
 
-  const int xrow = li % B;  // B <= 8
   bf16x8 a[NOPE / 32];
 #pragma unroll
   for (int ks = 0; ks < NOPE / 32; ++ks)
-    a[ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(nsm + xrow * AB_NPITCH + (32 * ks + 8 * lg) * 2));
+    a[ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(nsm + li * AB_NPITCH + (32 * ks + 8 * lg) * 2));
   const float sc = skvb[(size_t)(2 * h) * (LORA / 128) + quarter];
 #pragma unroll
   for (int cbi = 0; cbi < 2; ++cbi) {
@@ -338,24 +254,28 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const uint16_t *__rest
       const bf16x8 bw = {c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
       d4 = mfma16(a[ks], bw, d4);
     }
-    // D: latent column 16 cb + li of the quarter, sequences 4 lg .. 4 lg + 3
+    // D: latent column 16 cb + li of the quarter, sequences b0 + 4 lg .. +3
     const int c = 16 * cb + li;
     const float g = bf2f(gamma[quarter * 128 + c]);
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      if (4 * lg + e < B) *reinterpret_cast<uint16_t *>(osm + (4 * lg + e) * AB_OPITCH + c * 2) = f2bf(d4[e] * sc * g);
+      *reinterpret_cast<uint16_t *>(osm + (4 * lg + e) * AB_OPITCH + c * 2) = f2bf(d4[e] * sc * g);
   }
   __syncthreads();
-  if (tid < B * 16) {
+  {
     const int m = tid >> 4, c8 = tid & 15;
-    *reinterpret_cast<u32x4 *>(qbuf + qfrag_index(m, h, quarter * 128 + c8 * 8)) =
-        *reinterpret_cast<const u32x4 *>(osm + m * AB_OPITCH + c8 * 16);
+    if (m < nb)
+      *reinterpret_cast<u32x4 *>(qbuf + qfrag_index(b0 + m, h, quarter * 128 + c8 * 8)) =
+          *reinterpret_cast<const u32x4 *>(osm + m * AB_OPITCH + c8 * 16);
   }
   // rope half of the query: copied next to the absorbed latent query
-  if (quarter == 0 && tid < B * (ROPE / 2)) {
-    const int m = tid / (ROPE / 2), j = (tid % (ROPE / 2)) * 2;
-    const uint32_t v = *reinterpret_cast<const uint32_t *>(q + ((size_t)m * HEADS + h) * (NOPE + ROPE) + NOPE + j);
-    *reinterpret_cast<uint32_t *>(qbuf + qfrag_index(m, h, LORA + j)) = v;
+  if (quarter == 0) {
+    for (int e = tid; e < nb * (ROPE / 2); e += 256) {
+      const int m = e / (ROPE / 2), j = (e % (ROPE / 2)) * 2;
+      const uint32_t v =
+          *reinterpret_cast<const uint32_t *>(q + ((size_t)(b0 + m) * HEADS + h) * (NOPE + ROPE) + NOPE + j);
+      *reinterpret_cast<uint32_t *>(qbuf + qfrag_index(b0 + m, h, LORA + j)) = v;
+    }
   }
 }
 
@@ -1072,35 +992,38 @@ AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, const SeqSplits
   o1 = a1;
 }
 
-// Grid (H, ceil(B / 4)), 512 threads: workgroup (h, g) finishes sequences
-// 4g .. 4g+3 of head h, so W_UV[h] is read once per four sequences.
-//   waves 2j and 2j+1 merge the splits of sequence 4g + j, the first half of
-//     the splits and the second (lane: latent columns 8l .. 8l+7, one 16-byte
-//     load per split, up to XB splits in flight): both take the max over all
-//     the splits, each sums its half with exp2(m_s - M), and the second hands
-//     its sums to the first through LDS (fixed order);
+// Grid (H, ceil(B / SQ)), 512 threads: workgroup (h, g) finishes sequences
+// SQ g .. SQ g + SQ - 1 of head h, so W_UV[h] is read once per SQ sequences
+// (SQ = 4 up to batch 8, else 16: the MFMA's 16 columns).
+//   merge units (sequence, part of its splits), WPS parts per sequence (2 up
+//     to batch 8, else 1), go to the 8 waves in turn (lane: latent columns
+//     8l .. 8l+7, one 16-byte load per split, up to XB splits in flight);
+//     every part takes the max over all the sequence's splits and sums its
+//     own with exp2(m_s - M); the parts' sums meet in LDS in part order;
 //   a sequence with a flagged split is merged by the whole workgroup with
 //     exact recomputation of the flagged splits (rare);
 //   lat = O / l times kv_a_layernorm gamma and W_UV's block scale, as bf16;
 //   out[b][v] = W_UV[h][v] . lat[b] by 16x16x32 MFMAs: A = W_UV rows (fp8
-//     converted exactly), B = lat of the four sequences (columns 4.. zero);
-//     wave w produces rows v = 16w .. 16w+15.
+//     converted exactly), B = lat of the SQ sequences (columns past them
+//     zero); wave w produces rows v = 16w .. 16w+15.
+template <int SQ, int WPS>
 __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const uint8_t *__restrict__ wkvb,
                                                          const float *__restrict__ skvb,
                                                          const uint16_t *__restrict__ gamma, int B,
                                                          uint16_t *__restrict__ attn) {
-  constexpr int SQ = 4;           // sequences per workgroup
+  constexpr int NU = SQ * WPS;    // merge units
   constexpr int XB = 16;          // splits in flight per wave (a batch)
-  constexpr int WMAX = 128;       // weights per wave: half of at most 256 splits, a whole number of batches
+  constexpr int WMAX = 256;       // weights per unit: at most 256 splits, a whole number of batches
   constexpr int LROW = LORA + 8;  // bf16 per lat row in LDS (16 B pad)
+  static_assert(SQ <= 16 && NU <= 16, "one MFMA column per sequence; at most two units per wave");
   const int h = blockIdx.x, b0 = blockIdx.y * SQ;
   const int nb = min(SQ, B - b0);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   __shared__ __align__(16) uint16_t latb[SQ][LROW];
   __shared__ float wsp[8][WMAX];
-  __shared__ float xacc[SQ][8][64];  // second half's sums, [column e][lane]
-  __shared__ float xl[SQ];
+  __shared__ float xacc[NU][8][64];  // each unit's sums, [column e][lane]
+  __shared__ float xl[NU];
   __shared__ float qs[QKD];
   __shared__ float ps[256];
   __shared__ float red[8];
@@ -1123,21 +1046,22 @@ __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const ui
     for (int ks = 0; ks < LORA / 32; ++ks) wa[ks] = ldg8(wr + ks * 32);
   }
 
-  // ---- fast merge: wave w, sequence b0 + w / 2, half w % 2 of its splits.
-  // The first batch of partial rows is in flight while the max and the
+  // ---- fast merge: unit u = (sequence b0 + u / WPS, part u % WPS).  A
+  // unit's first batch of partial rows is in flight while the max and the
   // weights are formed.
-  const int sw = wave >> 1, hf = wave & 1;
-  bool flagged = false;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float L = 0.f;
-  if (sw < nb) {
-    const SeqSplits sp = seq_splits(ap, b0 + sw);
+  for (int u = wave; u < NU; u += 8) {
+    const int su = u / WPS, pu = u % WPS;
+    if (su >= nb) {
+      if (pu == 0 && lane == 0) s_flag[su] = 0;
+      continue;
+    }
+    const SeqSplits sp = seq_splits(ap, b0 + su);
     const size_t base = (size_t)sp.first * HEADS + h;
     const u32x4 *po = reinterpret_cast<const u32x4 *>(ap.part_o + base * LORA) + lane;
     const size_t stride = (size_t)HEADS * LORA / 8;
     const int nsp = sp.count;
-    const int half = (nsp + 1) >> 1;
-    const int s0 = hf ? half : 0, s1 = hf ? nsp : half;  // this wave's splits [s0, s1)
+    const int chunk = (nsp + WPS - 1) / WPS;
+    const int s0 = min(pu * chunk, nsp), s1 = min(s0 + chunk, nsp);  // this unit's splits [s0, s1)
     u32x4 v[XB];
 #pragma unroll
     for (int j = 0; j < XB; ++j) v[j] = po[(size_t)min(s0 + j, nsp - 1) * stride];
@@ -1148,59 +1072,64 @@ __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const ui
       badl = badl || ap.part_ml[(base + (size_t)s * HEADS) * 2 + 1] < 0.f;
     }
     const float M = wave_max(mloc);
-    flagged = __builtin_amdgcn_ballot_w64(badl) != 0;
-    if (lane == 0 && hf == 0) s_flag[sw] = flagged;
-    if (!flagged) {
-      // weights of this half, zero past its last split up to a whole batch
-      float lloc = 0.f;
-      const int nw = ((s1 - s0 + XB - 1) / XB) * XB;
-      for (int k = lane; k < nw; k += 64) {
-        float w = 0.f;
-        if (s0 + k < s1) {
-          const size_t row = base + (size_t)(s0 + k) * HEADS;
-          const float ms = ap.part_ml[row * 2];
-          w = ms == -INFINITY ? 0.f : exp2f(ms - M);
-          lloc += w * ap.part_ml[row * 2 + 1];
-        }
-        wsp[wave][k] = w;
+    const bool flagged = __builtin_amdgcn_ballot_w64(badl) != 0;
+    if (pu == 0 && lane == 0) s_flag[su] = flagged;
+    if (flagged) continue;
+    // weights of this unit, zero past its last split up to a whole batch
+    float lloc = 0.f;
+    const int nw = ((s1 - s0 + XB - 1) / XB) * XB;
+    for (int k = lane; k < nw; k += 64) {
+      float w = 0.f;
+      if (s0 + k < s1) {
+        const size_t row = base + (size_t)(s0 + k) * HEADS;
+        const float ms = ap.part_ml[row * 2];
+        w = ms == -INFINITY ? 0.f : exp2f(ms - M);
+        lloc += w * ap.part_ml[row * 2 + 1];
       }
-      L = wave_sum(lloc);
-      for (int k = 0; k < s1 - s0; k += XB) {
+      wsp[wave][k] = w;
+    }
+    const float L = wave_sum(lloc);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < s1 - s0; k += XB) {
 #pragma unroll
-        for (int j = 0; j < XB; ++j) {
-          const float w = wsp[wave][k + j];
+      for (int j = 0; j < XB; ++j) {
+        const float w = wsp[wave][k + j];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            acc[2 * e] += w * lo_bf(v[j][e]);
-            acc[2 * e + 1] += w * hi_bf(v[j][e]);
-          }
-        }
-        if (k + XB < s1 - s0) {
-#pragma unroll
-          for (int j = 0; j < XB; ++j) v[j] = po[(size_t)min(s0 + k + XB + j, nsp - 1) * stride];
+        for (int e = 0; e < 4; ++e) {
+          acc[2 * e] += w * lo_bf(v[j][e]);
+          acc[2 * e + 1] += w * hi_bf(v[j][e]);
         }
       }
-      if (hf == 1) {
+      if (k + XB < s1 - s0) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xacc[sw][e][lane] = acc[e];
-        if (lane == 0) xl[sw] = L;
+        for (int j = 0; j < XB; ++j) v[j] = po[(size_t)min(s0 + k + XB + j, nsp - 1) * stride];
       }
     }
-  } else if (hf == 0 && lane == 0) {
-    s_flag[sw] = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xacc[u][e][lane] = acc[e];
+    if (lane == 0) xl[u] = L;
   }
   __syncthreads();
-  if (sw < nb && hf == 0 && !flagged) {
+  for (int sq = wave; sq < nb; sq += 8) {
+    if (s_flag[sq]) continue;
+    float acc[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += xacc[sw][e][lane];
-    const float inv = 1.f / (L + xl[sw]);
+    for (int e = 0; e < 8; ++e) acc[e] = xacc[sq * WPS][e][lane];
+    float L = xl[sq * WPS];
+#pragma unroll
+    for (int pu = 1; pu < WPS; ++pu) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += xacc[sq * WPS + pu][e][lane];
+      L += xl[sq * WPS + pu];
+    }
+    const float inv = 1.f / L;
     const float sc = bsc[(8 * lane) / 128];
     const u32x4 gm = *reinterpret_cast<const u32x4 *>(gamma + 8 * lane);
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       o[e] = pack_bf16(acc[2 * e] * inv * lo_bf(gm[e]) * sc, acc[2 * e + 1] * inv * hi_bf(gm[e]) * sc);
-    *reinterpret_cast<u32x4 *>(&latb[sw][8 * lane]) = o;
+    *reinterpret_cast<u32x4 *>(&latb[sq][8 * lane]) = o;
   }
   __syncthreads();
 
@@ -1446,16 +1375,9 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   mark(ev, 3, st);
   int32_t *plan = reinterpret_cast<int32_t *>(ws + L.plan);
   const int tmax = mla_context_bound(*a);
-  {
-    const uint8_t *wkvb = reinterpret_cast<const uint8_t *>(a->w_kv_b);
-    const uint16_t *gkv = reinterpret_cast<const uint16_t *>(a->gamma_kv);
-    if (B <= 8)
-      absorb_mfma_kernel<<<dim3(HEADS, LORA / 128), 256, 0, st>>>(q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions, tmax,
-                                                            L.units, L.slots, plan);
-    else
-      absorb_kernel<8><<<dim3(HEADS, LORA / 128, (B + 7) / 8), 256, 0, st>>>(
-          q, wkvb, a->s_kv_b, gkv, B, qbuf, a->positions, tmax, L.units, L.slots, plan);
-  }
+  absorb_kernel<<<dim3(HEADS, LORA / 128, (B + AB_SEQ - 1) / AB_SEQ), 256, 0, st>>>(
+      q, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv), B,
+      qbuf, a->positions, tmax, L.units, L.slots, plan);
   if ((rc = check_launch("mla absorb"))) return rc;
 
   // 5. attention over the latent cache, split over context
@@ -1479,9 +1401,14 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   // 6. merge splits, W_UV
   mark(ev, 5, st);
   uint16_t *attn = reinterpret_cast<uint16_t *>(a->attn_out ? a->attn_out : ws + L.attn);
-  combine_uv_kernel<<<dim3(HEADS, (B + 3) / 4), 512, 0, st>>>(ap, reinterpret_cast<const uint8_t *>(a->w_kv_b),
-                                                              a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv),
-                                                              B, attn);
+  if (B <= 8)
+    combine_uv_kernel<4, 2><<<dim3(HEADS, (B + 3) / 4), 512, 0, st>>>(
+        ap, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv), B,
+        attn);
+  else
+    combine_uv_kernel<16, 1><<<dim3(HEADS, (B + 15) / 16), 512, 0, st>>>(
+        ap, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv), B,
+        attn);
   if ((rc = check_launch("mla combine"))) return rc;
 
   // 7. o_proj (+ residual in layer mode)
