@@ -474,10 +474,14 @@ AMLA_DEV float max_lane_groups(float v) {
 }
 
 
-// Grid: one workgroup per split slot (seq_splits), 256 threads, one
-// workgroup per CU (~150 KB of LDS).
-// Scores: wave w owns heads 32w .. 32w+31; values: wave w owns latent columns
-// 128w .. 128w+127 of every head.  Per tile of 32 cache rows:
+// Grid: one workgroup per split slot (seq_splits) and group of HG = 64 NTW
+// heads (NTW = 2: all 128 heads, grid (slots); NTW = 1: two head groups, grid
+// (slots, 2), for launches with few slots, where the query load and the
+// partial O store of a workgroup, both in proportion to its heads, dominate);
+// 256 threads, one workgroup per CU (~150 KB of LDS).
+// Scores: wave w owns heads 16 NTW w .. of the group; values: wave w owns
+// latent columns 128w .. 128w+127 of every head of the group.  Per tile of 32
+// cache rows:
 //   each wave computes r_t of its 8 copied rows and rotates their rope keys,
 //     one tile ahead of use;
 //   S^T (t x head) = K_tile (32 x 576) . Q^T with the tile rows as the MFMA M
@@ -489,11 +493,11 @@ AMLA_DEV float max_lane_groups(float v) {
 //     whose sum of p reaches 2^64 (a later score far above m_ref) is flagged
 //     instead and recomputed exactly by the combine;
 //   P^T (p * r_t as bf16) of the wave's heads goes to LDS;
-//   O^T (128 latent x 128 heads, fp32) += C^T (128 x t) . P^T (t x 128), C^T
+//   O^T (128 latent x HG heads, fp32) += C^T (128 x t) . P^T (t x HG), C^T
 //     by transpose reads of the wave's 128 columns of the raw tile: first the
-//     wave's own 32 heads (P from registers), then, after a barrier, the other
-//     waves' 96 heads from LDS.
-// Registers: O^T takes 256 accumulators, the query fragments 144; the loop
+//     wave's own heads (P from registers), then, after a barrier, the other
+//     waves' heads from LDS.
+// Registers (NTW = 2): O^T takes 256 accumulators, the query fragments 144; the loop
 // must not spill (a scratch reload would wait for every copy in flight),
 // which is why the copies use scalar bases and there is no rescaling path.
 //
@@ -504,7 +508,13 @@ AMLA_DEV float max_lane_groups(float v) {
 // scheduled before it.  Counting only this code's own reads is safe: LDS
 // operations complete in order, so any other LDS operation issued in between
 // only makes a wait stricter; nothing in the loop uses scalar memory loads.
+template <int NTW>
 __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
+  static_assert(NTW == 1 || NTW == 2, "16 or 32 heads per wave");
+  constexpr int HPW = 16 * NTW;  // heads per wave (scores)
+  constexpr int HG = 4 * HPW;    // heads of the workgroup
+  constexpr int NH = HG / 16;    // 16-head blocks of the workgroup (PV)
+  constexpr int NO = NH - NTW;   // blocks of the other waves
   const int slot = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -530,24 +540,30 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   const int tb = split_tile(nb, ns, split);
   const int te = split_tile(nb, ns, split + 1);
   extern __shared__ __align__(16) uint8_t smem[];
-  const int head0 = wave * 32;
+  const int hl0 = wave * HPW;                     // the wave's first head in the group
+  const int head0 = blockIdx.y * HG + hl0;
   const uint32_t lane16 = static_cast<uint32_t>(lane) * 16u;  // the copies' lane offset inside the context
 
   // query fragments (B operand: head = column l%16, K = 8*lg .. of each 32-wide step)
-  bf16x8 qf[2][QKD / 32];
+  bf16x8 qf[NTW][QKD / 32];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NTW; ++nt) {
     const uint16_t *qr = p.qbuf + qfrag_index(b, head0 + nt * 16, 0) + lane * 8;
 #pragma unroll
     for (int ks = 0; ks < QKD / 32; ++ks) qf[nt][ks] = as_bf16x8(ldg16(qr + ks * 512));
   }
 
-  f32x4 o[8][8];  // O^T: latent 128*wave + 16*mt + .., heads 16*nt + ..
+  f32x4 o[8][NH];  // O^T: latent 128*wave + 16*mt + .., head block (NTW*wave + j) % NH of the group
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) o[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_ref[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    for (int nt = 0; nt < NH; ++nt) o[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_ref[NTW], l_run[NTW];
+#pragma unroll
+  for (int nt = 0; nt < NTW; ++nt) {
+    m_ref[nt] = -INFINITY;
+    l_run[nt] = 0.f;
+  }
 
   if (tb < te) {
     dma_tile(p, b, tb, T, smem, smem, wave, lane);
@@ -596,7 +612,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
 #define AMLA_RDA(dst, S, MT) \
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(kaddr), "i"(((MT) * 16 * KROW + (S) * 32) * 2))
 #define AMLA_RD(dst, addr, off) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(off))
-      f32x4 sc[2][2];
+      f32x4 sc[2][NTW];
       // r_t of the lane's C-layout rows 4*lg + r (mt 0) and 16 + 4*lg + r (mt 1)
       // (read at iteration 12, needed from step 16 on)
       f32x4 rc[2];
@@ -635,13 +651,16 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
 #pragma unroll
           for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) sc[mt][nt] *= rc[mt];
-          asm volatile("s_nop 4" : "+v"(sc[0][0]), "+v"(sc[0][1]), "+v"(sc[1][0]), "+v"(sc[1][1])::"memory");
+            for (int nt = 0; nt < NTW; ++nt) sc[mt][nt] *= rc[mt];
+          if constexpr (NTW == 2)
+            asm volatile("s_nop 4" : "+v"(sc[0][0]), "+v"(sc[0][1]), "+v"(sc[1][0]), "+v"(sc[1][1])::"memory");
+          else
+            asm volatile("s_nop 4" : "+v"(sc[0][0]), "+v"(sc[1][0])::"memory");
         }
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
+          for (int nt = 0; nt < NTW; ++nt) {
             if (ks == 0)
               asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=v"(sc[mt][nt]) : "v"(ab[c][mt]), "v"(qf[nt][ks]));
             else
@@ -722,7 +741,10 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
         if (ks < TILE_DMA) dma_piece(p, b, min(tile + 2, te - 1), tile + 2, T, smem, nst, wave, lane, lane16, ks);
       }
       // the softmax reads sc: MFMA write -> VALU read wait states
-      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sc[0][0]), "+v"(sc[0][1]), "+v"(sc[1][0]), "+v"(sc[1][1])::"memory");
+      if constexpr (NTW == 2)
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sc[0][0]), "+v"(sc[0][1]), "+v"(sc[1][0]), "+v"(sc[1][1])::"memory");
+      else
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sc[0][0]), "+v"(sc[1][0])::"memory");
 #undef AMLA_RD
 #undef AMLA_RDA
       __builtin_amdgcn_sched_barrier(0);
@@ -734,9 +756,9 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       // context exist only in the last tile of a sequence)
       const int tbase = tile * TT;
       const bool partial = tbase + TT > T;
-      u32x4 pk[2];
+      u32x4 pk[NTW];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
+      for (int nt = 0; nt < NTW; ++nt) {
         float sv[8];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
@@ -771,9 +793,9 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       // exactly this lane's eight scores, and the k order of the transpose
       // reads below (so pk[nt] is also this wave's own B fragment)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int nt = 0; nt < NTW; ++nt)
         asm volatile("ds_write_b128 %0, %1" ::"v"(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-                         (__attribute__((address_space(3))) uint8_t *)(smem + P_OFF + (head0 + nt * 16 + li) * PROW +
+                         (__attribute__((address_space(3))) uint8_t *)(smem + P_OFF + (hl0 + nt * 16 + li) * PROW +
                                                                        lg * 16)))),
                      "v"(pk[nt])
                      : "memory");
@@ -784,10 +806,10 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       // C[t0 .. t0+3][c0 + L]; t0 = 4*lg and 16 + 4*lg match P^T's k order.
       // All eight column blocks of this wave's 128 latent columns are read
       // once and kept for both passes (outputs early-clobber: two reads share
-      // one address).  Accumulator block j holds head block (2*wave + j) & 7,
-      // so blocks 0 and 1 are this wave's own heads: their MFMAs run on P
-      // straight from registers while the other waves' P^T is written, and
-      // only the other six blocks wait for the barrier.
+      // one address).  Accumulator block j holds head block (NTW*wave + j) % NH
+      // of the group, so blocks j < NTW are this wave's own heads: their MFMAs
+      // run on P straight from registers while the other waves' P^T is
+      // written, and only the other NO blocks wait for the barrier.
       const int s16 = lane & 15;
       const uint32_t a0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
           (__attribute__((address_space(3))) const uint16_t *)(K + (4 * lg + (s16 >> 2)) * KROW + wave * 128 +
@@ -806,7 +828,10 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   asm volatile("s_waitcnt lgkmcnt(" #N ")" : "+v"(ta[MT]), "+v"(tb[MT])::"memory")
       // the own-head MFMAs read pk, written by VALU (the cvt/pack above): cover
       // the VALU write -> MFMA read wait states the compiler does not see
-      asm volatile("s_nop 4" : "+v"(pk[0]), "+v"(pk[1])::"memory");
+      if constexpr (NTW == 2)
+        asm volatile("s_nop 4" : "+v"(pk[0]), "+v"(pk[1])::"memory");
+      else
+        asm volatile("s_nop 4" : "+v"(pk[0])::"memory");
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) {
         switch (mt) {
@@ -820,39 +845,41 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
           default: AMLA_WTR(7, 0); break;
         }
         const bf16x8 a = as_bf16x8(u32x4{ta[mt].x, ta[mt].y, tb[mt].x, tb[mt].y});
-        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(o[mt][0]) : "v"(a), "v"(pk[0]));
-        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(o[mt][1]) : "v"(a), "v"(pk[1]));
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(o[mt][j]) : "v"(a), "v"(pk[j]));
       }
 #undef AMLA_WTR
       // every LDS operation of this wave is complete (lgkmcnt(0) above): after
       // the barrier all waves' P^T is visible
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      u32x4 pb[6];
+      u32x4 pb[NO];
       {
         const uint32_t paddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
             (__attribute__((address_space(3))) const uint8_t *)(smem + P_OFF + li * PROW + lg * 16)));
 #pragma unroll
-        for (int j = 0; j < 6; ++j) {
-          const uint32_t off = static_cast<uint32_t>((((2 * wave + 2 + j) & 7) * 16) * PROW);  // wave-uniform
+        for (int j = 0; j < NO; ++j) {
+          const uint32_t off = static_cast<uint32_t>((((NTW * wave + NTW + j) % NH) * 16) * PROW);  // wave-uniform
           asm volatile("ds_read_b128 %0, %1" : "=v"(pb[j]) : "v"(paddr + off));
         }
       }
+      // wait for block j's read: NO - 1 - j reads were issued after it
 #define AMLA_WPB(J, N) asm volatile("s_waitcnt lgkmcnt(" #N ")" : "+v"(pb[J])::"memory")
 #pragma unroll
-      for (int j = 0; j < 6; ++j) {
-        switch (j) {
-          case 0: AMLA_WPB(0, 5); break;
-          case 1: AMLA_WPB(1, 4); break;
-          case 2: AMLA_WPB(2, 3); break;
-          case 3: AMLA_WPB(3, 2); break;
-          case 4: AMLA_WPB(4, 1); break;
-          default: AMLA_WPB(5, 0); break;
+      for (int j = 0; j < NO; ++j) {
+        switch (NO - 1 - j) {
+          case 5: AMLA_WPB(j, 5); break;
+          case 4: AMLA_WPB(j, 4); break;
+          case 3: AMLA_WPB(j, 3); break;
+          case 2: AMLA_WPB(j, 2); break;
+          case 1: AMLA_WPB(j, 1); break;
+          default: AMLA_WPB(j, 0); break;
         }
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt) {  // accumulators pinned to AGPRs (only these MFMAs touch them in the loop)
           const bf16x8 a = as_bf16x8(u32x4{ta[mt].x, ta[mt].y, tb[mt].x, tb[mt].y});
-          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(o[mt][2 + j]) : "v"(a), "v"(pb[j]));
+          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(o[mt][NTW + j]) : "v"(a), "v"(pb[j]));
         }
       }
 #undef AMLA_WPB
@@ -870,9 +897,9 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   // MFMA write-to-read wait states the compiler does not see for inline asm
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   // ---- partial results of this split: (m, l) of the wave's heads, O of its
-  // latent columns for every head
+  // latent columns for every head of the group
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NTW; ++nt) {
     float l = l_run[nt];
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
@@ -893,16 +920,16 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   wait_vmcnt<0>();
   __syncthreads();
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt)
+  for (int nt = 0; nt < NH; ++nt)
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt)
-      *reinterpret_cast<u32x2 *>(smem + ((((2 * wave + nt) & 7) * 16) + li) * OROW +
+      *reinterpret_cast<u32x2 *>(smem + ((((NTW * wave + nt) % NH) * 16) + li) * OROW +
                                  (wave * 128 + mt * 16 + 4 * lg) * 2) =
           u32x2{pack_bf16(o[mt][nt].x, o[mt][nt].y), pack_bf16(o[mt][nt].z, o[mt][nt].w)};
   __syncthreads();
-  uint8_t *const dst = reinterpret_cast<uint8_t *>(p.part_o + (size_t)slot * HEADS * LORA);
+  uint8_t *const dst = reinterpret_cast<uint8_t *>(p.part_o + ((size_t)slot * HEADS + blockIdx.y * HG) * LORA);
 #pragma unroll 8
-  for (int i = 0; i < HEADS * LORA * 2 / (256 * 16); ++i) {
+  for (int i = 0; i < HG * LORA * 2 / (256 * 16); ++i) {
     const int chunk = i * 256 + tid, head = chunk >> 6, c16 = chunk & 63;
     *reinterpret_cast<u32x4 *>(dst + (size_t)chunk * 16) = *reinterpret_cast<const u32x4 *>(smem + head * OROW + c16 * 16);
   }
@@ -1203,6 +1230,12 @@ struct DecodeLayout {
 // many, one after another on the stream, sharing one workspace.
 constexpr int DECODE_MAX_BATCH = 64;
 
+// Head groups of the attention launch: two (64 heads per workgroup) while the
+// split slots fill at most half the CUs, so that a workgroup's fixed cost (the
+// query fragments in, the partial O out, both in proportion to its heads)
+// halves and twice the CUs share it; else one (all 128 heads).
+static int attn_head_groups(const DecodeLayout &L) { return L.slots <= 128 ? 2 : 1; }
+
 static DecodeLayout decode_layout(const amla_mla_args &a) {
   DecodeLayout L = {};
   const int B = std::min(a.batch, DECODE_MAX_BATCH);
@@ -1394,7 +1427,10 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   ap.part_o = reinterpret_cast<uint16_t *>(ws + L.part_o);
   ap.part_ml = reinterpret_cast<float *>(ws + L.part_ml);
   for (int r = 0; r < attn_repeat; ++r) {
-    attn_kernel<<<dim3(L.slots), 256, ATTN_LDS, st>>>(ap);
+    if (attn_head_groups(L) == 2)
+      attn_kernel<1><<<dim3(L.slots, 2), 256, ATTN_LDS, st>>>(ap);
+    else
+      attn_kernel<2><<<dim3(L.slots), 256, ATTN_LDS, st>>>(ap);
     if ((rc = check_launch("mla attention"))) return rc;
   }
 
@@ -1431,7 +1467,9 @@ static bool g_attr_set = false;
 static void set_attn_attr() {
   if (!g_attr_set) {
     // Opt in to more than 64 KB of dynamic LDS (gfx950 has 160 KB per CU).
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_kernel),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_kernel<1>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)ATTN_LDS);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_kernel<2>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)ATTN_LDS);
     (void)hipGetLastError();
     g_attr_set = true;
