@@ -969,7 +969,7 @@ struct XgShape {
   static constexpr int WPITCH = WSLICE * 2 + 16;  // bytes per x row of a slice
   static constexpr int XWP = WSLICE / 64;         // 16-byte pieces per lane and slice (8 rows)
   static constexpr size_t XLDS = XWAVE ? (size_t)XG_WAVES * 2 * XG_MAXM * WPITCH : (size_t)NXB * XG_MAXM * PITCH;
-  static constexpr size_t GAM = NCH == 1 ? (size_t)KC * 2 : 0;  // the norm weight (one chunk only)
+  static constexpr size_t GAM = NCH == 1 ? (size_t)KC * 4 : 0;  // the norm weight as fp32 (one chunk only)
   static constexpr size_t LDS = XLDS + GAM + (size_t)XG_WAVES * TPW * 64 * 16;
 };
 
@@ -981,7 +981,7 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
   constexpr int WK = S::WK, KC = S::KC, PITCH = S::PITCH, NIT = S::NIT, XPT = S::XPT;
   extern __shared__ __align__(16) uint8_t xsm[];
   const int M = p.M;
-  uint8_t *const gsm = xsm + S::XLDS;  // norm weight, bf16
+  uint8_t *const gsm = xsm + S::XLDS;  // norm weight, fp32
   f32x4 *const red = reinterpret_cast<f32x4 *>(gsm + S::GAM);
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1101,9 +1101,14 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
   if constexpr (S::XWAVE) store_xw(0);  // this wave's own reads follow in order: no barrier
   else store_x(0);
   if (NCH == 1) {
+    // unpacked once here: every row's pass below reads it as fp32
 #pragma unroll
     for (int i = 0; i < GPT; ++i)
-      if (tid + 512 * i < KC / 8) *reinterpret_cast<u32x4 *>(gsm + (tid + 512 * i) * 16) = gs[i];
+      if (tid + 512 * i < KC / 8) {
+        f32x4 *gd = reinterpret_cast<f32x4 *>(gsm + (tid + 512 * i) * 32);
+        gd[0] = f32x4{lo_bf(gs[i].x), hi_bf(gs[i].x), lo_bf(gs[i].y), hi_bf(gs[i].y)};
+        gd[1] = f32x4{lo_bf(gs[i].z), hi_bf(gs[i].z), lo_bf(gs[i].w), hi_bf(gs[i].w)};
+      }
   }
   if (NCH == 1 && p.xg) {
     // rms_norm(x, xg, eps_in) of each row (inference/ops.py:10-12) in place,
@@ -1116,23 +1121,37 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
       // the norm r = 1 and bf16(x * 1) = x
       float r = 1.f;
       if (p.xnorm) {
-        float ss = 0.f;
+        // squares of a bf16 pair in one v_dot2_f32_bf16 (exact products,
+        // fp32 sum), two chains
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int i = 0; i < PL; ++i) {
           const u32x4 v = *reinterpret_cast<const u32x4 *>(xr + (lane + 64 * i) * 16);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) ss += lo_bf(v[e]) * lo_bf(v[e]) + hi_bf(v[e]) * hi_bf(v[e]);
+          // named components: a subscripted element cast to bf16x2 was
+          // compiled as element 0
+          const uint32_t d0 = v.x, d1 = v.y, d2 = v.z, d3 = v.w;
+          s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, d0), __builtin_bit_cast(bf16x2, d0), s0, false);
+          s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, d1), __builtin_bit_cast(bf16x2, d1), s1, false);
+          s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, d2), __builtin_bit_cast(bf16x2, d2), s0, false);
+          s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, d3), __builtin_bit_cast(bf16x2, d3), s1, false);
         }
-        r = rsqrtf(vg_sum64(ss) / (float)p.K + p.eps_in);
+        r = rsqrtf(vg_sum64(s0 + s1) / (float)p.K + p.eps_in);
       }
+      // bf16(bf16(x r) g): one packed conversion rounds both halves of a
+      // pair after each product
 #pragma unroll
       for (int i = 0; i < PL; ++i) {
         const u32x4 v = *reinterpret_cast<const u32x4 *>(xr + (lane + 64 * i) * 16);
-        const u32x4 g = *reinterpret_cast<const u32x4 *>(gsm + (lane + 64 * i) * 16);
+        const f32x4 g0 = *reinterpret_cast<const f32x4 *>(gsm + (lane + 64 * i) * 32);
+        const f32x4 g1 = *reinterpret_cast<const f32x4 *>(gsm + (lane + 64 * i) * 32 + 16);
+        const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
         u32x4 y;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          y[e] = pack_bf16(round_bf16(lo_bf(v[e]) * r) * lo_bf(g[e]), round_bf16(hi_bf(v[e]) * r) * hi_bf(g[e]));
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t t = pack_bf16(lo_bf(v[e]) * r, hi_bf(v[e]) * r);
+          y[e] = pack_bf16(lo_bf(t) * g[2 * e], hi_bf(t) * g[2 * e + 1]);
+        }
         *reinterpret_cast<u32x4 *>(xr + (lane + 64 * i) * 16) = y;
       }
     }
