@@ -61,16 +61,18 @@ struct GemvPlan {
   int groups;        // workgroups
   size_t lds;        // dynamic LDS bytes per workgroup
   size_t part_bytes; // fp32 partial sums (kparts * M * N * 4) when kparts > 1
-  int vec;           // streaming GEMV, no K parts: 1 vgemv_kernel, 2 vgemv_short_kernel (one row of x),
-                     // 3 xgemv_kernel (2 .. 8 rows of x in LDS)
+  int vec;           // streaming GEMV: 1 vgemv_kernel, 2 vgemv_short_kernel (one row of x),
+                     // 3 xgemv_kernel (2 .. 8 rows of x in LDS), 4 mgemv_kernel (9 .. 64 rows of x,
+                     // kparts K parts summed by a finish as for gemv_kernel)
 };
 
 GemvPlan plan_gemv(int M, int N, int K);
 // plan_gemv, or a streaming GEMV where one applies: one row of x, N % 8 == 0,
 // and 4096 <= K <= 16384 (K % 128 == 0; vec = 1) or K = 1536 (one weight
 // segment, not the cache-row epilogue; vec = 2); or 2 .. 8 rows of x at the
-// attention projections' shapes (vec = 3).  For launch_gemv only (the
-// grouped and scheduled launches take plan_gemv plans).
+// attention projections' shapes (vec = 3); or 9 .. 64 rows of x at the MLA
+// projections' shapes (vec = 4).  For launch_gemv only (the grouped and
+// scheduled launches take plan_gemv plans).
 GemvPlan plan_linear(int M, int N, int K);
 size_t gemv_lds_bytes(int MT, int kpb, int rg, int kparts);  // MT = 16-row tiles of x (1, 2 or 4)
 // Launches the skinny GEMM for M <= 64 (N % 16 == 0, K % 128 == 0, 16-byte aligned rows);

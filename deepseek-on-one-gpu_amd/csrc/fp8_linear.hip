@@ -1312,6 +1312,352 @@ static int launch_xgemv(const GemvParams &p, int mode, hipStream_t st) {
   return check_launch("fp8 GEMV (x in LDS)");
 }
 
+// ---------------------------------------------------------------- streaming GEMV, 9 .. 64 rows of x
+//
+// The form of xgemv_kernel for more rows of x: NCT column tiles of 16 rows
+// (MP = 16 NCT), so each weight fragment feeds NCT MFMAs.  A workgroup (8
+// waves = WT tile groups x WK K groups) owns R = 16 TPW WT consecutive weight
+// rows and one of KP equal K parts (grid y); x of the part moves through LDS
+// in NCH chunks of KC = 128 IPW WK columns (all MP rows, double buffered,
+// staged through registers one chunk ahead; rows past M repeat row M - 1);
+// the weights stream straight into registers as whole 128-byte lines, D
+// 128-wide blocks ahead, converted and swapped into fragment order as in
+// xgemv_kernel.  Each block's TPW x NCT sums are scaled by its scale_inv; the
+// WK waves of a tile meet in LDS at the end (in wave order) and the workgroup
+// stores either the GEMV epilogue (KP = 1) or its fp32 K-part sums in the
+// [part][M][N] layout that gemv_finish (or the q_a | kv_a finish) sums in
+// part order.  With p.xg the GEMM takes bf16(x * xg) (the folded input norm).
+template <int NCT, int TPW, int WT, int IPW, int NCH>
+struct MgShape {
+  static constexpr int MP = 16 * NCT;
+  static constexpr int WK = XG_WAVES / WT;
+  static constexpr int KC = IPW * WK * 128;
+  static constexpr int PITCH = KC * 2 + 16;  // the 16 rows of a fragment read differ in bits 4-7
+  static constexpr int NXB = NCH > 1 ? 2 : 1;
+  static constexpr int XPT = MP * KC / 4096;  // 16-byte x pieces per thread and chunk
+  static constexpr int RING = NCH > 4 && NCT <= 2 ? 4 : 2;  // chunks of weights in registers
+  static constexpr size_t XLDS = (size_t)NXB * MP * PITCH;
+  static constexpr size_t RED = (size_t)XG_WAVES * TPW * NCT * 64 * 16;  // aliases the x buffers at the end
+  static constexpr size_t LDS = XLDS > RED ? XLDS : RED;
+  static_assert(XPT >= 1 && MP * KC % 4096 == 0, "whole x pieces per thread");
+};
+
+template <int NCT, int TPW, int WT, int IPW, int NCH, int MODE, bool PART>
+__global__ __launch_bounds__(512, 1) void mgemv_kernel(GemvParams p, int rpw) {
+  typedef MgShape<NCT, TPW, WT, IPW, NCH> S;
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  constexpr int WK = S::WK, KC = S::KC, PITCH = S::PITCH, XPT = S::XPT, MP = S::MP;
+  extern __shared__ __align__(16) uint8_t xsm[];
+  f32x4 *const red = reinterpret_cast<f32x4 *>(xsm);  // after the last chunk
+  const int M = p.M;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wt = wave % WT, wk = wave / WT;
+  const int li = lane & 15, lg = lane >> 4;
+  const int r0 = blockIdx.x * rpw;
+  const int rend = min(r0 + rpw, p.N);
+  const int KB = p.K >> 7;
+  const int kb0 = blockIdx.y * (NCH * IPW * WK);  // first 128-wide block of this K part
+  const bool two = MODE == GEMV_QKVA || p.w1 != nullptr;
+
+  // whole-line weight loads (xgemv_kernel's layout): lane l takes row l & 7
+  // (+8 for the second load) and 16-byte chunk cl of the block
+  const int cl = ((lane >> 4) & 1) + 2 * (lane >> 5) + 4 * ((lane >> 3) & 1);
+  const bool hi8 = (lane >> 3) & 1;
+  const uint8_t *wrow[TPW][2];
+  const float *srow[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int t0 = r0 + 16 * (wt + WT * j);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int rc = min(t0 + 8 * hf + (lane & 7), rend - 1);
+      const bool s1 = two && rc >= p.n_split;
+      wrow[j][hf] = (s1 ? p.w1 : p.w0) + (size_t)(s1 ? rc - p.n_split : rc) * p.K + 16 * cl;
+    }
+    const int rd = min(t0 + 4 * lg, p.N - 1);
+    const bool d1 = two && rd >= p.n_split;
+    srow[j] = (d1 ? p.s1 : p.s0) + (size_t)((d1 ? rd - p.n_split : rd) >> 7) * KB;
+  }
+
+  // x chunk c of the part -> registers (piece q: row q / (KC / 8), 16-byte
+  // column piece q % (KC / 8)), times xg when set
+  u32x4 xs[XPT];
+  auto load_x = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int q = tid + 512 * i, m = min(q / (KC / 8), M - 1), c8 = q % (KC / 8);
+      xs[i] = ldg16(p.x + (size_t)m * p.ldx + (size_t)kb0 * 128 + (size_t)c * KC + c8 * 8);
+    }
+  };
+  auto store_x = [&](int c) __attribute__((always_inline)) {
+    uint8_t *xb = xsm + (size_t)(c % S::NXB) * MP * PITCH;
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int q = tid + 512 * i, m = q / (KC / 8), c8 = q % (KC / 8);
+      u32x4 v = xs[i];
+      if (p.xg) {
+        const u32x4 g = ldg16(p.xg + (size_t)kb0 * 128 + (size_t)c * KC + c8 * 8);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = pack_bf16(lo_bf(v[e]) * lo_bf(g[e]), hi_bf(v[e]) * hi_bf(g[e]));
+      }
+      *reinterpret_cast<u32x4 *>(xb + m * PITCH + c8 * 16) = v;
+    }
+  };
+  auto lds_barrier = [&]() __attribute__((always_inline)) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // weights of RING chunks in registers: buffer c % RING holds chunk c's IPW
+  // blocks; chunk c + RING is loaded into it as soon as chunk c is consumed.
+  // Past the part's end the last chunk is read again (the same lines: no
+  // extra traffic), so every load is unconditional and the compiler's waits
+  // count exactly the loads in flight.
+  constexpr int RING = S::RING;
+  u32x4 W[RING][IPW][TPW][2];
+  float SC[RING][IPW][TPW];
+  auto load_w = [&](int buf, int c, int ii) __attribute__((always_inline)) {
+    const int kb = kb0 + min(c, NCH - 1) * (IPW * WK) + wk * IPW + ii;
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) W[buf][ii][j][hf] = ldg16_nt(wrow[j][hf] + (size_t)kb * 128);
+      SC[buf][ii][j] = srow[j][kb];
+    }
+  };
+
+  // x first, then the weights (waiting for x does not wait for the weights)
+  load_x(0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < RING; ++r)
+#pragma unroll
+    for (int ii = 0; ii < IPW; ++ii) load_w(r, r, ii);
+  __builtin_amdgcn_sched_barrier(0);
+  store_x(0);
+  lds_barrier();
+  load_x(min(1, NCH - 1));
+  __builtin_amdgcn_sched_barrier(0);
+
+  f32x4 acc[TPW][NCT];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j)
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) acc[j][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // chunk c from weight buffer buf; B operand of column tile ct: x row
+  // 16 ct + li (rows past M hold row M - 1)
+  auto chunk = [&](int c, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ii = 0; ii < IPW; ++ii) {
+      const uint8_t *xb = xsm + (size_t)(c % S::NXB) * MP * PITCH + li * PITCH + ((wk * IPW + ii) * 128 + 16 * lg) * 2;
+      f32x4 sm[TPW][NCT];
+#pragma unroll
+      for (int j = 0; j < TPW; ++j)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) sm[j][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        bf16x8 xf[NCT][2];
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            xf[ct][h] = as_bf16x8(*reinterpret_cast<const u32x4 *>(xb + (size_t)16 * ct * PITCH + 128 * st + 16 * h));
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) {
+          // rows 0-7 | rows 8-15 -> fragment order of step st
+          u32x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t x0 = W[buf][ii][j][0][e], x1 = W[buf][ii][j][1][e];
+            if (st == 0) {
+              const uint32_t r1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x1, 0x128, 0xf, 0xf, false);  // row_ror:8
+              w[e] = hi8 ? r1 : x0;
+            } else {
+              const uint32_t r0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x0, 0x128, 0xf, 0xf, false);
+              w[e] = hi8 ? x1 : r0;
+            }
+          }
+          bf16x2_t q[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            q[2 * e] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[e], 1.f, false);
+            q[2 * e + 1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[e], 1.f, true);
+          }
+          const bf16x8 a0 = {q[0][0], q[0][1], q[1][0], q[1][1], q[2][0], q[2][1], q[3][0], q[3][1]};
+          const bf16x8 a1 = {q[4][0], q[4][1], q[5][0], q[5][1], q[6][0], q[6][1], q[7][0], q[7][1]};
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) {
+            sm[j][ct] = mfma16(a0, xf[ct][0], sm[j][ct]);
+            sm[j][ct] = mfma16(a1, xf[ct][1], sm[j][ct]);
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < TPW; ++j)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) acc[j][ct] += SC[buf][ii][j] * sm[j][ct];
+      load_w(buf, c + RING, ii);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (NCH > 1 && c + 1 < NCH) {
+      // every wave is done with chunk c - 1, whose buffer takes chunk c + 1
+      // (loaded during chunk c - 1); then chunk c + 2 on its way
+      store_x(c + 1);
+      lds_barrier();
+      load_x(min(c + 2, NCH - 1));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  if constexpr (NCH <= 4) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) chunk(c, c % RING);
+  } else {
+    static_assert(NCH % RING == 0, "whole rings of chunks");
+#pragma unroll 1
+    for (int c = 0; c < NCH; c += RING) {
+#pragma unroll
+      for (int r = 0; r < RING; ++r) chunk(c + r, r);
+    }
+  }
+
+  // the x buffers become the reduction buffer: every wave is past its last read
+  lds_barrier();
+#pragma unroll
+  for (int j = 0; j < TPW; ++j)
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) red[((wave * TPW + j) * NCT + ct) * 64 + lane] = acc[j][ct];
+  lds_barrier();
+  const int ntile = (rend - r0 + 15) >> 4;
+  for (int u = tid; u < ntile * NCT * 64; u += 512) {
+    const int ln = u & 63, ct = (u >> 6) % NCT, tw = (u >> 6) / NCT;
+    const int wtt = tw % WT, j = tw / WT;
+    f32x4 v = red[((wtt * TPW + j) * NCT + ct) * 64 + ln];
+#pragma unroll
+    for (int k = 1; k < WK; ++k) v += red[(((k * WT + wtt) * TPW + j) * NCT + ct) * 64 + ln];
+    const int m = 16 * ct + (ln & 15), n = r0 + 16 * tw + 4 * (ln >> 4);
+    if (m < M && n < rend) {
+      if constexpr (PART)
+        *reinterpret_cast<f32x4 *>(p.part + ((size_t)blockIdx.y * M + m) * p.N + n) = v;
+      else
+        store4<MODE>(p, m, n, v);
+    }
+  }
+}
+
+// Shapes with an instantiation (the MLA projections): K, N, tile groups, K
+// parts; rows per workgroup R = 16 TPW WT.
+struct MgCfg {
+  int K, N, tpw, wt, ipw, nch, kp;
+};
+// Measured against the skinny MFMA GEMM (gemv_kernel + finish) at M = 16, 32
+// and 64 (kernel trace, one box): q_b 12.0 / 14.9 / 19.0 -> 10.7 / 12.1 /
+// 15.2 us, q_a | kv_a 11.4 / 13.8 / 18.6 -> 9.4 / 10.6 / 13.7, q_a 11.8 /
+// 13.4 / 18.2 -> 9.4 / 10.2 / 13.5, kv_b 7.3 / 8.7 / 11.5 -> 6.3 / 6.8 / 8.7.
+// o_proj (128 rows x 4 parts of 4096: 30.5 / 35.4 / 44.5 -> 36.2 / 39.2 /
+// 44.9) and kv_a alone (63 workgroups) stay on the skinny GEMM.
+constexpr MgCfg MG_CFGS[] = {
+    {1536, 24576, 3, 2, 1, 3, 1},  // q_b: 96 rows, whole K (256 workgroups)
+    {7168, 2112, 2, 2, 1, 2, 7},   // q_a | kv_a: 64 rows x 7 parts of 1024 (231 workgroups)
+    {7168, 1536, 2, 2, 1, 2, 7},   // q_a
+    {512, 32768, 2, 4, 2, 1, 1},   // kv_b: 128 rows, whole K (256 workgroups)
+};
+constexpr int MG_NCFG = sizeof(MG_CFGS) / sizeof(MG_CFGS[0]);
+
+static int mgemv_cfg(int M, int N, int K) {
+  if (M <= XG_MAXM || M > 64) return -1;
+  for (int c = 0; c < MG_NCFG; ++c)
+    if (MG_CFGS[c].K == K && MG_CFGS[c].N == N) return c;
+  return -1;
+}
+
+template <int NCT, int TPW, int WT, int IPW, int NCH, int MODE, bool PART>
+static void launch_mg(const GemvParams &p, int rpw, dim3 grid, hipStream_t st) {
+  typedef MgShape<NCT, TPW, WT, IPW, NCH> S;
+  static bool attr_set = false;  // raise the dynamic LDS limit once per process
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void *)mgemv_kernel<NCT, TPW, WT, IPW, NCH, MODE, PART>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    attr_set = true;
+  }
+  static_assert(S::LDS <= 160 * 1024, "LDS budget");
+  mgemv_kernel<NCT, TPW, WT, IPW, NCH, MODE, PART><<<grid, 512, S::LDS, st>>>(p, rpw);
+}
+
+template <int NCT, int TPW, int WT, int IPW, int NCH, bool PART>
+static void launch_mg_mode(const GemvParams &p, int mode, int rpw, dim3 grid, hipStream_t st) {
+  if constexpr (PART) {
+    launch_mg<NCT, TPW, WT, IPW, NCH, GEMV_F32, true>(p, rpw, grid, st);
+  } else {
+    switch (mode) {
+      case GEMV_PLAIN: launch_mg<NCT, TPW, WT, IPW, NCH, GEMV_PLAIN, false>(p, rpw, grid, st); break;
+      case GEMV_RESID: launch_mg<NCT, TPW, WT, IPW, NCH, GEMV_RESID, false>(p, rpw, grid, st); break;
+      case GEMV_QKVA: launch_mg<NCT, TPW, WT, IPW, NCH, GEMV_QKVA, false>(p, rpw, grid, st); break;
+      case GEMV_F32: launch_mg<NCT, TPW, WT, IPW, NCH, GEMV_F32, false>(p, rpw, grid, st); break;
+      default: launch_mg<NCT, TPW, WT, IPW, NCH, GEMV_QROPE, false>(p, rpw, grid, st); break;
+    }
+  }
+}
+
+// configurations with K parts store fp32 part sums (PART), the others the
+// GEMV epilogue
+template <int NCT>
+static void launch_mg_cfg(const GemvParams &p, int mode, int c, int rpw, dim3 grid, hipStream_t st) {
+  switch (c) {
+    case 0: launch_mg_mode<NCT, 3, 2, 1, 3, false>(p, mode, rpw, grid, st); break;
+    case 1:
+    case 2: launch_mg_mode<NCT, 2, 2, 1, 2, true>(p, mode, rpw, grid, st); break;
+    default: launch_mg_mode<NCT, 2, 4, 2, 1, false>(p, mode, rpw, grid, st); break;
+  }
+}
+
+static int launch_mgemv(const GemvParams &p, int mode, const GemvPlan &pl, hipStream_t st, bool finish) {
+  const int c = mgemv_cfg(p.M, p.N, p.K);
+  if (c < 0) return fail(AMLA_EINVAL, "fp8 GEMV (9 .. 64 rows of x): plan for another shape (M=%d N=%d K=%d)", p.M, p.N, p.K);
+  const MgCfg &g = MG_CFGS[c];
+  if (p.ldx < p.K || p.ldx % 8 || !aligned16(p.x) || (p.xg && !aligned16(p.xg)))
+    return fail(AMLA_EINVAL, "fp8 GEMV (9 .. 64 rows of x): x must be 16-byte aligned rows of at least K elements");
+  if ((mode == GEMV_QKVA || p.w1) && p.n_split % 4)
+    return fail(AMLA_EUNSUPPORTED, "fp8 GEMV (9 .. 64 rows of x): the first weight segment must be a multiple of 4 rows");
+  if (g.kp > 1 && !p.part) return fail(AMLA_EWORKSPACE, "fp8 GEMV (9 .. 64 rows of x): missing partial-sum workspace");
+  const int rpw = 16 * g.tpw * g.wt;
+  const dim3 grid((unsigned)((p.N + rpw - 1) / rpw), (unsigned)g.kp);
+  if (p.M <= 16) launch_mg_cfg<1>(p, mode, c, rpw, grid, st);
+  else if (p.M <= 32) launch_mg_cfg<2>(p, mode, c, rpw, grid, st);
+  else launch_mg_cfg<4>(p, mode, c, rpw, grid, st);
+  int rc = check_launch("fp8 GEMV (9 .. 64 rows of x)");
+  if (rc) return rc;
+  if (g.kp > 1 && finish) {
+    const int64_t total = (int64_t)p.M * (p.N / 4);
+    const unsigned blocks = (unsigned)((total + 63) / 64);
+    switch (mode) {
+      case GEMV_PLAIN: gemv_finish<GEMV_PLAIN><<<blocks, 64, 0, st>>>(p, g.kp); break;
+      case GEMV_RESID: gemv_finish<GEMV_RESID><<<blocks, 64, 0, st>>>(p, g.kp); break;
+      case GEMV_QKVA: gemv_finish<GEMV_QKVA><<<blocks, 64, 0, st>>>(p, g.kp); break;
+      case GEMV_F32: gemv_finish<GEMV_F32><<<blocks, 64, 0, st>>>(p, g.kp); break;
+      default: gemv_finish<GEMV_QROPE><<<blocks, 64, 0, st>>>(p, g.kp); break;
+    }
+    return check_launch("fp8 GEMV finish (9 .. 64 rows of x)");
+  }
+  (void)pl;
+  return AMLA_OK;
+}
+
+static GemvPlan plan_mgemv(int M, int N, int K) {
+  GemvPlan pl = {};
+  const MgCfg &g = MG_CFGS[mgemv_cfg(M, N, K)];
+  const int rpw = 16 * g.tpw * g.wt;
+  pl.kparts = g.kp;
+  pl.kpb = K / 128 / g.kp;
+  pl.rg = g.tpw * g.wt;
+  pl.groups = ((N + rpw - 1) / rpw) * g.kp;
+  pl.part_bytes = g.kp > 1 ? (size_t)g.kp * M * N * 4 : 0;
+  pl.vec = 4;
+  return pl;
+}
+
 // rows per workgroup of the streaming GEMV: about VG_GRID workgroups
 static int vgemv_rpw(int N) {
   const int r = (N + VG_GRID - 1) / VG_GRID;
@@ -1345,6 +1691,8 @@ GemvPlan plan_linear(int M, int N, int K) {
   } else if (xgemv_cfg(M, N, K) >= 0) {
     pl.groups = (N + xgemv_rpw(N) - 1) / xgemv_rpw(N);
     pl.vec = 3;
+  } else if (mgemv_cfg(M, N, K) >= 0) {
+    return plan_mgemv(M, N, K);
   } else {
     return plan_gemv(M, N, K);
   }
@@ -1404,6 +1752,7 @@ static void launch_mt(const GemvParams &p, int mode, const GemvPlan &pl, hipStre
 }
 
 int launch_gemv(const GemvParams &p0, int mode, const GemvPlan &pl, hipStream_t st, bool finish) {
+  if (pl.vec == 4) return launch_mgemv(p0, mode, pl, st, finish);
   if (pl.vec) return launch_vgemv(p0, mode, pl.vec, st);
   if (p0.M < 1 || p0.M > 64) return fail(AMLA_EINVAL, "skinny fp8 GEMM needs 1 <= M <= 64 (got %d)", p0.M);
   if (p0.N % 16 || p0.K % 128)

@@ -165,7 +165,7 @@ int amla_mla_decode_profiled_repeat(const amla_mla_args *args, void *stream, voi
  * overlap in time on one device (two streams, two threads) race and must be
  * serialised by the caller.  Returns AMLA_EWORKSPACE, launching nothing, when
  * amla_mla_decode_workspace_bytes(args) exceeds the array. */
-#define AMLA_NOALLOC_SCRATCH_BYTES (64u << 20)
+#define AMLA_NOALLOC_SCRATCH_BYTES (48u << 20)
 int amla_mla_decode_noalloc(const amla_mla_args *args, void *stream);
 
 /* Replaces mla_attention(...) for S >= 1 with a causal mask over the new rows

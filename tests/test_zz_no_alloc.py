@@ -64,7 +64,7 @@ def test_noalloc_refuses_a_call_beyond_the_array():
     aw, hidden, cache, tab, gamma = _case("noalloc-over", 64, 256)
     out = torch.empty_like(hidden)
     a, keep = _args(aw, hidden, cache, tab, 256, gamma, out)
-    assert lib().amla_mla_decode_workspace_bytes(a) > (64 << 20)
+    assert lib().amla_mla_decode_workspace_bytes(a) > (48 << 20)
     before = cache[0].clone()
     rc = lib().amla_mla_decode_noalloc(ctypes.byref(a), torch.cuda.current_stream().cuda_stream)
     assert rc == -2 and b"static array" in lib().amla_last_error()
