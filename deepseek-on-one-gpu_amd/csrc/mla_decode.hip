@@ -1019,9 +1019,11 @@ AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, const SeqSplits
   o1 = a1;
 }
 
-// Grid (H, ceil(B / SQ)), 512 threads: workgroup (h, g) finishes sequences
-// SQ g .. SQ g + SQ - 1 of head h, so W_UV[h] is read once per SQ sequences
-// (SQ = 4 up to batch 8, else 16: the MFMA's 16 columns).
+// Grid (VH H, ceil(B / SQ)), 512 threads: workgroup (VH h + i, g) finishes
+// sequences SQ g .. SQ g + SQ - 1 of head h, output rows 128 i / VH .. of
+// 128 / VH, so W_UV[h] is read once per SQ sequences (SQ = 4 up to batch 8,
+// else 16: the MFMA's 16 columns; VH = 2 for one sequence group, where two
+// workgroups per head halve each one's weight stream and both merge).
 //   merge units (sequence, part of its splits), WPS parts per sequence (2 up
 //     to batch 8, else 1), go to the 8 waves in turn (lane: latent columns
 //     8l .. 8l+7, one 16-byte load per split, up to XB splits in flight);
@@ -1033,7 +1035,7 @@ AMLA_DEV void recompute_split(const AttnParams &p, int b, int h, const SeqSplits
 //   out[b][v] = W_UV[h][v] . lat[b] by 16x16x32 MFMAs: A = W_UV rows (fp8
 //     converted exactly), B = lat of the SQ sequences (columns past them
 //     zero); wave w produces rows v = 16w .. 16w+15.
-template <int SQ, int WPS>
+template <int SQ, int WPS, int VH>
 __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const uint8_t *__restrict__ wkvb,
                                                          const float *__restrict__ skvb,
                                                          const uint16_t *__restrict__ gamma, int B,
@@ -1043,7 +1045,10 @@ __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const ui
   constexpr int WMAX = 256;       // weights per unit: at most 256 splits, a whole number of batches
   constexpr int LROW = LORA + 8;  // bf16 per lat row in LDS (16 B pad)
   static_assert(SQ <= 16 && NU <= 16, "one MFMA column per sequence; at most two units per wave");
-  const int h = blockIdx.x, b0 = blockIdx.y * SQ;
+  static_assert(VH == 1 || VH == 2, "whole or half W_UV[h] per workgroup");
+  constexpr int VW = 8 / VH;  // waves with W_UV rows
+  const int h = blockIdx.x / VH, b0 = blockIdx.y * SQ;
+  const int vbase = (blockIdx.x % VH) * (VD / VH);  // first output row of this workgroup
   const int nb = min(SQ, B - b0);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1059,18 +1064,22 @@ __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const ui
 #pragma unroll
   for (int q = 0; q < 4; ++q) bsc[q] = skvb[(size_t)(2 * h + 1) * (LORA / 128) + q];
 
-  // W_UV rows of this wave (rows v = 16w .. 16w+15, 8 bytes per lane and K
-  // step) are loaded first: nothing they feed depends on the merge
+  // W_UV rows of this wave (rows v = vbase + 16w .. +15, 8 bytes per lane and
+  // K step; waves w < VW) are loaded first: nothing they feed depends on the
+  // merge
   const int li = lane & 15, lg = lane >> 4;
-  const uint8_t *wr = wkvb + ((size_t)h * (NOPE + VD) + NOPE + 16 * wave + li) * LORA + 8 * lg;
+  const bool vwave = wave < VW;
+  const uint8_t *wr = wkvb + ((size_t)h * (NOPE + VD) + NOPE + vbase + 16 * (wave % VW) + li) * LORA + 8 * lg;
   u32x2 wa[LORA / 32];
   // non-temporal when this is the only workgroup reading these weight rows
-  if (gridDim.y == 1) {
+  if (vwave) {
+    if (gridDim.y == 1) {
 #pragma unroll
-    for (int ks = 0; ks < LORA / 32; ++ks) wa[ks] = ldg8_nt(wr + ks * 32);
-  } else {
+      for (int ks = 0; ks < LORA / 32; ++ks) wa[ks] = ldg8_nt(wr + ks * 32);
+    } else {
 #pragma unroll
-    for (int ks = 0; ks < LORA / 32; ++ks) wa[ks] = ldg8(wr + ks * 32);
+      for (int ks = 0; ks < LORA / 32; ++ks) wa[ks] = ldg8(wr + ks * 32);
+    }
   }
 
   // ---- fast merge: unit u = (sequence b0 + u / WPS, part u % WPS).  A
@@ -1196,7 +1205,8 @@ __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const ui
     __syncthreads();
   }
 
-  // ---- out = W_UV[h] . lat: wave w, rows 16w .. 16w+15, 16 K steps of 32
+  // ---- out = W_UV[h] . lat: wave w < VW, rows vbase + 16w .. +15, 16 K steps of 32
+  if (!vwave) return;
   f32x4 c = {0.f, 0.f, 0.f, 0.f};
   const bool bvalid = li < nb;
   const uint16_t *lr = &latb[bvalid ? li : 0][8 * lg];
@@ -1213,7 +1223,7 @@ __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const ui
   }
   // C: lane holds sequence b0 + li, rows v = 16w + 4 lg .. +3
   if (bvalid) {
-    uint16_t *dst = attn + (size_t)(b0 + li) * HEADS * VD + h * VD + 16 * wave + 4 * lg;
+    uint16_t *dst = attn + (size_t)(b0 + li) * HEADS * VD + h * VD + vbase + 16 * wave + 4 * lg;
     *reinterpret_cast<u32x2 *>(dst) = u32x2{pack_bf16(c.x, c.y), pack_bf16(c.z, c.w)};
   }
 }
@@ -1437,12 +1447,16 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   // 6. merge splits, W_UV
   mark(ev, 5, st);
   uint16_t *attn = reinterpret_cast<uint16_t *>(a->attn_out ? a->attn_out : ws + L.attn);
-  if (B <= 8)
-    combine_uv_kernel<4, 2><<<dim3(HEADS, (B + 3) / 4), 512, 0, st>>>(
+  if (B <= 2)  // one sequence group: W_UV[h] split over two workgroups
+    combine_uv_kernel<4, 2, 2><<<dim3(2 * HEADS, 1), 512, 0, st>>>(
+        ap, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv), B,
+        attn);
+  else if (B <= 8)
+    combine_uv_kernel<4, 2, 1><<<dim3(HEADS, (B + 3) / 4), 512, 0, st>>>(
         ap, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv), B,
         attn);
   else
-    combine_uv_kernel<16, 1><<<dim3(HEADS, (B + 15) / 16), 512, 0, st>>>(
+    combine_uv_kernel<16, 1, 1><<<dim3(HEADS, (B + 15) / 16), 512, 0, st>>>(
         ap, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv), B,
         attn);
   if ((rc = check_launch("mla combine"))) return rc;
