@@ -1335,7 +1335,7 @@ struct MgShape {
   static constexpr int PITCH = KC * 2 + 16;  // the 16 rows of a fragment read differ in bits 4-7
   static constexpr int NXB = NCH > 1 ? 2 : 1;
   static constexpr int XPT = MP * KC / 4096;  // 16-byte x pieces per thread and chunk
-  static constexpr int RING = NCH > 4 && NCT <= 2 ? 4 : 2;  // chunks of weights in registers
+  static constexpr int RING = 2;              // chunks of weights in registers
   static constexpr size_t XLDS = (size_t)NXB * MP * PITCH;
   static constexpr size_t RED = (size_t)XG_WAVES * TPW * NCT * 64 * 16;  // aliases the x buffers at the end
   static constexpr size_t LDS = XLDS > RED ? XLDS : RED;
@@ -1511,17 +1511,9 @@ __global__ __launch_bounds__(512, 1) void mgemv_kernel(GemvParams p, int rpw) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  if constexpr (NCH <= 4) {
+  static_assert(NCH <= 4, "the chunk loop is unrolled");
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) chunk(c, c % RING);
-  } else {
-    static_assert(NCH % RING == 0, "whole rings of chunks");
-#pragma unroll 1
-    for (int c = 0; c < NCH; c += RING) {
-#pragma unroll
-      for (int r = 0; r < RING; ++r) chunk(c + r, r);
-    }
-  }
+  for (int c = 0; c < NCH; ++c) chunk(c, c % RING);
 
   // the x buffers become the reduction buffer: every wave is past its last read
   lds_barrier();
