@@ -91,20 +91,44 @@ __global__ __launch_bounds__(256) void dequant_scalar_kernel(const uint8_t *__re
 
 // ---------------------------------------------------------------- epilogue
 
-AMLA_DEV int row_position(const GemvParams &p, int m) {
-  return p.pos[m / p.seq_len] + m % p.seq_len;
+// Operands the epilogue of outputs (m, n .. n+3) reads besides the sums: the
+// residual (RESID), the position of row m (QKVA, QROPE) and the (cos, sin)
+// pairs of that position for columns n .. n+3 (QROPE; loaded for every column,
+// used by the rope columns).  The streaming GEMVs load them at the start
+// (epi_load1, then epi_load2, which depends on the position, once the stream
+// is issued), so that their tail waits for no further round trip.
+struct EpiOps {
+  int pos;
+  u32x2 res;
+  f32x4 cs;
+};
+
+template <int MODE>
+AMLA_DEV void epi_load1(const GemvParams &p, int m, int n, EpiOps &e) {
+  if constexpr (MODE == GEMV_RESID) e.res = *reinterpret_cast<const u32x2 *>(p.res + (size_t)m * p.ldr + n);
+  if constexpr (MODE == GEMV_QKVA || MODE == GEMV_QROPE) e.pos = p.pos[m / p.seq_len];
 }
 
-// Stores 4 consecutive outputs n .. n+3 of row m (fp32, fully reduced).
 template <int MODE>
-AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
+AMLA_DEV void epi_load2(const GemvParams &p, int m, int n, EpiOps &e) {
+  if constexpr (MODE == GEMV_QROPE) {
+    const int i = max(n % p.head_dim - p.nope, 0) >> 1;
+    const int64_t row = min(e.pos + m % p.seq_len, p.rope_rows - 1);  // in bounds for any device position
+    e.cs = *reinterpret_cast<const f32x4 *>(p.rope_table + (row * (p.rope >> 1) + i) * 2);
+  }
+}
+
+// Stores 4 consecutive outputs n .. n+3 of row m (fp32, fully reduced), its
+// other operands from e.
+template <int MODE>
+AMLA_DEV void store4e(const GemvParams &p, int m, int n, f32x4 v, const EpiOps &e) {
   if (MODE == GEMV_PLAIN) {
     u32x2 o = {pack_bf16(v.x, v.y), pack_bf16(v.z, v.w)};
     *reinterpret_cast<u32x2 *>(p.y + (size_t)m * p.ldy + n) = o;
   } else if (MODE == GEMV_F32) {
     *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.y) + (size_t)m * p.ldy + n) = v;
   } else if (MODE == GEMV_RESID) {
-    const u32x2 r = *reinterpret_cast<const u32x2 *>(p.res + (size_t)m * p.ldr + n);
+    const u32x2 r = e.res;
     u32x2 o = {pack_bf16(lo_bf(r.x) + round_bf16(v.x), hi_bf(r.x) + round_bf16(v.y)),
                pack_bf16(lo_bf(r.y) + round_bf16(v.z), hi_bf(r.y) + round_bf16(v.w))};
     *reinterpret_cast<u32x2 *>(p.y + (size_t)m * p.ldy + n) = o;
@@ -114,7 +138,7 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
       *reinterpret_cast<u32x2 *>(p.y + (size_t)m * p.ldy + n) = o;
     } else {
       const int b = m / p.seq_len;
-      const int64_t row = row_position(p, m);
+      const int64_t row = e.pos + m % p.seq_len;
       if (row >= p.max_rows) return;  // a device position past the cache: nothing is written
       const int nn = n - p.n_split;
       uint16_t *dst = nn < p.kv_lora
@@ -124,11 +148,8 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
     }
   } else {  // GEMV_QROPE
     float a0 = round_bf16(v.x), a1 = round_bf16(v.y), a2 = round_bf16(v.z), a3 = round_bf16(v.w);
-    const int d = n % p.head_dim;
-    if (d >= p.nope) {
-      const int i = (d - p.nope) >> 1;
-      const int64_t row = min(row_position(p, m), p.rope_rows - 1);  // in bounds for any device position
-      const f32x4 cs = *reinterpret_cast<const f32x4 *>(p.rope_table + (row * (p.rope >> 1) + i) * 2);
+    if (n % p.head_dim >= p.nope) {
+      const f32x4 cs = e.cs;
       // (x0 + i x1) * (c + i s), each product rounded, no fused multiply-add
       const float r0 = __fsub_rn(__fmul_rn(a0, cs.x), __fmul_rn(a1, cs.y));
       const float r1 = __fadd_rn(__fmul_rn(a0, cs.y), __fmul_rn(a1, cs.x));
@@ -139,6 +160,15 @@ AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
     u32x2 o = {pack_bf16(a0, a1), pack_bf16(a2, a3)};
     *reinterpret_cast<u32x2 *>(p.y + (size_t)m * p.ldy + n) = o;
   }
+}
+
+// store4e with its operands loaded here.
+template <int MODE>
+AMLA_DEV void store4(const GemvParams &p, int m, int n, f32x4 v) {
+  EpiOps e = {};
+  epi_load1<MODE>(p, m, n, e);
+  epi_load2<MODE>(p, m, n, e);
+  store4e<MODE>(p, m, n, v, e);
 }
 
 // ---------------------------------------------------------------- skinny GEMM
@@ -675,6 +705,11 @@ __global__ __launch_bounds__(256, 2) void vgemv_kernel(GemvParams p, int rpw) {
   const int nb = blockIdx.x * rpw;
   const int C = p.K >> 4;  // 16-byte chunks per weight row
   const int KB = p.K >> 7;
+  // epilogue operands of this thread's four rows (threads past them load the
+  // run's last four, in bounds)
+  const int en = min(nb + min(4 * tid, rpw - 4), p.N - 4);
+  EpiOps eo = {};
+  epi_load1<MODE>(p, 0, en, eo);
 
   // this thread's chunks of x (16 bf16 each) and of xg, loaded before the
   // weights so that waiting for them does not wait for the weight loads
@@ -733,6 +768,7 @@ __global__ __launch_bounds__(256, 2) void vgemv_kernel(GemvParams p, int rpw) {
   };
   const int ng = rpw / VG_R;  // even, >= 2
   load(wa, sa, nb);  // in flight while x is prepared
+  epi_load2<MODE>(p, 0, en, eo);
   if (p.xnorm) {
     // rms_norm(x, xg, eps_in) of the whole row (inference/ops.py:10-12), as
     // the row-norm kernel computes it; the barrier is LDS-only, so the weight
@@ -786,7 +822,7 @@ __global__ __launch_bounds__(256, 2) void vgemv_kernel(GemvParams p, int rpw) {
       const int r = 4 * tid + i;
       v[i] = (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]);
     }
-    store4<MODE>(p, 0, nb + 4 * tid, v);
+    store4e<MODE>(p, 0, nb + 4 * tid, v, eo);
   }
 }
 
@@ -809,6 +845,11 @@ __global__ __launch_bounds__(256, 2) void vgemv_short_kernel(GemvParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nw = blockIdx.x * VGS_RPW + wave * (VGS_RPW / 4);  // this wave's first row
   const int KB = p.K >> 7;
+  // epilogue operands of this thread's four rows (threads past them load the
+  // workgroup's last four, in bounds)
+  const int en = min(blockIdx.x * VGS_RPW + min(4 * tid, VGS_RPW - 4), p.N - 4);
+  EpiOps eo = {};
+  epi_load1<MODE>(p, 0, en, eo);
   // span chunk i of this lane: row ri[i] of the span, column chunk ci[i]
   int ri[VGS_CPL], ci[VGS_CPL];
 #pragma unroll
@@ -876,6 +917,7 @@ __global__ __launch_bounds__(256, 2) void vgemv_short_kernel(GemvParams p) {
   };
   load(wa, nw);
   load(wb, nw + VGS_G * VGS_S);
+  epi_load2<MODE>(p, 0, en, eo);
   // x prepared while the weights are in flight: rms_norm(x, xg, eps_in) of
   // the whole row (inference/ops.py:10-12; each wave holds every column
   // chunk, the span's first row once), or bf16(x * xg)
@@ -916,7 +958,7 @@ __global__ __launch_bounds__(256, 2) void vgemv_short_kernel(GemvParams p) {
     f32x4 v;
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = red[4 * tid + i];
-    store4<MODE>(p, 0, nb + 4 * tid, v);
+    store4e<MODE>(p, 0, nb + 4 * tid, v, eo);
   }
 }
 
@@ -992,6 +1034,11 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
   const int rend = min(r0 + rpw, p.N);
   const int KB = p.K >> 7;
   const bool two = MODE == GEMV_QKVA || p.w1 != nullptr;
+  // epilogue operands of the outputs this thread stores (tile tid / 64, x row
+  // lane % 16, rows 4 (lane / 16) ..; threads past them load in-bounds ones)
+  const int em = min(lane & 15, M - 1), en = min(r0 + 16 * (tid >> 6) + 4 * (lane >> 4), rend - 4);
+  EpiOps eo = {};
+  epi_load1<MODE>(p, em, en, eo);
 
   // Weight loads read whole 128-byte lines: for each tile and 128-wide block
   // one load covers rows 0-7 and one rows 8-15, lane l taking row l & 7 and
@@ -1097,6 +1144,7 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 0; i < D; ++i) load_w(i);
+  epi_load2<MODE>(p, em, en, eo);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (S::XWAVE) store_xw(0);  // this wave's own reads follow in order: no barrier
   else store_x(0);
@@ -1238,7 +1286,7 @@ __global__ __launch_bounds__(512, 1) void xgemv_kernel(GemvParams p, int rpw) {
 #pragma unroll
     for (int k = 1; k < WK; ++k) v += red[((k * WT + wtt) * TPW + j) * 64 + ln];
     const int m = ln & 15, n = r0 + 16 * tw + 4 * (ln >> 4);
-    if (m < M && n < rend) store4<MODE>(p, m, n, v);
+    if (m < M && n < rend) store4e<MODE>(p, m, n, v, eo);  // (m, n) = (em, en) here
   }
 }
 
