@@ -310,6 +310,18 @@ def test_layer_mode_batch8_cache_rows():
         _check_cache(gc, rc, [(pos, pos + 1)] * B)
 
 
+def test_layer_mode_batches_above_8():
+    """Layer-mode decode of 9-64 sequences: the q_a|kv_a GEMV for 9-64 rows of x projects
+    bf16(x * gamma) in K parts and the finish applies each row's norm factor (the folded input
+    norm of _check_layer_cache); 24 and 40 sequences take two and four 16-row column tiles."""
+    for tag, B, pos, max_seq in (("layerb24", 24, 500, 504), ("layerb40", 40, 200, 208)):
+        got, want, gc, rc = _run_case(tag, B, 1, pos, max_seq, layer_mode=True)
+        assert_parity(got, want, f"layer {tag}")
+        lay = _layer("mla/" + tag)
+        _check_layer_cache(gc, rc, synth.make_hidden(R1, B, 1, tag), lay.input_layernorm, lay.attn_weights,
+                           pos, pos + 1)
+
+
 def test_prefill_row_equals_decode():
     """Prefill of S tokens, row S-1 == prefill of S-1 tokens followed by a decode step."""
     lay = _layer("mla/consistency")
