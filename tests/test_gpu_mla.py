@@ -209,6 +209,15 @@ def test_decode_ragged_positions():
     _check_cache(gc, rc, [(p, p + 1) for p in pos])
 
 
+def test_decode_ragged_head_groups():
+    """A ragged batch with few split slots (3 sequences, 75 split units): the attention runs two
+    workgroups of 64 heads per slot, both reading the split plan table of the unequal tile counts."""
+    pos = [1500, 90, 777]
+    got, want, gc, rc = _run_case("raggedhg", 3, 1, pos, 1600)
+    assert_parity(got, want, "ragged decode, head groups")
+    _check_cache(gc, rc, [(p, p + 1) for p in pos])
+
+
 def test_decode_batch32_ragged():
     """Batched decode at batch 32 with ragged positions (the reference's batched-decode
     workload, at contexts the oracle finishes in seconds): 17..32-row skinny GEMMs and
