@@ -1041,7 +1041,7 @@ __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const ui
                                                          const uint16_t *__restrict__ gamma, int B,
                                                          uint16_t *__restrict__ attn) {
   constexpr int NU = SQ * WPS;    // merge units
-  constexpr int XB = 16;          // splits in flight per wave (a batch)
+  constexpr int XB = SQ > 4 ? 8 : 16;  // splits in flight per wave (a batch)
   constexpr int WMAX = 256;       // weights per unit: at most 256 splits, a whole number of batches
   constexpr int LROW = LORA + 8;  // bf16 per lat row in LDS (16 B pad)
   static_assert(SQ <= 16 && NU <= 16, "one MFMA column per sequence; at most two units per wave");
