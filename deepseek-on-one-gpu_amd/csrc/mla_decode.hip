@@ -80,16 +80,23 @@ inline size_t plan_ints(int B, int slots) { return PLAN_HDR + 2 * (size_t)B + sl
 
 AMLA_DEV int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
-// Smallest and largest tile count of the batch (uniform scalar loads).
+// Smallest and largest tile count of the batch (B <= 64), wave-uniform: lane
+// b loads sequence b's position (one vector load: a loop of scalar loads
+// waited for each one in turn, a round trip per sequence), then a butterfly
+// over the wave.  Every lane of the wave must call it.
 AMLA_DEV int2 batch_tile_range(const int32_t *pos, int tmax, int B) {
+  const int lane = threadIdx.x & 63;
   int lo = INT_MAX, hi = 0;
-  for (int b = 0; b < B; ++b) {
-    const int T = min(pos[b] + 1, tmax);
-    const int n = T > 0 ? ceil_div(T, TT) : 0;
-    lo = min(lo, n);
-    hi = max(hi, n);
+  if (lane < B) {
+    const int T = min(pos[lane] + 1, tmax);
+    lo = hi = T > 0 ? ceil_div(T, TT) : 0;
   }
-  return int2{lo, hi};
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    lo = min(lo, __shfl_xor(lo, o, 64));
+    hi = max(hi, __shfl_xor(hi, o, 64));
+  }
+  return int2{__builtin_amdgcn_readfirstlane(lo), __builtin_amdgcn_readfirstlane(hi)};
 }
 
 // Splits per sequence of a batch whose sequences all have n tiles.
@@ -97,67 +104,91 @@ AMLA_DEV int uniform_splits(int n, int units, int B) {
   return n > 0 ? ceil_div(n, ceil_div(n, units / B)) : 1;
 }
 
-// The table of a batch with unequal tile counts: one 256-thread workgroup,
-// batch <= 64 (the decode limit); lds holds 2 * B + 4 ints.
+// ceil(a / b) for 0 <= a < 2^22, b >= 1, with rb = 1 / b in fp32: the product
+// is within 1 of a / b, so one correction step makes the quotient exact (an
+// integer division is a long instruction sequence on the GPU).
+AMLA_DEV int ceil_div_rcp(int a, int b, float rb) {
+  int q = static_cast<int>(static_cast<float>(a) * rb);
+  int r = a - q * b;
+  if (r < 0) {
+    --q;
+    r += b;
+  } else if (r >= b) {
+    ++q;
+    r -= b;
+  }
+  return q + (r > 0);
+}
+
+AMLA_DEV int wave_sum_int(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+AMLA_DEV int wave_max_int(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// The table of a batch with unequal tile counts, by one 256-thread workgroup
+// (batch <= 64, the decode limit; lds holds 2 * B + 4 ints).  Wave 0 holds
+// sequence b's tile count in lane b and finds L by bisection (the sum of
+// ceil(N_b / L) does not grow with L, and L = max N_b fits), then s_b and
+// first_b by a scan over its lanes; every thread then writes the sequence of
+// its slots (a binary search over first_b).
 AMLA_DEV void build_split_plan(const int32_t *__restrict__ pos, int tmax, int B, int units, int slots,
                                int32_t *__restrict__ plan, int *lds) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int *nt = lds, *first = lds + B, *sh = lds + 2 * B;
-  if (tid < B) {
-    const int T = min(pos[tid] + 1, tmax);
-    nt[tid] = T > 0 ? ceil_div(T, TT) : 0;
-  }
-  __syncthreads();
-  int N = 0, most = 0;
-  for (int b = 0; b < B; ++b) {
-    N += nt[b];
-    most = max(most, nt[b]);
-  }
-  // smallest L in [lo, hi] that fits: 256 candidates per round, the last one
-  // hi itself (which fits), so each round keeps the interval between two
-  // neighbouring candidates
-  int lo = max(1, ceil_div(N, units)), hi = max(lo, most);
-  while (lo < hi) {
-    const int step = (hi - lo + 254) / 255;
-    const int cand = min(hi, lo + step * tid);
-    int f = 0;
-    for (int b = 0; b < B; ++b) f += ceil_div(nt[b], cand);
-    const unsigned long long fits = __builtin_amdgcn_ballot_w64(f <= units);
-    if (lane == 0) sh[wave] = fits ? wave * 64 + __builtin_ctzll(fits) : 256;
-    __syncthreads();
-    const int k = min(min(sh[0], sh[1]), min(sh[2], sh[3]));
-    __syncthreads();
-    if (k == 0) {
-      hi = lo;
-    } else if (k == 256) {  // not reached while batch <= units
-      lo = hi;
-    } else {
-      const int top = min(hi, lo + step * k);
-      lo = lo + step * (k - 1) + 1;
-      hi = top;
+  int *first = lds + B, *sh = lds + 2 * B;
+  if (wave == 0) {
+    int n = 0;
+    if (lane < B) {
+      const int T = min(pos[lane] + 1, tmax);
+      n = T > 0 ? ceil_div(T, TT) : 0;
     }
-  }
-  const int L = lo;
-  if (tid == 0) {
-    int acc = 0;
-    for (int b = 0; b < B; ++b) {
-      const int sb = max(1, ceil_div(nt[b], L));
-      first[b] = acc;
-      plan[PLAN_HDR + 2 * b] = acc;
-      plan[PLAN_HDR + 2 * b + 1] = sb;
-      acc += sb;
+    const int N = wave_sum_int(n), most = wave_max_int(n);
+    int lo = max(1, ceil_div(N, units)), hi = max(lo, most);
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      const float rm = 1.f / static_cast<float>(mid);
+      const int f = wave_sum_int(lane < B ? ceil_div_rcp(n, mid, rm) : 0);
+      if (f <= units) hi = mid;
+      else lo = mid + 1;
     }
-    plan[0] = L;
-    plan[1] = acc;
-    sh[0] = acc;
+    const int L = lo;
+    const int sb = lane < B ? max(1, ceil_div(n, L)) : 0;
+    int incl = sb;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += v;
+    }
+    if (lane < B) {
+      first[lane] = incl - sb;
+      plan[PLAN_HDR + 2 * lane] = incl - sb;
+      plan[PLAN_HDR + 2 * lane + 1] = sb;
+    }
+    if (lane == B - 1) {
+      plan[0] = L;
+      plan[1] = incl;
+      sh[0] = incl;
+    }
   }
   __syncthreads();
   const int total = sh[0];
+  // the sequence of each slot: the last b with first_b <= slot (first is
+  // increasing, every s_b >= 1)
   for (int slot = tid; slot < slots; slot += 256) {
     int b = -1;
     if (slot < total) {
-      b = 0;
-      while (b + 1 < B && first[b + 1] <= slot) ++b;
+      int l = 0, r = B - 1;
+      while (l < r) {
+        const int mid = (l + r + 1) >> 1;
+        if (first[mid] <= slot) l = mid;
+        else r = mid - 1;
+      }
+      b = l;
     }
     plan[PLAN_HDR + 2 * B + slot] = b;
   }
@@ -166,7 +197,7 @@ AMLA_DEV void build_split_plan(const int32_t *__restrict__ pos, int tmax, int B,
 // ---------------------------------------------------------------- absorb
 
 // One workgroup (4 waves) per (head h, 128-column quarter q of the latent,
-// group of 16 sequences): it stages the quarter W_UK[h][:, 128q .. +127]
+// group of 16 or 32 sequences): it stages the quarter W_UK[h][:, 128q .. +127]
 // (16 KB, W_UK[h] = kv_b rows h*256 .. h*256+127, one 128-row scale block)
 // and the group's q_nope rows in LDS; wave w computes latent columns
 // 32w .. +31 of it by 16x16x32 MFMAs: A = q_nope (sequences x d; rows past
@@ -174,13 +205,16 @@ AMLA_DEV void build_split_plan(const int32_t *__restrict__ pos, int tmax, int B,
 // column) by the 8-bit transpose read (lane L of a 16-lane group receives
 // column L of the eight rows its group addresses), fp8 -> bf16 exactly;
 // qt = gamma_kv * s_UK * sum, through LDS into 16-byte stores of the
-// fragment-ordered query.  Workgroup (0, 0, 0) also writes the split plan
-// table of a batch with unequal tile counts.
-constexpr int AB_SEQ = 16;                // sequences per workgroup (the MFMA's 16 rows)
+// fragment-ordered query.  An extra workgroup (HEADS, 0, 0) writes the split
+// plan table of a batch with unequal tile counts.
+constexpr int AB_SEQ = 16;                // sequences per MFMA row tile (the MFMA's 16 rows)
 constexpr int AB_WPITCH = 128 + 16;       // bytes per W_UK quarter row in LDS (fp8)
 constexpr int AB_NPITCH = NOPE * 2 + 16;  // bytes per q_nope row (bf16)
 constexpr int AB_OPITCH = 128 * 2 + 16;   // bytes per output row (bf16)
 
+// RT row tiles of 16 sequences per workgroup (2 above 16 sequences: each
+// W_UK fragment read feeds both, and the quarter is read once per 32)
+template <int RT>
 __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict__ q,  // (B, H, 192)
                                                      const uint8_t *__restrict__ wkvb,
                                                      const float *__restrict__ skvb,
@@ -190,21 +224,24 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
                                                      int slots, int32_t *__restrict__ plan) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   typedef int v2i __attribute__((ext_vector_type(2)));
+  constexpr int NS = RT * AB_SEQ;  // sequences of the workgroup
   __shared__ __align__(16) uint8_t wsm[NOPE * AB_WPITCH];
-  __shared__ __align__(16) uint8_t nsm[AB_SEQ * AB_NPITCH];
-  __shared__ __align__(16) uint8_t osm[AB_SEQ * AB_OPITCH];
+  __shared__ __align__(16) uint8_t nsm[NS * AB_NPITCH];
+  __shared__ __align__(16) uint8_t osm[NS * AB_OPITCH];
   static_assert(sizeof(wsm) >= (2 * 64 + 8) * sizeof(int), "the plan's scratch (batch <= 64) fits wsm");
-  const int h = blockIdx.x, quarter = blockIdx.y, b0 = blockIdx.z * AB_SEQ;
-  const int nb = min(AB_SEQ, B - b0);
+  const int h = blockIdx.x, quarter = blockIdx.y, b0 = blockIdx.z * NS;
+  const int nb = min(NS, B - b0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  if (h == 0 && quarter == 0 && blockIdx.z == 0) {
-    const int2 r = batch_tile_range(pos, tmax, B);
-    if (r.x != r.y) {
-      // the plan's scratch (2 B + 4 ints) is wsm, written below after the barrier
-      build_split_plan(pos, tmax, B, units, slots, plan, reinterpret_cast<int *>(wsm));
-      __syncthreads();
+  if (h == HEADS) {
+    // the extra column of workgroups: (HEADS, 0, 0) writes the split plan of
+    // a batch with unequal tile counts (alongside the absorb workgroups, not
+    // before one of them), the others have no work
+    if (quarter == 0 && blockIdx.z == 0) {
+      const int2 r = batch_tile_range(pos, tmax, B);
+      if (r.x != r.y) build_split_plan(pos, tmax, B, units, slots, plan, reinterpret_cast<int *>(wsm));
     }
+    return;
   }
   // W_UK quarter: 128 rows x 128 bytes, four 16-byte pieces per thread
   // (non-temporal when this is the only group of sequences reading it);
@@ -225,24 +262,32 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
       wv[i] = ldg16(wq + (size_t)(p >> 3) * LORA + (p & 7) * 16);
     }
   }
-  const u32x4 nv = ldg16(q + ((size_t)(b0 + min(tid >> 4, nb - 1)) * HEADS + h) * (NOPE + ROPE) + (tid & 15) * 8);
+  u32x4 nv[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+    nv[r] = ldg16(q + ((size_t)(b0 + min(16 * r + (tid >> 4), nb - 1)) * HEADS + h) * (NOPE + ROPE) + (tid & 15) * 8);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int p = tid + 256 * i;
     *reinterpret_cast<u32x4 *>(wsm + (p >> 3) * AB_WPITCH + (p & 7) * 16) = wv[i];
   }
-  *reinterpret_cast<u32x4 *>(nsm + (tid >> 4) * AB_NPITCH + (tid & 15) * 16) = nv;
+#pragma unroll
+  for (int r = 0; r < RT; ++r) *reinterpret_cast<u32x4 *>(nsm + (16 * r + (tid >> 4)) * AB_NPITCH + (tid & 15) * 16) = nv[r];
   __syncthreads();
 
-  bf16x8 a[NOPE / 32];
+  bf16x8 a[RT][NOPE / 32];
 #pragma unroll
-  for (int ks = 0; ks < NOPE / 32; ++ks)
-    a[ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(nsm + li * AB_NPITCH + (32 * ks + 8 * lg) * 2));
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int ks = 0; ks < NOPE / 32; ++ks)
+      a[r][ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(nsm + (16 * r + li) * AB_NPITCH + (32 * ks + 8 * lg) * 2));
   const float sc = skvb[(size_t)(2 * h) * (LORA / 128) + quarter];
 #pragma unroll
   for (int cbi = 0; cbi < 2; ++cbi) {
     const int cb = 2 * wave + cbi;
-    f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 d4[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) d4[r] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < NOPE / 32; ++ks) {
       const uint8_t *ap = wsm + (32 * ks + 8 * lg + (li >> 1)) * AB_WPITCH + 16 * cb + 8 * (li & 1);
@@ -252,18 +297,22 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
       const bf16x2_t c2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w2.y, 1.f, false);
       const bf16x2_t c3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w2.y, 1.f, true);
       const bf16x8 bw = {c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
-      d4 = mfma16(a[ks], bw, d4);
+#pragma unroll
+      for (int r = 0; r < RT; ++r) d4[r] = mfma16(a[r][ks], bw, d4[r]);
     }
-    // D: latent column 16 cb + li of the quarter, sequences b0 + 4 lg .. +3
+    // D: latent column 16 cb + li of the quarter, sequences b0 + 16 r + 4 lg .. +3
     const int c = 16 * cb + li;
     const float g = bf2f(gamma[quarter * 128 + c]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      *reinterpret_cast<uint16_t *>(osm + (4 * lg + e) * AB_OPITCH + c * 2) = f2bf(d4[e] * sc * g);
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        *reinterpret_cast<uint16_t *>(osm + (16 * r + 4 * lg + e) * AB_OPITCH + c * 2) = f2bf(d4[r][e] * sc * g);
   }
   __syncthreads();
-  {
-    const int m = tid >> 4, c8 = tid & 15;
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    const int m = 16 * r + (tid >> 4), c8 = tid & 15;
     if (m < nb)
       *reinterpret_cast<u32x4 *>(qbuf + qfrag_index(b0 + m, h, quarter * 128 + c8 * 8)) =
           *reinterpret_cast<const u32x4 *>(osm + m * AB_OPITCH + c8 * 16);
@@ -1418,9 +1467,14 @@ static int decode_chunk(const amla_mla_args *a, hipStream_t st, hipEvent_t const
   mark(ev, 3, st);
   int32_t *plan = reinterpret_cast<int32_t *>(ws + L.plan);
   const int tmax = mla_context_bound(*a);
-  absorb_kernel<<<dim3(HEADS, LORA / 128, (B + AB_SEQ - 1) / AB_SEQ), 256, 0, st>>>(
-      q, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv), B,
-      qbuf, a->positions, tmax, L.units, L.slots, plan);
+  if (B <= AB_SEQ)
+    absorb_kernel<1><<<dim3(HEADS + 1, LORA / 128, 1), 256, 0, st>>>(
+        q, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv), B,
+        qbuf, a->positions, tmax, L.units, L.slots, plan);
+  else
+    absorb_kernel<2><<<dim3(HEADS + 1, LORA / 128, (B + 2 * AB_SEQ - 1) / (2 * AB_SEQ)), 256, 0, st>>>(
+        q, reinterpret_cast<const uint8_t *>(a->w_kv_b), a->s_kv_b, reinterpret_cast<const uint16_t *>(a->gamma_kv), B,
+        qbuf, a->positions, tmax, L.units, L.slots, plan);
   if ((rc = check_launch("mla absorb"))) return rc;
 
   // 5. attention over the latent cache, split over context
