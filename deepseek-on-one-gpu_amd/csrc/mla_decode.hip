@@ -330,6 +330,11 @@ __global__ __launch_bounds__(256) void absorb_kernel(const uint16_t *__restrict_
 
 // ---------------------------------------------------------------- attention
 
+template <bool V>
+struct BoolC {
+  static constexpr bool value = V;
+};
+
 struct AttnParams {
   const uint16_t *qbuf;  // B x (H, 576) bf16 in fragment order (qfrag_index): absorbed latent query | rotated rope query
   const uint16_t *ckv;   // cache (B_alloc, max_seq, 512)
@@ -593,7 +598,15 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   const int head0 = blockIdx.y * HG + hl0;
   const uint32_t lane16 = static_cast<uint32_t>(lane) * 16u;  // the copies' lane offset inside the context
 
-  // query fragments (B operand: head = column l%16, K = 8*lg .. of each 32-wide step)
+  // the first tile's copies, then the query fragments (B operand: head =
+  // column l%16, K = 8*lg .. of each 32-wide step); the first tile starts
+  // once both have landed (the compiler's wait before the first fragment use
+  // is for every load issued so far), the second tile's copies go out during
+  // its score steps
+  if (tb < te) dma_tile(p, b, tb, T, smem, smem, wave, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  constexpr int QLOADS = NTW * (QKD / 32);  // per wave, after the copies
+  static_assert(TILE_DMA + QLOADS <= 63, "vmcnt range");
   bf16x8 qf[NTW][QKD / 32];
 #pragma unroll
   for (int nt = 0; nt < NTW; ++nt) {
@@ -601,6 +614,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
 #pragma unroll
     for (int ks = 0; ks < QKD / 32; ++ks) qf[nt][ks] = as_bf16x8(ldg16(qr + ks * 512));
   }
+  __builtin_amdgcn_sched_barrier(0);
 
   f32x4 o[8][NH];  // O^T: latent 128*wave + 16*mt + .., head block (NTW*wave + j) % NH of the group
 #pragma unroll
@@ -615,22 +629,22 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
   }
 
   if (tb < te) {
-    dma_tile(p, b, tb, T, smem, smem, wave, lane);
-    if (tb + 1 < te) {
-      dma_tile(p, b, tb + 1, T, smem, smem + STAGE_BYTES, wave, lane);
-      wait_vmcnt<TILE_DMA>();
-    } else {
-      wait_vmcnt<0>();
-    }
+    // the first tile's copies landed (the query loads, issued after them, may
+    // still be in flight: loads complete in order)
+    wait_vmcnt<QLOADS>();
     prepare_own_rows(smem, smem + TAB_OFF + (tb & 1) * TAB_BYTES, wave, lane, p.eps);
     // LDS-only barrier: __syncthreads would also wait for the second tile's
     // copies (each wave waited for its own first-tile copies above; the second
-    // tile is waited for at the first score step)
+    // tile is waited for after the first one)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     bool have_ref = false;
-    for (int tile = tb; tile < te; ++tile) {
+    // One tile.  FIRST (the split's first tile) prepares no next tile inside
+    // its score steps: it starts once its own copies have landed, and the
+    // second tile, whose copies were issued with them, is prepared after it.
+    auto tile_body = [&](const int tile, auto first_c) __attribute__((always_inline)) {
+      constexpr bool FIRST = decltype(first_c)::value;
       const int it = tile - tb;
       uint8_t *const cur = smem + (it % NST) * STAGE_BYTES;
       // copies of the tile after next, one per score step below (its stage was
@@ -655,7 +669,11 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       // nothing reads any more) so that the counts hold.
       constexpr int NSTEP = QKD / 32;
       constexpr int SD = 3;
-      constexpr int kLgkm[NSTEP] = {4, 8, 8, 8, 4, 4, 8, 8, 8, 4, 4, 7, 7, 9, 6, 6, 4, 2};
+      constexpr int F3 = NSTEP - TILE_DMA;  // the first tile's first step copying the third tile
+      static_assert(F3 > 0 && F3 < TILE_DMA, "first-tile copy schedule");
+      constexpr int kLgkmN[NSTEP] = {4, 8, 8, 8, 4, 4, 8, 8, 8, 4, 4, 7, 7, 9, 6, 6, 4, 2};
+      // the first tile: only the fragment reads and the r_t reads of step 12
+      constexpr int kLgkmF[NSTEP] = {4, 4, 4, 4, 4, 4, 4, 4, 4, 4, 4, 4, 4, 6, 6, 6, 2, 0};
       const uint32_t kaddr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
           (__attribute__((address_space(3))) const uint16_t *)(K + li * KROW + 8 * lg)));
 #define AMLA_RDA(dst, S, MT) \
@@ -685,13 +703,14 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
 #pragma unroll
       for (int ks = 0; ks < NSTEP; ++ks) {
         const int c = ks % SD;
-        switch (kLgkm[ks]) {
+        switch (FIRST ? kLgkmF[ks] : kLgkmN[ks]) {
           case 9: asm volatile("s_waitcnt lgkmcnt(9)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
           case 8: asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
           case 7: asm volatile("s_waitcnt lgkmcnt(7)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
           case 6: asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
           case 4: asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
-          default: asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
+          case 2: asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
+          default: asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ab[c][0]), "+v"(ab[c][1])::"memory"); break;
         }
         if (ks == LORA / 32) {
           // latent part complete: apply r_t before the rope K steps (MFMA
@@ -719,7 +738,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
         // covers every operation issued before step ks's reads).  The empty
         // asm names the registers, so the compiler cannot hoist their use
         // above the wait: a wait orders memory operations, not register uses.
-        if (ks == 5 || ks == 10) {
+        if (!FIRST && (ks == 5 || ks == 10)) {
           asm volatile("" : "+v"(pv4[0]), "+v"(pv4[1]), "+v"(pv4[2]), "+v"(pv4[3]));
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -729,7 +748,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
             pss = dot2_bf16(pv4[i].w, pss);
           }
         }
-        if (ks == 15) {
+        if (!FIRST && ks == 15) {
           // r_t = rsqrt(mean(c_t^2) + eps): sum over the row's 8 lanes (every
           // lane of the row ends with the total); rope key rotated in fp32,
           // rounded to bf16 (inference/ops.py:10-12, :93-97); the reads of
@@ -756,7 +775,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
           AMLA_RDA(ab[c][0], ks + SD, 0);
           AMLA_RDA(ab[c][1], ks + SD, 1);
         }
-        if (ks == 0) {
+        if (!FIRST && ks == 0) {
           // the next tile's copies landed (issued during the previous tile;
           // this tile's own copies start below)
           wait_vmcnt<0>();
@@ -764,12 +783,12 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
           AMLA_RD(pv4[1], rpa, 128);
           AMLA_RD(pv4[2], rpa, 256);
           AMLA_RD(pv4[3], rpa, 384);
-        } else if (ks == 5) {
+        } else if (!FIRST && ks == 5) {
           AMLA_RD(pv4[0], rpa, 512);
           AMLA_RD(pv4[1], rpa, 640);
           AMLA_RD(pv4[2], rpa, 768);
           AMLA_RD(pv4[3], rpa, 896);
-        } else if (ks == 10) {
+        } else if (!FIRST && ks == 10) {
           const uint32_t rawa = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
               (__attribute__((address_space(3))) const uint8_t *)(nxt + K_BYTES + prow * (ROPE * 2) + pq * 16)));
           const uint32_t taba = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
@@ -787,7 +806,16 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
         // tile is copied again (an L2 hit) into a stage nothing reads any more;
         // the table block is the parity of tile + 2, never the one the
         // preparation of tile + 1 reads
-        if (ks < TILE_DMA) dma_piece(p, b, min(tile + 2, te - 1), tile + 2, T, smem, nst, wave, lane, lane16, ks);
+        if constexpr (FIRST) {
+          // the second tile's copies (steps 0 .. 10), then the third tile's
+          // (steps 7 .. 17, after the second tile's piece of the same step)
+          if (ks < TILE_DMA)
+            dma_piece(p, b, min(tile + 1, te - 1), tile + 1, T, smem, smem + STAGE_BYTES, wave, lane, lane16, ks);
+          if (ks >= F3)
+            dma_piece(p, b, min(tile + 2, te - 1), tile + 2, T, smem, nst, wave, lane, lane16, ks - F3);
+        } else {
+          if (ks < TILE_DMA) dma_piece(p, b, min(tile + 2, te - 1), tile + 2, T, smem, nst, wave, lane, lane16, ks);
+        }
       }
       // the softmax reads sc: MFMA write -> VALU read wait states
       if constexpr (NTW == 2)
@@ -939,7 +967,18 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnParams p) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
+    };
+    tile_body(tb, BoolC<true>{});
+    if (tb + 1 < te) {
+      // the second tile's copies landed (the third tile's pieces issued after
+      // its last one may still be in flight); prepared here, then the steady loop
+      wait_vmcnt<QKD / 32 - TILE_DMA + 1>();
+      prepare_own_rows(smem + STAGE_BYTES, smem + TAB_OFF + ((tb + 1) & 1) * TAB_BYTES, wave, lane, p.eps);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
     }
+    for (int tile = tb + 1; tile < te; ++tile) tile_body(tile, BoolC<false>{});
   }
 
   // the accumulators' last MFMA writes are read by VALU code below: cover the
