@@ -1129,8 +1129,9 @@ __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const ui
                                                          const uint16_t *__restrict__ gamma, int B,
                                                          uint16_t *__restrict__ attn) {
   constexpr int NU = SQ * WPS;    // merge units
-  constexpr int XB = SQ > 4 ? 8 : 16;  // splits in flight per wave (a batch)
-  constexpr int WMAX = 256;       // weights per unit: at most 256 splits, a whole number of batches
+  constexpr int XB = SQ > 4 ? 8 : 20;  // splits in flight per wave (a batch)
+  constexpr int WMAX = 256;       // splits per sequence
+  constexpr int MLR = WMAX / 64;  // (m, l) loads per lane
   constexpr int LROW = LORA + 8;  // bf16 per lat row in LDS (16 B pad)
   static_assert(SQ <= 16 && NU <= 16, "one MFMA column per sequence; at most two units per wave");
   static_assert(VH == 1 || VH == 2, "whole or half W_UV[h] per workgroup");
@@ -1141,7 +1142,7 @@ __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const ui
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   __shared__ __align__(16) uint16_t latb[SQ][LROW];
-  __shared__ float wsp[8][WMAX];
+  __shared__ float wsp[8][WMAX + XB];  // weight of split s, zero past the last split
   __shared__ float xacc[NU][8][64];  // each unit's sums, [column e][lane]
   __shared__ float xl[NU];
   __shared__ float qs[QKD];
@@ -1171,8 +1172,9 @@ __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const ui
   }
 
   // ---- fast merge: unit u = (sequence b0 + u / WPS, part u % WPS).  A
-  // unit's first batch of partial rows is in flight while the max and the
-  // weights are formed.
+  // unit's first batch of partial rows and every split's (m, l) are loaded
+  // together (lane l: splits l, l + 64, ..); the max and the weights are
+  // formed from those registers while the rows are in flight.
   for (int u = wave; u < NU; u += 8) {
     const int su = u / WPS, pu = u % WPS;
     if (su >= nb) {
@@ -1189,35 +1191,49 @@ __global__ __launch_bounds__(512) void combine_uv_kernel(AttnParams ap, const ui
     u32x4 v[XB];
 #pragma unroll
     for (int j = 0; j < XB; ++j) v[j] = po[(size_t)min(s0 + j, nsp - 1) * stride];
+    float2 ml[MLR];
+#pragma unroll
+    for (int r = 0; r < MLR; ++r) {
+      ml[r] = float2{-INFINITY, 0.f};
+      if (64 * r < nsp) {
+        const int s = min(lane + 64 * r, nsp - 1);
+        const float2 e = *reinterpret_cast<const float2 *>(ap.part_ml + (base + (size_t)s * HEADS) * 2);
+        if (lane + 64 * r < nsp) ml[r] = e;
+      }
+    }
     float mloc = -INFINITY;
     bool badl = false;
-    for (int s = lane; s < nsp; s += 64) {
-      mloc = fmaxf(mloc, ap.part_ml[(base + (size_t)s * HEADS) * 2]);
-      badl = badl || ap.part_ml[(base + (size_t)s * HEADS) * 2 + 1] < 0.f;
+#pragma unroll
+    for (int r = 0; r < MLR; ++r) {
+      mloc = fmaxf(mloc, ml[r].x);
+      badl = badl || ml[r].y < 0.f;
     }
     const float M = wave_max(mloc);
     const bool flagged = __builtin_amdgcn_ballot_w64(badl) != 0;
     if (pu == 0 && lane == 0) s_flag[su] = flagged;
     if (flagged) continue;
-    // weights of this unit, zero past its last split up to a whole batch
+    // weights of this unit's splits (by split index), zero past its last
+    // split up to a whole batch
     float lloc = 0.f;
-    const int nw = ((s1 - s0 + XB - 1) / XB) * XB;
-    for (int k = lane; k < nw; k += 64) {
-      float w = 0.f;
-      if (s0 + k < s1) {
-        const size_t row = base + (size_t)(s0 + k) * HEADS;
-        const float ms = ap.part_ml[row * 2];
-        w = ms == -INFINITY ? 0.f : exp2f(ms - M);
-        lloc += w * ap.part_ml[row * 2 + 1];
+#pragma unroll
+    for (int r = 0; r < MLR; ++r) {
+      const int s = lane + 64 * r;
+      if (64 * r < s0 + ((s1 - s0 + XB - 1) / XB) * XB) {
+        float w = 0.f;
+        if (s >= s0 && s < s1 && ml[r].x != -INFINITY) {
+          w = exp2f(ml[r].x - M);
+          lloc += w * ml[r].y;
+        }
+        wsp[wave][s] = w;
       }
-      wsp[wave][k] = w;
     }
+    if (lane < XB) wsp[wave][WMAX + lane] = 0.f;
     const float L = wave_sum(lloc);
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int k = 0; k < s1 - s0; k += XB) {
 #pragma unroll
       for (int j = 0; j < XB; ++j) {
-        const float w = wsp[wave][k + j];
+        const float w = wsp[wave][s0 + k + j];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           acc[2 * e] += w * lo_bf(v[j][e]);
