@@ -196,6 +196,14 @@ def test_decode_t4096():
     _check_cache(gc, rc, [(4095, 4096)])
 
 
+def test_decode_batch1_context32768_256_splits():
+    """One sequence at context 32768: 256 splits of 128 rows, so the combine's merge reads
+    (m, l) over four rounds of 64 lanes and each of its two parts runs seven batches of rows."""
+    got, want, gc, rc = _run_case("decode32k", 1, 1, 32767, 32768)
+    assert_parity(got, want, "decode B=1 T=32768")
+    _check_cache(gc, rc, [(32767, 32768)])
+
+
 def test_decode_batch8_shared_position():
     got, want, gc, rc = _run_case("decodeb8", 8, 1, 1023, 1030)
     assert_parity(got, want, "decode B=8 T=1024")
